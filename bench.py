@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Benchmark of the cooperative-matrix path on one MI355X.
+
+Headline (BASELINE.json metric): the bf16 GEMM at M=N=K=8192 (A row-major,
+B column-major, fp32 C) -- `value` is its TFLOP/s -- and the causal
+flash-attention forward at B=4, H=32, S=4096, D=128 (fp16), reported beside it
+in the same JSON line with its own roofline.  Inputs are the seeded synthetic
+tensors of the parity tests, generated on the device and resident in HBM
+before timing starts.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256]
+
+A step is one kernel launch over the whole problem.  Kernel time comes from HIP
+events recorded on the launch stream around the K timed launches; wall time
+from a synchronised host clock around the same region.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "lava.jl_amd"))
+
+METRIC = "GEMM TFLOP/s at 8192³ bf16 + causal attn fwd TFLOP/s; % of MFMA peak"
+
+# MI355X published dense peaks
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_FP16_TFLOPS = 2516.6
+PEAK_INT8_TOPS = 5033.2
+PEAK_HBM_GBS = 8000.0
+
+
+def timed(lh, launch, steps: int, warmup: int, stream):
+    """Warm up, then time exactly `steps` launches: HIP events on `stream` give the
+    kernel time; a synchronised host clock gives the wall time."""
+    for _ in range(warmup):
+        launch()
+    lh.synchronize()
+    e0, e1 = lh.Event(), lh.Event()
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        launch()
+    e1.record(stream)
+    lh.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_ms(e1) / steps, wall * 1e3 / steps
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by the copy-kernel calibration), committed under profiles/."""
+    p = REPO / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(name, {}).get("bytes_per_launch")
+    except Exception:
+        return None
+
+
+def roofline(bound, achieved, peak, unit, traffic):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ---------------------------------------------------------------- workloads
+def bench_gemm(lh, dt, n, steps, warmup, stream, cfg):
+    A = lh.HIPDeviceArray(dt, (n, n), order="C")
+    B = lh.HIPDeviceArray(dt, (n, n), order="F")
+    acc = "i32" if dt == "i8" else "f32"
+    C = lh.HIPDeviceArray(acc, (n, n), order="C")
+    if dt == "i8":
+        lh.fill_i8(A, lh.seed(cfg, 0))
+        lh.fill_i8(B, lh.seed(cfg, 1))
+    else:
+        lh.fill_uniform(A, lh.seed(cfg, 0), -1.0, 1.0)
+        lh.fill_uniform(B, lh.seed(cfg, 1), -1.0, 1.0)
+    lh.synchronize()
+    kern_ms, wall_ms = timed(lh, lambda: lh.gemm(C, A, B, stream=stream), steps, warmup, stream)
+    flop = 2.0 * n ** 3
+    return flop, kern_ms, wall_ms
+
+
+def bench_gemm_layout(lh, dt, n, layout, steps, warmup, stream, cfg):
+    A = lh.HIPDeviceArray(dt, (n, n), order="C" if layout & 1 else "F")
+    B = lh.HIPDeviceArray(dt, (n, n), order="C" if layout & 2 else "F")
+    C = lh.HIPDeviceArray("f32", (n, n), order="C" if layout & 4 else "F")
+    lh.fill_uniform(A, lh.seed(cfg, 0), -1.0, 1.0)
+    lh.fill_uniform(B, lh.seed(cfg, 1), -1.0, 1.0)
+    lh.synchronize()
+    kern_ms, wall_ms = timed(lh, lambda: lh.gemm(C, A, B, stream=stream), steps, warmup, stream)
+    return 2.0 * n ** 3, kern_ms, wall_ms
+
+
+def bench_attn(lh, steps, warmup, stream, B=4, H=32, S=4096, D=128):
+    Q, K, V = (lh.HIPDeviceArray("f16", (D, S, H, B)) for _ in range(3))
+    O = lh.HIPDeviceArray("f16", (D, S, H, B))
+    for t, a in enumerate((Q, K, V)):
+        lh.fill_normal(a, lh.seed(4, t))
+    lh.synchronize()
+    sc = 1.0 / math.sqrt(D)
+    kern_ms, wall_ms = timed(lh, lambda: lh.flash_attn_fwd(O, Q, K, V, scale=sc, causal=True, stream=stream),
+                             steps, warmup, stream)
+    flop = 0.5 * 4.0 * B * H * S * S * D   # causal: half of 4*B*H*S^2*D
+    return flop, kern_ms, wall_ms
+
+
+def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6):
+    """Rotates `copies` weight/scale sets (> the 256 MB Infinity Cache) so that
+    every launch streams its weights from HBM."""
+    X = lh.HIPDeviceArray("f16", (M, K), order="C")
+    lh.fill_normal(X, lh.seed(3, 0))
+    Ws, Ss = [], []
+    for c in range(copies):
+        W = lh.HIPDeviceArray("i8", (K, N), order="C")
+        s = lh.HIPDeviceArray("f16", (N,))
+        lh.fill_i8(W, lh.seed(3, 1) + 1000 * c, symmetric=True)
+        lh.fill_uniform(s, lh.seed(3, 2) + 1000 * c, 0.001, 0.02)
+        Ws.append(W)
+        Ss.append(s)
+    Y = lh.HIPDeviceArray("f32", (M, N), order="C")
+    lh.synchronize()
+    state = {"i": 0}
+
+    def launch():
+        i = state["i"] % copies
+        state["i"] += 1
+        lh.w8a16(Y, X, Ws[i], Ss[i], stream=stream)
+
+    kern_ms, wall_ms = timed(lh, launch, steps, warmup, stream)
+    nbytes = K * N + 2 * N + 2 * M * K + 4 * M * N
+    return nbytes, kern_ms, wall_ms
+
+
+# ---------------------------------------------------------------- CPU baseline
+def cpu_baseline_gemm(n=8192, budget_s=12.0):
+    """The oracle's fp32-accumulate GEMM (a port of the tile loop, not the Lava
+    path: Julia/Mantle/lavapipe are not on the GPU box) on all host threads, over
+    a bounded number of rows of the same 8192^3 bf16 problem."""
+    sys.path.insert(0, str(REPO))
+    from oracle import oracle as o
+    max_rows = 2048
+    A = o.fill_uniform(max_rows * n, "bf16", 0x4C415641 + 256, -1.0, 1.0)   # the first rows of A
+    B = o.fill_uniform(n * n, "bf16", 0x4C415641 + 257, -1.0, 1.0)    # B column-major, n x n
+    t0 = time.perf_counter()
+    o.gemm_f32acc(A, "bf16", B, "bf16", n, n, n, n, 1, 4)
+    probe = time.perf_counter() - t0
+    rows = int(max(4, min(max_rows, 4 * budget_s / max(probe, 1e-3))))
+    t0 = time.perf_counter()
+    o.gemm_f32acc(A, "bf16", B, "bf16", n, n, n, n, 1, rows)
+    dt = time.perf_counter() - t0
+    tflops = 2.0 * rows * n * n / dt / 1e12
+    return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": o.num_threads(), "kind": "port",
+            "sample": f"{rows} rows of C of the bf16 8192^3 GEMM (2*{rows}*8192*8192 FLOP, fp32 accumulate, "
+                      f"includes decoding B), oracle/lava_oracle.c oracle_gemm_f32acc, {dt:.1f} s"}
+
+
+# ---------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="headline",
+                    choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the cooperative-matrix path has no multi-GPU form in this build "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE={world}). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import lava_hip as lh
+    lh.init()
+    s = lh.Stream()
+    stream = s.handle
+    K, W = args.steps, args.warmup
+    out = {"metric": METRIC, "n_gpus": 1, "steps": K, "warmup": W, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "data": "synthetic (seeded: uniform[-1,1] GEMM inputs, normal(0,1) Q/K/V), "
+                                         "generated on the device before timing"}
+
+    if args.workload in ("headline", "gemm_bf16"):
+        flop, kms, wms = bench_gemm(lh, "bf16", 8192, K, W, stream, 1)
+        achieved = flop / (kms * 1e-3) / 1e12
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "bf16",
+                    "config": {"workload": "bf16 GEMM M=N=K=8192, A row-major, B column-major, fp32 accumulate "
+                                           "and output (BASELINE configs[1])", "M": 8192, "N": 8192, "K": 8192},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("mfma", achieved, PEAK_BF16_TFLOPS, "TFLOP/s", load_traffic("gemm_bf16_8192"))})
+        if args.workload == "headline":
+            aflop, akms, awms = bench_attn(lh, K, W, stream)
+            a_ach = aflop / (akms * 1e-3) / 1e12
+            out["attn_fwd"] = {"value": round(aflop / (awms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
+                               "ms_per_step": round(awms, 4), "kernel_ms": round(akms, 4), "dtype": "f16",
+                               "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=128 fp16, "
+                                                      "fp32 softmax state (BASELINE configs[4]); FLOP = "
+                                                      "0.5*4*B*H*S^2*D"},
+                               "roofline": roofline("mfma", a_ach, PEAK_FP16_TFLOPS, "TFLOP/s",
+                                                    load_traffic("flash_fwd_causal"))}
+    elif args.workload == "gemm_bf16_4096":
+        flop, kms, wms = bench_gemm(lh, "bf16", 4096, K, W, stream, 1)
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "bf16", "config": {"workload": "bf16 GEMM 4096^3 A row-major B column-major"},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "attn":
+        flop, kms, wms = bench_attn(lh, K, W, stream)
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "f16", "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=128"},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s",
+                                         load_traffic("flash_fwd_causal"))})
+    elif args.workload == "gemm_i8":
+        flop, kms, wms = bench_gemm(lh, "i8", 4096, K, W, stream, 2)
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "int8", "config": {"workload": "int8 GEMM 4096^3 -> int32 (BASELINE configs[2])"},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_INT8_TOPS, "TOP/s",
+                                         load_traffic("gemm_i8_4096"))})
+    elif args.workload == "w8a16":
+        nbytes, kms, wms = bench_w8a16(lh, K, W, stream)
+        out.update({"value": round(nbytes / (wms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 5),
+                    "dtype": "f16", "config": {"workload": "W8A16 16x4096 . 4096x14336, per-column fp16 scale, "
+                                                           "6 rotating weight copies (BASELINE configs[3])"},
+                    "kernel_ms": round(kms, 5),
+                    "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s",
+                                         load_traffic("w8a16"))})
+    elif args.workload == "gemm_f16_256":
+        flop, kms, wms = bench_gemm_layout(lh, "f16", 256, 3 | 4, K, W, stream, 0)
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "f16", "config": {"workload": "fp16 GEMM 256^3, A and B row-major (BASELINE configs[0])"},
+                    "kernel_ms": round(kms, 5),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
+
+    if args.workload in ("headline", "gemm_bf16") and not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_gemm()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

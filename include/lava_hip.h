@@ -1,0 +1,226 @@
+/*
+ * lava_hip.h -- C ABI of liblava_hip.so, the MI355X (gfx950) implementation of
+ * Lava.jl's cooperative-matrix compute path.
+ *
+ * Conventions for every entry point:
+ *   - returns LAVA_HIP_OK (0) on success, a negative status otherwise; the
+ *     thread-local message is read with lava_hip_last_error().  No exception
+ *     crosses the ABI.
+ *   - pointers to device memory are plain addresses (hipMalloc'd or any other
+ *     device allocation); the caller owns every buffer.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the default stream.
+ *     Launches are asynchronous on that stream.
+ *   - element strides (lda, ldb, ...) are in elements, not bytes.
+ *   - argument checks happen on the host before any GPU call, so a bad call
+ *     fails with LAVA_HIP_ERR_INVALID_ARG / _UNSUPPORTED and touches no device.
+ *
+ * Reference boundary being replaced (Lava.jl, paths relative to its tree):
+ * Lava compiles a kernel written against the vocabulary of
+ * src/vocabulary/coopmat.jl into a `LavaGPUKernel` (src/compiler/compilation.jl:409-426,
+ * src/compiler/cache.jl:109-138) whose arguments travel in one buffer addressed by
+ * an 8-byte push constant (src/compiler/entry_wrapper.jl:26-178); the launcher
+ * (Mantle.jl) dispatches it.  Here each kernel is compiled ahead of time and each
+ * entry point takes its arguments directly.
+ */
+#ifndef LAVA_HIP_H
+#define LAVA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+#define LAVA_HIP_OK 0
+#define LAVA_HIP_ERR_INVALID_ARG (-1) /* shape, stride, pointer or alignment error */
+#define LAVA_HIP_ERR_UNSUPPORTED (-2) /* valid request this build does not implement */
+#define LAVA_HIP_ERR_HIP (-3)         /* the HIP runtime reported an error */
+#define LAVA_HIP_ERR_NO_DEVICE (-4)   /* no usable gfx950 device */
+
+/* ---- element type codes (dtype arguments) ------------------------------- */
+#define LAVA_HIP_F16 0
+#define LAVA_HIP_BF16 1
+#define LAVA_HIP_F32 2
+#define LAVA_HIP_I8 3
+#define LAVA_HIP_U8 4
+#define LAVA_HIP_I32 5
+#define LAVA_HIP_U32 6
+
+/* ---- GEMM layout flags ---------------------------------------------------
+ * bit0: A row-major, bit1: B row-major, bit2: C row-major; a clear bit means
+ * column-major, Julia's default (src/device/devicearray.jl:138-174).  Row- vs
+ * column-major is the MemoryLayout operand of the load/store
+ * (src/vocabulary/coopmat.jl:124-161; src/compiler/spirv/coopmat.jl:664-744). */
+#define LAVA_HIP_A_ROWMAJOR 1u
+#define LAVA_HIP_B_ROWMAJOR 2u
+#define LAVA_HIP_C_ROWMAJOR 4u
+
+/* ---- CoopMatReduce masks (src/vocabulary/coopmat.jl:292-297) ------------- */
+#define LAVA_HIP_REDUCE_ROW 1u
+#define LAVA_HIP_REDUCE_COLUMN 2u
+#define LAVA_HIP_REDUCE_ROW_AND_COLUMN 3u
+#define LAVA_HIP_REDUCE_TWO_BY_TWO 4u /* declared by the reference, unverified there: unsupported */
+
+/* reduce combiners */
+#define LAVA_HIP_COMBINE_ADD 0
+#define LAVA_HIP_COMBINE_MAX 1
+#define LAVA_HIP_COMBINE_MIN 2
+
+/* ========================================================================= */
+/* Runtime plumbing: what Mantle's LavaArray / buffer layer provides to a     */
+/* Lava kernel (README.md:11-13), reduced to hipMalloc/hipMemcpy wrappers.    */
+/* ========================================================================= */
+
+/* Idempotent and thread-safe.  Selects nothing; checks that device 0 is gfx950.
+ * Replaces the device/context set-up Lava leaves to Mantle (src/Lava.jl:128-142). */
+int lava_hip_init(void);
+int lava_hip_device_count(int* count);
+int lava_hip_malloc(void** ptr, size_t bytes);
+int lava_hip_free(void* ptr);
+int lava_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int lava_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int lava_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
+/* Byte fill by a kernel (not hipMemsetAsync), so it is safe under graph capture. */
+int lava_hip_fill_bytes(void* dst, uint8_t value, size_t bytes, void* stream);
+int lava_hip_synchronize(void);
+int lava_hip_stream_synchronize(void* stream);
+int lava_hip_stream_create(void** stream);
+int lava_hip_stream_destroy(void* stream);
+int lava_hip_event_create(void** event);
+int lava_hip_event_destroy(void* event);
+int lava_hip_event_record(void* event, void* stream);
+int lava_hip_event_elapsed_ms(float* ms, void* start, void* stop);
+/* Thread-local message of the last failure on this thread ("" if none).
+ * Replaces LavaError/LavaCompilationError reporting (src/runtime/errors.jl:12-51). */
+const char* lava_hip_last_error(void);
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int lava_hip_version(void);
+
+/* ========================================================================= */
+/* Device capabilities: the MI355X answer to `caps(backend)::DeviceCaps`       */
+/* (src/vocabulary/caps.jl:54-170) and `matrix_shapes` (caps.jl:158-159).     */
+/* ========================================================================= */
+
+/* out[0..n) receives, in order: coopmat (1), tile (16), subgroup (64),
+ * coopmatsubgroup (64), sharedbudget (LDS bytes per workgroup), workgrouplimit,
+ * cores (compute units), warps (SIMDs per CU x max waves per SIMD), clock_khz,
+ * hbm_bytes, l2_bytes, gfx_arch_number (950).  Fields past n are not written. */
+int lava_hip_device_caps(int64_t* out, int n);
+
+/* The subgroup-scope MatrixShape table (src/vocabulary/matrix.jl:88-95): row i is
+ * out[6*i .. 6*i+6) = {ab_dtype, acc_dtype, M, N, K, scope(0 = subgroup)}.
+ * *count receives the number of rows; at most max_rows are written. */
+int lava_hip_matrix_shapes(int32_t* out, int max_rows, int* count);
+
+/* ========================================================================= */
+/* Seeded input generator (device side of the oracle's definition)           */
+/* ========================================================================= */
+
+/* splitmix64 of (seed, index): uniform[a,b] rounded once to fp32 then RNE to
+ * dtype (F16, BF16 or F32). */
+int lava_hip_fill_uniform(void* dst, int dtype, int64_t n, uint64_t seed, double a, double b, void* stream);
+/* Box-Muller normal(0,1) from one draw per element, fp32 then RNE to dtype. */
+int lava_hip_fill_normal(void* dst, int dtype, int64_t n, uint64_t seed, void* stream);
+/* int8 over [-128,127] (symmetric=0) or [-127,127] (symmetric=1). */
+int lava_hip_fill_i8(void* dst, int64_t n, uint64_t seed, int symmetric, void* stream);
+
+/* ========================================================================= */
+/* Tile-level vocabulary: one subgroup (wavefront) per tile                   */
+/* ========================================================================= */
+
+/* D = muladd(A, B, C) on 16x16x16 tiles, exactly the sequence
+ *   a = AcceleratedMatrix{Ta,16,16,MatrixA}(pA, offA, strideA[, Val(true)])
+ *   b = AcceleratedMatrix{Tb,16,16,MatrixB}(pB, offB, strideB[, Val(true)])
+ *   c = AcceleratedMatrix{Tc,16,16,Accumulator}(pC, offC, strideC[, Val(true)])
+ *   copyto!(pD, offD, strideD, muladd(a, b, c)[, Val(true)])
+ * (docs/src/device.md:81-88; src/vocabulary/coopmat.jl:124-161,196-199).
+ * Offsets are Lava's 1-based element offsets; strides are element strides
+ * between columns (column-major) or rows (row-major).  `layout` bits 0..3 mark
+ * A, B, C, D row-major.  `ntiles` independent tiles are processed, tile t
+ * reading at offsets + t * tile_step (elements).
+ * Type pairs (ab_dtype, acc_dtype): (F16, F32), (I8, I32) signed, (U8, U32)
+ * unsigned (test/spirv/test_coopmat_int8.jl:25-98). */
+int lava_hip_coopmat_muladd_16x16x16(int ab_dtype, int acc_dtype, const void* A, int64_t offA, int64_t strideA,
+                                     const void* B, int64_t offB, int64_t strideB, const void* C, int64_t offC,
+                                     int64_t strideC, void* D, int64_t offD, int64_t strideD, uint32_t layout,
+                                     int64_t ntiles, int64_t tile_step, void* stream);
+
+/* coopmat_perelement(f, m) with f(row, col, e) = e * (row + 1) + col on fp32
+ * 16x16 (and 32x32 when tile == 32) Accumulator tiles loaded column-major with
+ * stride `tile` from `in` and stored the same way to `out`
+ * (test/spirv/test_coopmat_perelement_inline.jl:19-37;
+ * src/device/coopmat_intrinsics.jl:535-628). */
+int lava_hip_coopmat_perelement_rowcol(const float* in, float* out, int tile, int64_t ntiles, void* stream);
+
+/* coopmat_perelement(f, m, o) with f(row, col, x, y) = max(x, y) + row - col: the
+ * matrix-operand form (src/device/coopmat_intrinsics.jl:630-678). */
+int lava_hip_coopmat_perelement_pair(const float* m, const float* o, float* out, int tile, int64_t ntiles,
+                                     void* stream);
+
+/* coopmat_reduce(f, Dst, m, Val(mask)) on fp32 tile x tile Accumulators (tile 16
+ * or 32), same-shape destination, result smeared along the reduced axis
+ * (src/device/coopmat_intrinsics.jl:685-755).  combine: LAVA_HIP_COMBINE_*. */
+int lava_hip_coopmat_reduce(const float* in, float* out, int tile, uint32_t mask, int combine, int64_t ntiles,
+                            void* stream);
+
+/* convert(AcceleratedMatrix{T,...}, m) of fp32 tiles to F16 or BF16, RNE
+ * (src/vocabulary/coopmat.jl:178-182; src/compiler/passes/exact_narrowing.jl:31-36).
+ * n must be a multiple of 256 (whole 16x16 tiles). */
+int lava_hip_coopmat_convert(const float* in, void* out, int out_dtype, int64_t n, void* stream);
+
+/* y[i] = dot4x8(a[i], b[i]) (src/vocabulary/vocabulary.jl:31-35). */
+int lava_hip_dot4x8(const uint32_t* a, const uint32_t* b, int32_t* y, int64_t n, void* stream);
+
+/* ========================================================================= */
+/* Kernels                                                                    */
+/* ========================================================================= */
+
+/* C (M x N) = A (M x K) * B (K x N), fp32 accumulate, C overwritten.
+ * Replaces the coopmat GEMM kernels Lava compiles for Mantle (`coopmat_gemm_kernel!`,
+ * named at src/device/coopmat_intrinsics.jl:90; the staged form
+ * src/device/coopmat_intrinsics.jl:104-148; the coopmat2 form
+ * test/glsl/coopmat2_gemm_regs.comp:37-84 with push block {pa, pb, pc, M, N, K}).
+ * Any M, N, K >= 0; layout flags as above; lda/ldb/ldc >= the extent they stride. */
+int lava_hip_gemm_f16_f32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
+/* The bf16 form (no Lava counterpart: the coopmat component table has no bf16,
+ * src/device/coopmat_intrinsics.jl:16-19; same contract as the f16 form). */
+int lava_hip_gemm_bf16_f32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                           int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
+/* int8 x int8 -> int32, all operands signed (src/compiler/spirv/coopmat.jl:115-151),
+ * exact with two's-complement wrap of the 32-bit accumulator. */
+int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                         int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
+
+/* The 16x16x16 subgroup-tile GEMM written directly in the vocabulary, one
+ * wavefront per 16x16 tile of C, loading straight from global as
+ * docs/src/device.md:81-88 does (fp16 in, fp32 out).  M, N, K multiples of 16. */
+int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                                    int64_t lda, int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
+
+/* W8A16 (coopmat2 per-element dequant callback, src/device/coopmat_intrinsics.jl:535-628
+ * with the scale pointer in `extras`, :569-572):
+ *   Y (M x N, fp32) = (X (M x K, fp16) * float(W (K x N, int8))) .* s[col] (fp16).
+ * layout: bit0 X row-major, bit1 W row-major, bit2 Y row-major; this build
+ * implements X row-major, W row-major, Y row-major (layout == 7). */
+int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N, int64_t K,
+                        int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream);
+
+/* Flash-attention forward, fp16 Q/K/V/O, fp32 running max and sum:
+ *   O = softmax(Q K^T * scale + mask) V  per (head, batch),
+ * the `attn_flash_rows!` / flash_attn_cm2 form (src/vocabulary/coopmat.jl:158;
+ * src/device/coopmat_intrinsics.jl:638-720).  Tensors are (E, L, H, B) = (D, S, H, B):
+ * element (e, l, h, b) at e*st[0] + l*st[1] + h*st[2] + b*st[3]
+ * (src/device/tensor_intrinsics.jl:279-281).  causal != 0 masks key > query.
+ * Q, K, V share `strides`; O uses `ostrides` (NULL = same as strides). */
+int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const void* V, void* O, int64_t B, int64_t H, int64_t S,
+                                int64_t D, const int64_t* strides, const int64_t* ostrides, float scale, int causal,
+                                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAVA_HIP_H */

@@ -1,0 +1,101 @@
+// gemm.hip -- GEMM entry points: argument checks and kernel choice.
+//
+// A column-major C is handled as its row-major transpose, C^T = B^T A^T, which
+// swaps the operands and flips their layouts; so every kernel writes row-major C.
+// The compute-bound shapes with K-contiguous operands (A row-major, B
+// column-major: the bf16 configuration) take the TN kernel; everything else the
+// staged kernel.
+#include <hip/hip_runtime.h>
+
+#include "gemm_kernels.hpp"
+#include "lava_hip_internal.hpp"
+
+using namespace lava;
+
+namespace {
+
+template <typename T>
+int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+               int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
+    using Acc = typename Mfma16<T>::acc_elem;
+    LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative extent (M=%lld N=%lld K=%lld)", name, (long long)M,
+             (long long)N, (long long)K);
+    LAVA_ARG(layout <= 7u, "%s: layout %u has bits beyond A/B/C row-major", name, layout);
+    if (M == 0 || N == 0) return LAVA_HIP_OK;
+    LAVA_ARG(C != nullptr, "%s: null C", name);
+    LAVA_ARG(K == 0 || (A != nullptr && B != nullptr), "%s: null A or B", name);
+    bool arow = layout & 1u, brow = layout & 2u;
+    const bool crow = layout & 4u;
+    const int64_t k1 = K > 0 ? K : 1;
+    LAVA_ARG(lda >= (arow ? k1 : M), "%s: lda = %lld is smaller than %s", name, (long long)lda, arow ? "K" : "M");
+    LAVA_ARG(ldb >= (brow ? N : k1), "%s: ldb = %lld is smaller than %s", name, (long long)ldb, brow ? "N" : "K");
+    LAVA_ARG(ldc >= (crow ? N : M), "%s: ldc = %lld is smaller than %s", name, (long long)ldc, crow ? "N" : "M");
+    LAVA_ARG(aligned(A, sizeof(T)) && aligned(B, sizeof(T)) && aligned(C, sizeof(Acc)),
+             "%s: operands not aligned to their element size", name);
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+
+    const T* a = static_cast<const T*>(A);
+    const T* b = static_cast<const T*>(B);
+    if (!crow) {   // C^T = B^T A^T, row-major
+        const T* t = a;
+        a = b;
+        b = t;
+        const int64_t tm = M;
+        M = N;
+        N = tm;
+        const int64_t tl = lda;
+        lda = ldb;
+        ldb = tl;
+        const bool ar = arow;
+        arow = !brow;
+        brow = !ar;
+    }
+    hipStream_t s = as_stream(stream);
+    Acc* c = static_cast<Acc*>(C);
+    if (arow && !brow && tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc))
+        return launch_gemm_tn<T>(a, b, c, M, N, K, lda, ldb, ldc, s);
+    return launch_gemm_staged<T>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int lava_hip_gemm_f16_f32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
+    return gemm_entry<f16>("gemm_f16_f32", A, B, C, M, N, K, lda, ldb, ldc, layout, stream);
+}
+
+int lava_hip_gemm_bf16_f32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                           int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
+    return gemm_entry<bf16>("gemm_bf16_f32", A, B, C, M, N, K, lda, ldb, ldc, layout, stream);
+}
+
+int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                         int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
+    return gemm_entry<int8_t>("gemm_i8_i32", A, B, C, M, N, K, lda, ldb, ldc, layout, stream);
+}
+
+int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                                    int64_t lda, int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
+    LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "coopmat_gemm_f16_tiles: negative extent");
+    LAVA_ARG(M % 16 == 0 && N % 16 == 0 && K % 16 == 0,
+             "coopmat_gemm_f16_tiles: M, N, K must be multiples of the 16x16x16 tile (M=%lld N=%lld K=%lld)",
+             (long long)M, (long long)N, (long long)K);
+    LAVA_ARG(layout <= 7u, "coopmat_gemm_f16_tiles: layout %u has bits beyond A/B/C row-major", layout);
+    if (M == 0 || N == 0) return LAVA_HIP_OK;
+    LAVA_ARG(C != nullptr && (K == 0 || (A != nullptr && B != nullptr)), "coopmat_gemm_f16_tiles: null pointer");
+    const bool arow = layout & 1u, brow = layout & 2u, crow = layout & 4u;
+    const int64_t k1 = K > 0 ? K : 1;
+    LAVA_ARG(lda >= (arow ? k1 : M) && ldb >= (brow ? N : k1) && ldc >= (crow ? N : M),
+             "coopmat_gemm_f16_tiles: leading dimension too small");
+    LAVA_ARG(aligned(A, 2) && aligned(B, 2) && aligned(C, 4), "coopmat_gemm_f16_tiles: misaligned operand");
+    LAVA_ARG((M / 16) * (N / 16) / 4 < 0x7fffffff, "coopmat_gemm_f16_tiles: too many tiles");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    return launch_coopmat_tiles(static_cast<const f16*>(A), static_cast<const f16*>(B), static_cast<float*>(C), M, N,
+                                K, lda, ldb, ldc, layout, as_stream(stream));
+}
+
+}  // extern "C"

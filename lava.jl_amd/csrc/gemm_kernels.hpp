@@ -1,0 +1,27 @@
+// gemm_kernels.hpp -- host launchers of the GEMM kernels (internal).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "gemm_common.hpp"
+
+namespace lava {
+
+// Any layout, any shape; C row-major with ldc.
+template <typename T>
+int launch_gemm_staged(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
+                       int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, hipStream_t s);
+
+// The 16x16x16 vocabulary-tile GEMM (fp16 -> fp32); M, N, K multiples of 16.
+int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                         int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s);
+
+// The fast path: A row-major (M x K), B column-major (K x N) -- both K-contiguous --
+// C row-major.  Requires tn_gemm_eligible().
+template <typename T>
+bool tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                      int64_t ldb, int64_t ldc);
+template <typename T>
+int launch_gemm_tn(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
+                   int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s);
+
+}  // namespace lava

@@ -1,0 +1,269 @@
+// gemm_w8a16.hip -- decode-shape GEMM with int8 weights and a per-column scale.
+//
+// Lava writes this as a coopmat GEMM whose epilogue is a per-element callback
+// carrying the scale pointer in `extras` (src/device/coopmat_intrinsics.jl:535-628,
+// 569-572): Y[r, c] = s[c] * sum_k X[r, k] W[k, c].  At M = 16 the product is
+// bound by reading W once from HBM (58.7 MB at the headline shape), so the kernel
+// is a weight stream:
+//
+//  * a wavefront owns 128 columns and a 32-row slice of K per step: lane (q, g)
+//    = (lane % 16, lane / 16) loads 8 bytes (columns 8q .. 8q + 7) of the 8 rows
+//    8g .. 8g + 7 -- 16 lanes cover one 128-byte row segment;
+//  * those 64 bytes are 8 columns x 8 k-values; column t of them is lane q's
+//    column of MFMA tile t (tile t = columns {8q + t}), k-values in lane group g:
+//    exactly the B operand of v_mfma_f32_16x16x32_f16, after an in-register byte
+//    transpose (v_perm_b32) and an exact int8 -> fp16 conversion
+//    (0x6400 | (w ^ 0x80) is the fp16 value 1152 + w; subtract 1152);
+//  * X (16 x 32 per step, fp16) is the A operand, read straight from global/L2;
+//  * 4 wavefronts per workgroup split the workgroup's K range and reduce through
+//    LDS; `splits` workgroups split K further and the last one to finish (atomic
+//    ticket) adds the partials in a fixed order, applies s[c] and writes Y, so the
+//    result does not depend on arrival order;
+//  * the scale multiply is the fused per-element epilogue.
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+
+#include "lava_coopmat.hpp"
+#include "lava_hip_internal.hpp"
+
+namespace lava {
+
+constexpr int W8_COLS = 128;   // columns per workgroup
+constexpr int W8_KSTEP = 32;   // k per MFMA step
+constexpr int W8_WAVES = 4;
+
+__device__ __forceinline__ uint32_t w8_pair(uint32_t lo_row, uint32_t hi_row, int byte) {
+    // [lo_row.byte, 0, hi_row.byte, 0] -> two fp16 values 1152 + w, then subtract 1152
+    const uint32_t sel = (uint32_t)byte | 0x0c00u | ((uint32_t)(byte + 4) << 16) | 0x0c000000u;
+    return __builtin_amdgcn_perm(hi_row, lo_row, sel) ^ 0x64806480u;
+}
+
+template <int KSTEPS>
+__global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
+                                                    const f16* __restrict__ scale, float* __restrict__ Y,
+                                                    float* __restrict__ partial, int* __restrict__ tickets, int M,
+                                                    int N, int64_t ldx, int64_t ldw, int64_t ldy, int splits) {
+    __shared__ __attribute__((aligned(16))) float red[W8_WAVES][16][W8_COLS];
+    __shared__ int is_last;
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int q = lane & 15, g = lane >> 4;
+    const int cb = blockIdx.x;             // column block
+    const int split = blockIdx.y;          // K split
+    const int mb = blockIdx.z;             // 16-row block of X / Y
+    const int n0 = cb * W8_COLS;
+    const int m0 = mb * 16;
+    const int64_t k_wave = ((int64_t)split * W8_WAVES + w) * (KSTEPS * W8_KSTEP);
+
+    // A operand rows: X[m0 + q][k .. k + 8) for this lane's group; rows >= M read as 0
+    const bool xrow_ok = (m0 + q) < M;
+    const f16* xp = X + (int64_t)(m0 + q) * ldx + k_wave + 8 * g;
+    const int8_t* wp = W + (k_wave + 8 * g) * ldw + n0 + 8 * q;
+
+    f32x4 acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const f16x8 bias = {(f16)-1152.f, (f16)-1152.f, (f16)-1152.f, (f16)-1152.f,
+                        (f16)-1152.f, (f16)-1152.f, (f16)-1152.f, (f16)-1152.f};
+#pragma unroll 2
+    for (int s = 0; s < KSTEPS; ++s) {
+        u32x2 rows[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            rows[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(wp + ((int64_t)s * W8_KSTEP + r) * ldw));
+        uint4 xa = make_uint4(0, 0, 0, 0);
+        if (xrow_ok) xa = *reinterpret_cast<const uint4*>(xp + s * W8_KSTEP);
+        const f16x8 a = __builtin_bit_cast(f16x8, xa);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const int byte = t & 3;
+            uint4 bw;
+            if (t < 4) {
+                bw.x = w8_pair(rows[0].x, rows[1].x, byte);
+                bw.y = w8_pair(rows[2].x, rows[3].x, byte);
+                bw.z = w8_pair(rows[4].x, rows[5].x, byte);
+                bw.w = w8_pair(rows[6].x, rows[7].x, byte);
+            } else {
+                bw.x = w8_pair(rows[0].y, rows[1].y, byte);
+                bw.y = w8_pair(rows[2].y, rows[3].y, byte);
+                bw.z = w8_pair(rows[4].y, rows[5].y, byte);
+                bw.w = w8_pair(rows[6].y, rows[7].y, byte);
+            }
+            const f16x8 b = __builtin_bit_cast(f16x8, bw) + bias;   // exact: w = (1152 + w) - 1152
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
+        }
+    }
+    // acc[t] lane holds column 8q + t and rows 4g + j of this wave's partial
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[w][4 * g + j][8 * q + t] = acc[t][j];
+    __syncthreads();
+
+    // workgroup sum over the 4 wavefronts: thread -> (row, 8 consecutive columns)
+    const int tid = threadIdx.x;
+    const int row = tid >> 4, c8 = (tid & 15) * 8;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        v[i] = ((red[0][row][c8 + i] + red[1][row][c8 + i]) + red[2][row][c8 + i]) + red[3][row][c8 + i];
+
+    const int grow = m0 + row;
+    if (splits > 1) {
+        float* mine = partial + (((int64_t)split * gridDim.z + mb) * 16 + row) * N + n0 + c8;
+#pragma unroll
+        for (int i = 0; i < 8; i += 4) *reinterpret_cast<float4*>(mine + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) {
+            const int ticket = atomicAdd(&tickets[mb * gridDim.x + cb], 1);
+            is_last = (ticket == splits - 1);
+        }
+        __syncthreads();
+        if (!is_last) return;
+        __threadfence();
+        // fixed-order sum of all splits
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.f;
+        for (int sp = 0; sp < splits; ++sp) {
+            const float* p = partial + (((int64_t)sp * gridDim.z + mb) * 16 + row) * N + n0 + c8;
+            const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+            const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
+            v[0] += a[0]; v[1] += a[1]; v[2] += a[2]; v[3] += a[3];
+            v[4] += b[0]; v[5] += b[1]; v[6] += b[2]; v[7] += b[3];
+        }
+        if (tid == 0) tickets[mb * gridDim.x + cb] = 0;   // ready for the next call
+    }
+    if (grow < M) {
+        float* yp = Y + (int64_t)grow * ldy + n0 + c8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) yp[i] = v[i] * (float)scale[n0 + c8 + i];
+    }
+}
+
+// Any layout, any shape: one thread per output element, fp32 sums.
+__global__ void w8a16_generic_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
+                                     const f16* __restrict__ scale, float* __restrict__ Y, int64_t M, int64_t N,
+                                     int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= M * N) return;
+    const int64_t r = idx / N, c = idx % N;
+    const bool xrow = layout & 1u, wrow = layout & 2u, yrow = layout & 4u;
+    float s = 0.f;
+    for (int64_t k = 0; k < K; ++k) {
+        const float x = (float)X[xrow ? r * ldx + k : k * ldx + r];
+        const float wv = (float)W[wrow ? k * ldw + c : c * ldw + k];
+        s = fmaf(x, wv, s);
+    }
+    Y[yrow ? r * ldy + c : c * ldy + r] = s * (float)scale[c];
+}
+
+// Per-(device, stream) workspace for the split-K partials and tickets.  Tickets
+// are zeroed once when the buffer is created and returned to zero by the
+// workgroup that consumes them.
+struct W8Workspace {
+    void* buf = nullptr;
+    size_t bytes = 0;
+};
+static std::mutex g_ws_mutex;
+static std::map<std::pair<int, void*>, W8Workspace> g_ws;
+
+static int get_workspace(void* stream, size_t partial_bytes, size_t ticket_bytes, float** partial, int** tickets) {
+    int dev = 0;
+    LAVA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    W8Workspace& ws = g_ws[{dev, stream}];
+    const size_t need = partial_bytes + ticket_bytes;
+    if (ws.bytes < need) {
+        if (ws.buf) {
+            LAVA_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
+            LAVA_HIP_TRY(hipFree(ws.buf));
+            ws.buf = nullptr;
+            ws.bytes = 0;
+        }
+        void* p = nullptr;
+        LAVA_HIP_TRY(hipMalloc(&p, need));
+        int rc = lava_hip_fill_bytes(static_cast<char*>(p) + partial_bytes, 0, ticket_bytes, stream);
+        if (rc != LAVA_HIP_OK) {
+            (void)hipFree(p);
+            return rc;
+        }
+        ws.buf = p;
+        ws.bytes = need;
+    }
+    *partial = static_cast<float*>(ws.buf);
+    *tickets = reinterpret_cast<int*>(static_cast<char*>(ws.buf) + partial_bytes);
+    return LAVA_HIP_OK;
+}
+
+}  // namespace lava
+
+using namespace lava;
+
+extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N,
+                                   int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream) {
+    LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "gemm_w8a16: negative extent (M=%lld N=%lld K=%lld)", (long long)M,
+             (long long)N, (long long)K);
+    LAVA_ARG(layout <= 7u, "gemm_w8a16: layout %u has bits beyond X/W/Y row-major", layout);
+    if (M == 0 || N == 0) return LAVA_HIP_OK;
+    LAVA_ARG(Y != nullptr && scale != nullptr, "gemm_w8a16: null Y or scale");
+    LAVA_ARG(K == 0 || (X != nullptr && W != nullptr), "gemm_w8a16: null X or W");
+    const bool xrow = layout & 1u, wrow = layout & 2u, yrow = layout & 4u;
+    LAVA_ARG(ldx >= (xrow ? (K > 0 ? K : 1) : M), "gemm_w8a16: ldx = %lld too small", (long long)ldx);
+    LAVA_ARG(ldw >= (wrow ? N : (K > 0 ? K : 1)), "gemm_w8a16: ldw = %lld too small", (long long)ldw);
+    LAVA_ARG(ldy >= (yrow ? N : M), "gemm_w8a16: ldy = %lld too small", (long long)ldy);
+    LAVA_ARG(aligned(X, 2) && aligned(scale, 2) && aligned(Y, 4), "gemm_w8a16: misaligned X, scale or Y");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    hipStream_t s = as_stream(stream);
+
+    // fast path: all row-major, N in 128-column blocks, K in 128-row wavefront slices
+    const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % (W8_WAVES * W8_KSTEP) == 0 &&
+                      ldw % 8 == 0 && ldx % 8 == 0 && aligned(W, 8) && aligned(X, 16) && N <= 0x7fffffff &&
+                      M <= 0x7fffffff;
+    if (fast) {
+        // split K so that there are >= 2 workgroups per CU where K allows
+        const int64_t cblocks = N / W8_COLS, mblocks = (M + 15) / 16;
+        const int64_t kwave_steps = K / (W8_WAVES * W8_KSTEP);   // steps per wave at 1 split
+        int splits = 1;
+        while (splits < 16 && cblocks * mblocks * splits < 512 && kwave_steps % (2 * splits) == 0 &&
+               kwave_steps / (2 * splits) >= 2)
+            splits *= 2;
+        const int64_t ksteps = kwave_steps / splits;
+        LAVA_REQUIRE(mblocks <= 65535 && cblocks <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: grid too large");
+        float* partial = nullptr;
+        int* tickets = nullptr;
+        if (splits > 1) {
+            rc = get_workspace(stream, (size_t)splits * (size_t)mblocks * 16 * (size_t)N * sizeof(float),
+                               (size_t)(cblocks * mblocks) * sizeof(int), &partial, &tickets);
+            if (rc != LAVA_HIP_OK) return rc;
+        }
+        const dim3 grid((unsigned)cblocks, (unsigned)splits, (unsigned)mblocks);
+#define LAVA_W8_LAUNCH(KS)                                                                                           \
+    hipLaunchKernelGGL(w8a16_kernel<KS>, grid, dim3(256), 0, s, (const f16*)X, (const int8_t*)W, (const f16*)scale, \
+                       (float*)Y, partial, tickets, (int)M, (int)N, ldx, ldw, ldy, splits)
+        switch (ksteps) {
+        case 1: LAVA_W8_LAUNCH(1); break;
+        case 2: LAVA_W8_LAUNCH(2); break;
+        case 4: LAVA_W8_LAUNCH(4); break;
+        case 8: LAVA_W8_LAUNCH(8); break;
+        case 16: LAVA_W8_LAUNCH(16); break;
+        case 32: LAVA_W8_LAUNCH(32); break;
+        default: goto generic;
+        }
+#undef LAVA_W8_LAUNCH
+        LAVA_LAUNCH_CHECK("w8a16_kernel");
+        return LAVA_HIP_OK;
+    }
+generic : {
+    const int64_t total = M * N;
+    LAVA_REQUIRE((total + 255) / 256 <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: problem too large");
+    hipLaunchKernelGGL(w8a16_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (const f16*)X,
+                       (const int8_t*)W, (const f16*)scale, (float*)Y, M, N, K, ldx, ldw, ldy, layout);
+    LAVA_LAUNCH_CHECK("w8a16_generic_kernel");
+    return LAVA_HIP_OK;
+}
+}

@@ -1,0 +1,404 @@
+// lava_coopmat.hpp -- the cooperative-matrix device vocabulary on CDNA4 (gfx950).
+//
+// Lava.jl's kernels are written against an opaque subgroup tile,
+// `CoopMatrix{T,M,N,Use,Scope}` (src/vocabulary/coopmat.jl:36-92), and eleven
+// operations on it (src/vocabulary/coopmat.jl:216-312).  On MI355X a subgroup is a
+// 64-lane wavefront and the tile lives in the registers an MFMA instruction reads
+// and writes, so the "opaque handle" becomes `Frag<T, R, C, Use>`: the lane's share
+// of an R x C tile, held as a small array of registers whose (row, column) mapping
+// is the MFMA operand layout below.
+//
+// Layouts (64 lanes, lane = threadIdx.x % 64):
+//   Accumulator R x C, C in {16, 32}:
+//     C == 16: lane holds column lane % 16, rows 4 * (lane / 16) + j,            j < 4
+//     C == 32: lane holds column lane % 32, rows 8 * (j / 4) + 4 * (lane / 32) + j % 4,
+//              j < 16
+//   MatrixA R x K, R in {16, 32}: lane holds row lane % R, columns (k)
+//     (lane / R) * (K * R / 64) + j, j < K * R / 64 -- consecutive k per lane.
+//   MatrixB K x C, C in {16, 32}: lane holds column lane % C, rows (k)
+//     (lane / C) * (K * C / 64) + j.
+// A and B share one k distribution, and an MFMA pairs A's slot (group, j) with
+// B's slot (group, j), so the product is the same whatever order the hardware
+// consumes the slots in; the accumulator map is the one fact taken from the
+// hardware, and the per-element identity test pins it.
+//
+// Semantics of each operation are those of the SPIR-V instruction Lava's emitter
+// writes for it (src/compiler/spirv/coopmat.jl:664-991):
+//   load / store          OpCooperativeMatrixLoad/StoreKHR, ColumnMajor by default,
+//                         RowMajor on request (coopmat.jl:664-744).  Offsets here are
+//                         0-based element offsets; the host mirror maps Lava's 1-based
+//                         `offset` onto them (src/device/coopmat_intrinsics.jl:57-75).
+//   zero                  OpConstantNull (coopmat.jl:746-762)
+//   mma                   OpCooperativeMatrixMulAddKHR; int8 operands signed
+//                         (coopmat.jl:115-151, 764-781)
+//   convert               OpFConvert, round to nearest even (coopmat.jl:783-824;
+//                         src/compiler/passes/exact_narrowing.jl:31-36)
+//   mul / add             OpFMul / OpFAdd component-wise (coopmat.jl:870-885)
+//   length/getcomp/setcomp  this lane's components, 0-based (coopmat.jl:826-868)
+//   perelement            OpCooperativeMatrixPerElementOpNV: f(row, col, e, extras...)
+//                         with 0-based row/col (src/device/coopmat_intrinsics.jl:535-678)
+//   reduce                OpCooperativeMatrixReduceNV: combine along Row (1), Column
+//                         (2) or both (3); the result is smeared over the reduced
+//                         axis, not a vector (src/device/coopmat_intrinsics.jl:685-755)
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lava {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+enum Use { MatrixA = 0, MatrixB = 1, Accumulator = 2 };
+
+// CoopMatReduce masks (src/vocabulary/coopmat.jl:292-297)
+enum ReduceMask : uint32_t { ReduceRow = 1u, ReduceColumn = 2u, ReduceRowAndColumn = 3u };
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
+
+// ---------------------------------------------------------------------------
+// Lane <-> (row, col) maps
+// ---------------------------------------------------------------------------
+template <int R, int C, Use U>
+struct Layout;
+
+template <int R, int K>
+struct Layout<R, K, MatrixA> {
+    static_assert(R == 16 || R == 32, "MatrixA rows must be 16 or 32");
+    static constexpr int groups = 64 / R;
+    static constexpr int len = K / groups;
+    static_assert(len * groups == K && len >= 1, "K must split over the lane groups");
+    __device__ static int row(int lane, int) { return lane % R; }
+    __device__ static int col(int lane, int j) { return (lane / R) * len + j; }
+};
+
+template <int K, int C>
+struct Layout<K, C, MatrixB> {
+    static_assert(C == 16 || C == 32, "MatrixB columns must be 16 or 32");
+    static constexpr int groups = 64 / C;
+    static constexpr int len = K / groups;
+    static_assert(len * groups == K && len >= 1, "K must split over the lane groups");
+    __device__ static int row(int lane, int j) { return (lane / C) * len + j; }
+    __device__ static int col(int lane, int) { return lane % C; }
+};
+
+template <>
+struct Layout<16, 16, Accumulator> {
+    static constexpr int len = 4;
+    __device__ static int row(int lane, int j) { return 4 * (lane / 16) + j; }
+    __device__ static int col(int lane, int) { return lane % 16; }
+};
+
+template <>
+struct Layout<32, 32, Accumulator> {
+    static constexpr int len = 16;
+    __device__ static int row(int lane, int j) { return 8 * (j / 4) + 4 * (lane / 32) + (j % 4); }
+    __device__ static int col(int lane, int) { return lane % 32; }
+};
+
+// ---------------------------------------------------------------------------
+// Fragment
+// ---------------------------------------------------------------------------
+template <typename T, int R, int C, Use U>
+struct Frag {
+    using L = Layout<R, C, U>;
+    static constexpr int len = L::len;
+    T v[L::len];
+};
+
+// coopmat_length / getcomp / setcomp
+template <typename T, int R, int C, Use U>
+__device__ __forceinline__ constexpr int length(const Frag<T, R, C, U>&) { return Frag<T, R, C, U>::len; }
+template <typename T, int R, int C, Use U>
+__device__ __forceinline__ T getcomp(const Frag<T, R, C, U>& m, int i) { return m.v[i]; }
+template <typename T, int R, int C, Use U>
+__device__ __forceinline__ Frag<T, R, C, U> setcomp(Frag<T, R, C, U> m, int i, T x) { m.v[i] = x; return m; }
+
+template <typename FragT>
+__device__ __forceinline__ FragT zero() {
+    FragT m;
+#pragma unroll
+    for (int j = 0; j < FragT::len; ++j) m.v[j] = 0;
+    return m;
+}
+
+template <typename FragT, typename T>
+__device__ __forceinline__ FragT fill(T x) {
+    FragT m;
+#pragma unroll
+    for (int j = 0; j < FragT::len; ++j) m.v[j] = x;
+    return m;
+}
+
+// Element (r, c) of a tile whose top-left is p: row-major r*ld + c, column-major
+// c*ld + r.  `ld` is Lava's `stride`, the distance between consecutive columns
+// (column-major) or rows (row-major), in elements.
+__device__ __forceinline__ int64_t tile_index(int r, int c, int64_t ld, bool rowmajor) {
+    return rowmajor ? (int64_t)r * ld + c : (int64_t)c * ld + r;
+}
+
+template <typename FragT, typename S>
+__device__ __forceinline__ FragT load(const S* p, int64_t ld, bool rowmajor) {
+    FragT m;
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < FragT::len; ++j)
+        m.v[j] = (decltype(m.v[0]))p[tile_index(FragT::L::row(lane, j), FragT::L::col(lane, j), ld, rowmajor)];
+    return m;
+}
+
+template <typename S, typename T, int R, int C, Use U>
+__device__ __forceinline__ void store(S* p, int64_t ld, bool rowmajor, const Frag<T, R, C, U>& m) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < Frag<T, R, C, U>::len; ++j)
+        p[tile_index(Frag<T, R, C, U>::L::row(lane, j), Frag<T, R, C, U>::L::col(lane, j), ld, rowmajor)] = (S)m.v[j];
+}
+
+// ---------------------------------------------------------------------------
+// Round-to-nearest-even narrowing (coopmat_convert of an fp32 accumulator)
+// ---------------------------------------------------------------------------
+template <typename To>
+__device__ __forceinline__ To narrow(float x);
+template <>
+__device__ __forceinline__ float narrow<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ f16 narrow<f16>(float x) { return (f16)x; }     // v_cvt_f16_f32, RNE
+template <>
+__device__ __forceinline__ bf16 narrow<bf16>(float x) { return (bf16)x; }  // v_cvt_pk_bf16_f32, RNE
+
+template <typename To, typename T, int R, int C, Use U>
+__device__ __forceinline__ Frag<To, R, C, U> convert(const Frag<T, R, C, U>& m) {
+    Frag<To, R, C, U> o;
+#pragma unroll
+    for (int j = 0; j < Frag<T, R, C, U>::len; ++j) o.v[j] = narrow<To>((float)m.v[j]);
+    return o;
+}
+
+// coopmat_mul / coopmat_add
+template <typename T, int R, int C, Use U>
+__device__ __forceinline__ Frag<T, R, C, U> mul(const Frag<T, R, C, U>& a, const Frag<T, R, C, U>& b) {
+    Frag<T, R, C, U> o;
+#pragma unroll
+    for (int j = 0; j < Frag<T, R, C, U>::len; ++j) o.v[j] = a.v[j] * b.v[j];
+    return o;
+}
+template <typename T, int R, int C, Use U>
+__device__ __forceinline__ Frag<T, R, C, U> add(const Frag<T, R, C, U>& a, const Frag<T, R, C, U>& b) {
+    Frag<T, R, C, U> o;
+#pragma unroll
+    for (int j = 0; j < Frag<T, R, C, U>::len; ++j) o.v[j] = a.v[j] + b.v[j];
+    return o;
+}
+
+// ---------------------------------------------------------------------------
+// coopmat_perelement: f(row, col, e, extras...) with 0-based row and col
+// ---------------------------------------------------------------------------
+template <typename F, typename T, int R, int C, Use U, typename... X>
+__device__ __forceinline__ Frag<T, R, C, U> perelement(F f, Frag<T, R, C, U> m, X... extras) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < Frag<T, R, C, U>::len; ++j)
+        m.v[j] = f((uint32_t)Frag<T, R, C, U>::L::row(lane, j), (uint32_t)Frag<T, R, C, U>::L::col(lane, j), m.v[j],
+                   extras...);
+    return m;
+}
+
+// The matrix-operand form: f(row, col, m_e, o_e) over corresponding elements.
+template <typename F, typename T, int R, int C, Use U>
+__device__ __forceinline__ Frag<T, R, C, U> perelement_m(F f, Frag<T, R, C, U> m, const Frag<T, R, C, U>& o) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < Frag<T, R, C, U>::len; ++j)
+        m.v[j] = f((uint32_t)Frag<T, R, C, U>::L::row(lane, j), (uint32_t)Frag<T, R, C, U>::L::col(lane, j), m.v[j],
+                   o.v[j]);
+    return m;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane exchange (ds_swizzle-free: ds_bpermute through __shfl_xor)
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ T xor_lane(T x, int mask) {
+    static_assert(sizeof(T) == 4, "32-bit lanes only");
+    return __shfl_xor(x, mask, 64);
+}
+
+// coopmat_reduce over an accumulator fragment, same-shape destination.
+// Row: combine the elements of each row (across columns); Column: of each column.
+template <uint32_t MASK, typename F, typename T, int R, int C>
+__device__ __forceinline__ Frag<T, R, C, Accumulator> reduce(F f, Frag<T, R, C, Accumulator> m) {
+    constexpr int ncol_lanes = C;  // lanes sharing a row differ in lane % C
+    if constexpr ((MASK & ReduceRow) != 0) {
+#pragma unroll
+        for (int j = 0; j < Frag<T, R, C, Accumulator>::len; ++j) {
+#pragma unroll
+            for (int s = 1; s < ncol_lanes; s <<= 1) m.v[j] = f(m.v[j], xor_lane(m.v[j], s));
+        }
+    }
+    if constexpr ((MASK & ReduceColumn) != 0) {
+        T acc = m.v[0];
+#pragma unroll
+        for (int j = 1; j < Frag<T, R, C, Accumulator>::len; ++j) acc = f(acc, m.v[j]);
+#pragma unroll
+        for (int s = ncol_lanes; s < 64; s <<= 1) acc = f(acc, xor_lane(acc, s));
+#pragma unroll
+        for (int j = 0; j < Frag<T, R, C, Accumulator>::len; ++j) m.v[j] = acc;
+    }
+    return m;
+}
+
+// ---------------------------------------------------------------------------
+// coopmat_muladd: D = A * B + C, accumulated in C's type
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ Frag<float, 16, 16, Accumulator> mma(const Frag<f16, 16, 16, MatrixA>& a,
+                                                                const Frag<f16, 16, 16, MatrixB>& b,
+                                                                Frag<float, 16, 16, Accumulator> c) {
+    f16x4 av = {a.v[0], a.v[1], a.v[2], a.v[3]};
+    f16x4 bv = {b.v[0], b.v[1], b.v[2], b.v[3]};
+    f32x4 cv = {c.v[0], c.v[1], c.v[2], c.v[3]};
+    cv = __builtin_amdgcn_mfma_f32_16x16x16f16(av, bv, cv, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) c.v[j] = cv[j];
+    return c;
+}
+
+__device__ __forceinline__ Frag<float, 16, 16, Accumulator> mma(const Frag<f16, 16, 32, MatrixA>& a,
+                                                                const Frag<f16, 32, 16, MatrixB>& b,
+                                                                Frag<float, 16, 16, Accumulator> c) {
+    f16x8 av, bv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { av[j] = a.v[j]; bv[j] = b.v[j]; }
+    f32x4 cv = {c.v[0], c.v[1], c.v[2], c.v[3]};
+    cv = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, cv, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) c.v[j] = cv[j];
+    return c;
+}
+
+__device__ __forceinline__ Frag<float, 16, 16, Accumulator> mma(const Frag<bf16, 16, 32, MatrixA>& a,
+                                                                const Frag<bf16, 32, 16, MatrixB>& b,
+                                                                Frag<float, 16, 16, Accumulator> c) {
+    bf16x8 av, bv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { av[j] = a.v[j]; bv[j] = b.v[j]; }
+    f32x4 cv = {c.v[0], c.v[1], c.v[2], c.v[3]};
+    cv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, cv, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) c.v[j] = cv[j];
+    return c;
+}
+
+__device__ __forceinline__ Frag<float, 32, 32, Accumulator> mma(const Frag<f16, 32, 16, MatrixA>& a,
+                                                                const Frag<f16, 16, 32, MatrixB>& b,
+                                                                Frag<float, 32, 32, Accumulator> c) {
+    f16x8 av, bv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { av[j] = a.v[j]; bv[j] = b.v[j]; }
+    f32x16 cv;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) cv[j] = c.v[j];
+    cv = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, cv, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) c.v[j] = cv[j];
+    return c;
+}
+
+__device__ __forceinline__ Frag<float, 32, 32, Accumulator> mma(const Frag<bf16, 32, 16, MatrixA>& a,
+                                                                const Frag<bf16, 16, 32, MatrixB>& b,
+                                                                Frag<float, 32, 32, Accumulator> c) {
+    bf16x8 av, bv;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) { av[j] = a.v[j]; bv[j] = b.v[j]; }
+    f32x16 cv;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) cv[j] = c.v[j];
+    cv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, cv, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) c.v[j] = cv[j];
+    return c;
+}
+
+// int8 x int8 -> int32, signed operands, 16x16x16: the 16x16x32 instruction with
+// the upper half of each lane's k slots zero.
+__device__ __forceinline__ Frag<int32_t, 16, 16, Accumulator> mma(const Frag<int8_t, 16, 16, MatrixA>& a,
+                                                                  const Frag<int8_t, 16, 16, MatrixB>& b,
+                                                                  Frag<int32_t, 16, 16, Accumulator> c) {
+    uint32_t alo = 0, blo = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        alo |= (uint32_t)(uint8_t)a.v[j] << (8 * j);
+        blo |= (uint32_t)(uint8_t)b.v[j] << (8 * j);
+    }
+    long av = (long)(uint64_t)alo, bv = (long)(uint64_t)blo;
+    i32x4 cv = {c.v[0], c.v[1], c.v[2], c.v[3]};
+    cv = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, cv, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) c.v[j] = cv[j];
+    return c;
+}
+
+__device__ __forceinline__ Frag<int32_t, 16, 16, Accumulator> mma(const Frag<int8_t, 16, 64, MatrixA>& a,
+                                                                  const Frag<int8_t, 64, 16, MatrixB>& b,
+                                                                  Frag<int32_t, 16, 16, Accumulator> c) {
+    i32x4 av, bv;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        uint32_t x = 0, y = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            x |= (uint32_t)(uint8_t)a.v[4 * w + j] << (8 * j);
+            y |= (uint32_t)(uint8_t)b.v[4 * w + j] << (8 * j);
+        }
+        av[w] = (int)x;
+        bv[w] = (int)y;
+    }
+    i32x4 cv = {c.v[0], c.v[1], c.v[2], c.v[3]};
+    cv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, cv, 0, 0, 0);
+    for (int j = 0; j < 4; ++j) c.v[j] = cv[j];
+    return c;
+}
+
+// uint8 x uint8 -> uint32 (the unsigned product, no signedness operands:
+// test/spirv/test_coopmat_int8.jl:71-98).  CDNA4's integer MFMA is signed, so the
+// unsigned tile product runs on the packed VALU dot instruction v_dot4_u32_u8:
+// each lane produces its accumulator elements from a row of A and a column of B
+// exchanged through the lane's register copies.
+template <int K>
+__device__ __forceinline__ Frag<uint32_t, 16, 16, Accumulator> mma_u8(const uint8_t* a_rows, int64_t lda_elems_row,
+                                                                      const uint8_t* b_cols, int64_t ldb_elems_col,
+                                                                      Frag<uint32_t, 16, 16, Accumulator> c) {
+    // a_rows: row r of A at a_rows + r*lda (k contiguous); b_cols: column n of B at
+    // b_cols + n*ldb (k contiguous).  Used by the tile-level vocabulary kernels only.
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = Layout<16, 16, Accumulator>::row(lane, j), n = Layout<16, 16, Accumulator>::col(lane, j);
+        uint32_t s = c.v[j];
+        for (int k = 0; k < K; k += 4) {
+            uint32_t x = 0, y = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                x |= (uint32_t)a_rows[r * lda_elems_row + k + t] << (8 * t);
+                y |= (uint32_t)b_cols[n * ldb_elems_col + k + t] << (8 * t);
+            }
+            s = __builtin_amdgcn_udot4(x, y, s, false);
+        }
+        c.v[j] = s;
+    }
+    return c;
+}
+
+// dot4x8 (src/vocabulary/vocabulary.jl:31-35): v_dot4_i32_i8
+__device__ __forceinline__ int32_t dot4x8(uint32_t a, uint32_t b) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, 0, false);
+}
+
+}  // namespace lava

@@ -1,0 +1,44 @@
+// lava_hip_internal.hpp -- status handling shared by the entry points.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+
+#include "lava_hip.h"
+
+namespace lava {
+
+// Thread-local message behind lava_hip_last_error().
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+int hip_fail(hipError_t e, const char* what);
+// Launch check: the error (if any) hipGetLastError reports for the launch just made.
+int check_launch(const char* kernel);
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace lava
+
+#define LAVA_REQUIRE(cond, code, ...)      \
+    do {                                   \
+        if (!(cond)) {                     \
+            ::lava::set_error(__VA_ARGS__); \
+            return (code);                 \
+        }                                  \
+    } while (0)
+
+#define LAVA_ARG(cond, ...) LAVA_REQUIRE(cond, LAVA_HIP_ERR_INVALID_ARG, __VA_ARGS__)
+
+#define LAVA_HIP_TRY(expr)                                      \
+    do {                                                        \
+        hipError_t _lava_e = (expr);                            \
+        if (_lava_e != hipSuccess) return ::lava::hip_fail(_lava_e, #expr); \
+    } while (0)
+
+#define LAVA_LAUNCH_CHECK(name)                    \
+    do {                                           \
+        int _lava_rc = ::lava::check_launch(name); \
+        if (_lava_rc != LAVA_HIP_OK) return _lava_rc; \
+    } while (0)

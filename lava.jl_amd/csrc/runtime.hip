@@ -1,0 +1,253 @@
+// runtime.hip -- device-memory plumbing, errors and capability queries.
+//
+// Lava itself owns nothing at run time: buffers, queues and launches are
+// Mantle's (README.md:11-13; src/compiler/cache.jl:16-17).  A C ABI called from
+// Julia's `ccall` needs the minimum of that layer -- allocate, copy, synchronise,
+// time -- so it is here as thin wrappers over the HIP runtime.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "lava_hip_internal.hpp"
+
+namespace lava {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+void clear_error() { g_err[0] = 0; }
+
+int hip_fail(hipError_t e, const char* what) {
+    set_error("%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+    return e == hipErrorNoDevice ? LAVA_HIP_ERR_NO_DEVICE : LAVA_HIP_ERR_HIP;
+}
+
+int check_launch(const char* kernel) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("launch of %s failed: %s (%d)", kernel, hipGetErrorString(e), (int)e);
+        return LAVA_HIP_ERR_HIP;
+    }
+    return LAVA_HIP_OK;
+}
+
+__global__ void fill_bytes_kernel(uint8_t* __restrict__ dst, uint8_t value, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const uint32_t w = 0x01010101u * value;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    // 16-byte stores over the aligned body, bytes at the ends
+    const size_t head = (16 - ((uintptr_t)dst & 15)) & 15;
+    if (n <= head + 16) {
+        for (; i < n; i += stride) dst[i] = value;
+        return;
+    }
+    for (size_t b = i; b < head; b += stride) dst[b] = value;
+    uint4* body = reinterpret_cast<uint4*>(dst + head);
+    const size_t nv = (n - head) / 16;
+    for (size_t v = i; v < nv; v += stride) body[v] = make_uint4(w, w, w, w);
+    for (size_t b = head + nv * 16 + i; b < n; b += stride) dst[b] = value;
+}
+
+}  // namespace lava
+
+using namespace lava;
+
+extern "C" {
+
+const char* lava_hip_last_error(void) { return g_err; }
+
+int lava_hip_version(void) { return 100; }
+
+int lava_hip_init(void) {
+    static std::once_flag once;
+    static int status = LAVA_HIP_OK;
+    static char msg[512];
+    std::call_once(once, [] {
+        int n = 0;
+        hipError_t e = hipGetDeviceCount(&n);
+        if (e != hipSuccess || n == 0) {
+            snprintf(msg, sizeof(msg), "no HIP device available (%s)", hipGetErrorString(e));
+            status = LAVA_HIP_ERR_NO_DEVICE;
+            return;
+        }
+        hipDeviceProp_t p;
+        e = hipGetDeviceProperties(&p, 0);
+        if (e != hipSuccess) {
+            snprintf(msg, sizeof(msg), "hipGetDeviceProperties failed: %s", hipGetErrorString(e));
+            status = LAVA_HIP_ERR_HIP;
+            return;
+        }
+        if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+            snprintf(msg, sizeof(msg), "device 0 is %s; liblava_hip.so is built for gfx950 only", p.gcnArchName);
+            status = LAVA_HIP_ERR_NO_DEVICE;
+            return;
+        }
+    });
+    if (status != LAVA_HIP_OK) set_error("%s", msg);
+    return status;
+}
+
+int lava_hip_device_count(int* count) {
+    LAVA_ARG(count != nullptr, "device_count: null output pointer");
+    *count = 0;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice) return LAVA_HIP_OK;
+    LAVA_HIP_TRY(e);
+    *count = n;
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_malloc(void** ptr, size_t bytes) {
+    LAVA_ARG(ptr != nullptr, "malloc: null output pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return LAVA_HIP_OK;
+    LAVA_HIP_TRY(hipMalloc(ptr, bytes));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_free(void* ptr) {
+    if (ptr == nullptr) return LAVA_HIP_OK;
+    LAVA_HIP_TRY(hipFree(ptr));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return LAVA_HIP_OK;
+    LAVA_ARG(dst != nullptr && src != nullptr, "memcpy_h2d: null pointer");
+    LAVA_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return LAVA_HIP_OK;
+    LAVA_ARG(dst != nullptr && src != nullptr, "memcpy_d2h: null pointer");
+    LAVA_HIP_TRY(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return LAVA_HIP_OK;
+    LAVA_ARG(dst != nullptr && src != nullptr, "memcpy_d2d: null pointer");
+    LAVA_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_fill_bytes(void* dst, uint8_t value, size_t bytes, void* stream) {
+    if (bytes == 0) return LAVA_HIP_OK;
+    LAVA_ARG(dst != nullptr, "fill_bytes: null pointer");
+    size_t blocks = (bytes / 16 + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(fill_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                       static_cast<uint8_t*>(dst), value, bytes);
+    LAVA_LAUNCH_CHECK("fill_bytes_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_synchronize(void) {
+    LAVA_HIP_TRY(hipDeviceSynchronize());
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_stream_synchronize(void* stream) {
+    LAVA_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_stream_create(void** stream) {
+    LAVA_ARG(stream != nullptr, "stream_create: null output pointer");
+    hipStream_t s;
+    LAVA_HIP_TRY(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = s;
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_stream_destroy(void* stream) {
+    if (stream == nullptr) return LAVA_HIP_OK;
+    LAVA_HIP_TRY(hipStreamDestroy(as_stream(stream)));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_event_create(void** event) {
+    LAVA_ARG(event != nullptr, "event_create: null output pointer");
+    hipEvent_t e;
+    LAVA_HIP_TRY(hipEventCreate(&e));
+    *event = e;
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_event_destroy(void* event) {
+    if (event == nullptr) return LAVA_HIP_OK;
+    LAVA_HIP_TRY(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_event_record(void* event, void* stream) {
+    LAVA_ARG(event != nullptr, "event_record: null event");
+    LAVA_HIP_TRY(hipEventRecord(reinterpret_cast<hipEvent_t>(event), as_stream(stream)));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_event_elapsed_ms(float* ms, void* start, void* stop) {
+    LAVA_ARG(ms != nullptr && start != nullptr && stop != nullptr, "event_elapsed_ms: null argument");
+    LAVA_HIP_TRY(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)));
+    LAVA_HIP_TRY(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)));
+    return LAVA_HIP_OK;
+}
+
+// gfx950 MFMA shapes, subgroup scope, as (ab, acc, M, N, K).  Dense forms only.
+static const int32_t kShapes[][5] = {
+    {LAVA_HIP_F16, LAVA_HIP_F32, 16, 16, 16}, {LAVA_HIP_F16, LAVA_HIP_F32, 16, 16, 32},
+    {LAVA_HIP_F16, LAVA_HIP_F32, 32, 32, 8},  {LAVA_HIP_F16, LAVA_HIP_F32, 32, 32, 16},
+    {LAVA_HIP_BF16, LAVA_HIP_F32, 16, 16, 16}, {LAVA_HIP_BF16, LAVA_HIP_F32, 16, 16, 32},
+    {LAVA_HIP_BF16, LAVA_HIP_F32, 32, 32, 8}, {LAVA_HIP_BF16, LAVA_HIP_F32, 32, 32, 16},
+    {LAVA_HIP_I8, LAVA_HIP_I32, 16, 16, 32},  {LAVA_HIP_I8, LAVA_HIP_I32, 16, 16, 64},
+    {LAVA_HIP_I8, LAVA_HIP_I32, 32, 32, 16},  {LAVA_HIP_I8, LAVA_HIP_I32, 32, 32, 32},
+    {LAVA_HIP_F32, LAVA_HIP_F32, 16, 16, 4},  {LAVA_HIP_F32, LAVA_HIP_F32, 32, 32, 2},
+};
+
+int lava_hip_matrix_shapes(int32_t* out, int max_rows, int* count) {
+    LAVA_ARG(count != nullptr, "matrix_shapes: null count pointer");
+    const int n = (int)(sizeof(kShapes) / sizeof(kShapes[0]));
+    *count = n;
+    if (out == nullptr) return LAVA_HIP_OK;
+    for (int i = 0; i < n && i < max_rows; ++i) {
+        for (int j = 0; j < 5; ++j) out[6 * i + j] = kShapes[i][j];
+        out[6 * i + 5] = 0;
+    }
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_device_caps(int64_t* out, int n) {
+    LAVA_ARG(out != nullptr || n == 0, "device_caps: null output pointer");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    hipDeviceProp_t p;
+    LAVA_HIP_TRY(hipGetDeviceProperties(&p, 0));
+    int64_t v[12];
+    v[0] = 1;                                   // coopmat: MFMA present
+    v[1] = 16;                                  // tile: squarest fp16->fp32 shape
+    v[2] = p.warpSize;                          // subgroup
+    v[3] = p.warpSize;                          // coopmatsubgroup
+    v[4] = (int64_t)p.sharedMemPerBlock;        // sharedbudget
+    v[5] = p.maxThreadsPerBlock;                // workgrouplimit
+    v[6] = p.multiProcessorCount;               // cores
+    v[7] = (int64_t)(p.maxThreadsPerMultiProcessor / p.warpSize);  // warps resident per CU
+    v[8] = p.clockRate;                         // kHz
+    v[9] = (int64_t)p.totalGlobalMem;
+    v[10] = p.l2CacheSize;
+    v[11] = 950;
+    for (int i = 0; i < n && i < 12; ++i) out[i] = v[i];
+    return LAVA_HIP_OK;
+}
+
+}  // extern "C"

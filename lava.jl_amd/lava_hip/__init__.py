@@ -1,0 +1,28 @@
+"""lava_hip -- MI355X (gfx950) implementation of Lava.jl's cooperative-matrix path.
+
+The compute lives in liblava_hip.so (hand-written HIP kernels, C ABI in
+include/lava_hip.h).  This package is its Python host mirror: loader, device
+arrays, the host half of the vocabulary, and destination-first kernel calls.
+"""
+from . import _lib
+from ._lib import InvalidArgument, LavaHIPError, NoDevice, Unsupported, load
+from .device import Event, HIPDeviceArray, Stream, device_count, synchronize
+from .kernels import (coopmat_convert, coopmat_gemm_tiles, coopmat_muladd_16x16x16, coopmat_perelement_pair,
+                      coopmat_perelement_rowcol, coopmat_reduce, dot4x8, fill_i8, fill_normal, fill_uniform,
+                      flash_attn_fwd, flash_attn_fwd_raw, gemm, gemm_raw, w8a16, w8a16_raw)
+from .vocabulary import (Accumulator, CoopMatReduce, DeviceCaps, MatrixA, MatrixB, MatrixShape, SubgroupScope,
+                         WorkgroupScope, bestshape, caps, isbetter, library_shapes, matrix_shapes, supports,
+                         supports_coopmat_perelement, supports_coopmat_reduce, supports_flexible_coopmat_shapes,
+                         supports_tensor_addressing, wggranularity)
+
+# Input seeds: base "LAVA" + 256 * config index + tensor id (A=0, B=1, scale=2; Q=0, K=1, V=2).
+SEED_BASE = 0x4C415641
+
+
+def seed(config: int, tensor: int) -> int:
+    return SEED_BASE + 256 * config + tensor
+
+
+def init() -> None:
+    """Check that device 0 is a gfx950 (raises NoDevice otherwise)."""
+    _lib.call("lava_hip_init")

@@ -1,0 +1,151 @@
+"""The hot-path kernels, called destination-first as a Lava kernel launch is
+(`gemm!(C, A, B)`, like README.md's `vadd!(c, a, b)`), over HIPDeviceArrays or raw
+device addresses.
+
+Every function forwards to one entry point of liblava_hip.so; argument errors
+come back as InvalidArgument / Unsupported without touching the GPU.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+from typing import Optional, Sequence
+
+from . import _lib
+from .device import HIPDeviceArray
+
+_GEMM_ENTRY = {("f16", "f32"): "lava_hip_gemm_f16_f32", ("bf16", "f32"): "lava_hip_gemm_bf16_f32",
+               ("i8", "i32"): "lava_hip_gemm_i8_i32"}
+
+
+def _ld(a: HIPDeviceArray) -> int:
+    """Leading dimension of a 2-D array in its own order."""
+    if len(a.dims) != 2:
+        raise ValueError(f"expected a matrix, got dims {a.dims}")
+    return max(1, a.dims[0] if a.order == "F" else a.dims[1])
+
+
+def gemm_raw(ab: str, acc: str, A: int, B: int, C_: int, M: int, N: int, K: int, lda: int, ldb: int, ldc: int,
+             layout: int, stream: Optional[int] = None) -> None:
+    """C = A * B on raw device addresses; layout bits: A/B/C row-major (1/2/4)."""
+    try:
+        name = _GEMM_ENTRY[(ab, acc)]
+    except KeyError:
+        raise _lib.Unsupported(_lib.ERR_UNSUPPORTED, f"no GEMM for {ab} -> {acc}") from None
+    _lib.call(name, A, B, C_, M, N, K, lda, ldb, ldc, layout, stream)
+
+
+def gemm(C_: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray, stream: Optional[int] = None) -> HIPDeviceArray:
+    """`C = A * B` (muladd(a, b, zero(c)), src/vocabulary/coopmat.jl:196-203) with each
+    operand's own storage order."""
+    if A.dtype != B.dtype:
+        raise ValueError(f"A is {A.dtype}, B is {B.dtype}")
+    M, K = A.dims
+    K2, N = B.dims
+    if K2 != K or C_.dims != (M, N):
+        raise ValueError(f"shape mismatch: A {A.dims}, B {B.dims}, C {C_.dims}")
+    layout = (1 if A.order == "C" else 0) | (2 if B.order == "C" else 0) | (4 if C_.order == "C" else 0)
+    gemm_raw(A.dtype, C_.dtype, A.ptr, B.ptr, C_.ptr, M, N, K, _ld(A), _ld(B), _ld(C_), layout, stream)
+    return C_
+
+
+def coopmat_gemm_tiles(C_: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray,
+                       stream: Optional[int] = None) -> HIPDeviceArray:
+    """The 16x16x16 vocabulary-tile GEMM of docs/src/device.md:81-88 (fp16 -> fp32)."""
+    M, K = A.dims
+    _, N = B.dims
+    layout = (1 if A.order == "C" else 0) | (2 if B.order == "C" else 0) | (4 if C_.order == "C" else 0)
+    _lib.call("lava_hip_coopmat_gemm_f16_tiles", A.ptr, B.ptr, C_.ptr, M, N, K, _ld(A), _ld(B), _ld(C_), layout,
+              stream)
+    return C_
+
+
+def w8a16(Y: HIPDeviceArray, X: HIPDeviceArray, W: HIPDeviceArray, scale: HIPDeviceArray,
+          stream: Optional[int] = None) -> HIPDeviceArray:
+    """Y = (X * float(W)) .* scale[col]: the per-element dequant epilogue
+    (src/device/coopmat_intrinsics.jl:535-628)."""
+    M, K = X.dims
+    K2, N = W.dims
+    if K2 != K or Y.dims != (M, N) or scale.size != N:
+        raise ValueError(f"shape mismatch: X {X.dims}, W {W.dims}, scale {scale.dims}, Y {Y.dims}")
+    layout = (1 if X.order == "C" else 0) | (2 if W.order == "C" else 0) | (4 if Y.order == "C" else 0)
+    _lib.call("lava_hip_gemm_w8a16", X.ptr, W.ptr, scale.ptr, Y.ptr, M, N, K, _ld(X), _ld(W), _ld(Y), layout,
+              stream)
+    return Y
+
+
+def w8a16_raw(X: int, W: int, scale: int, Y: int, M: int, N: int, K: int, ldx: int, ldw: int, ldy: int,
+              layout: int = 7, stream: Optional[int] = None) -> None:
+    _lib.call("lava_hip_gemm_w8a16", X, W, scale, Y, M, N, K, ldx, ldw, ldy, layout, stream)
+
+
+def flash_attn_fwd_raw(Q: int, K: int, V: int, O: int, B: int, H: int, S: int, D: int,
+                       strides: Sequence[int], ostrides: Optional[Sequence[int]] = None,
+                       scale: Optional[float] = None, causal: bool = True, stream: Optional[int] = None) -> None:
+    st = (C.c_int64 * 4)(*strides)
+    ost = (C.c_int64 * 4)(*ostrides) if ostrides is not None else None
+    sc = 1.0 / math.sqrt(D) if scale is None else float(scale)
+    _lib.call("lava_hip_flash_attn_fwd_f16", Q, K, V, O, B, H, S, D, st, ost, sc, int(bool(causal)), stream)
+
+
+def flash_attn_fwd(O: HIPDeviceArray, Q: HIPDeviceArray, K: HIPDeviceArray, V: HIPDeviceArray,
+                   scale: Optional[float] = None, causal: bool = True, stream: Optional[int] = None) -> HIPDeviceArray:
+    """O = softmax(Q K^T * scale + causal mask) V over (E, L, H, B) fp16 arrays, head
+    dimension fastest (src/device/tensor_intrinsics.jl:279-281)."""
+    for t in (Q, K, V, O):
+        if t.dtype != "f16" or len(t.dims) != 4:
+            raise ValueError("Q, K, V, O must be 4-D f16 arrays (E, L, H, B)")
+    if not (Q.dims == K.dims == V.dims == O.dims):
+        raise ValueError("Q, K, V, O must share dims (E, L, H, B)")
+    if Q.order != "F" or K.order != Q.order or V.order != Q.order:
+        raise ValueError("Q, K, V must be column-major (E fastest)")
+    E, L, H, Bn = Q.dims
+    flash_attn_fwd_raw(Q.ptr, K.ptr, V.ptr, O.ptr, Bn, H, L, E, Q.strides(), O.strides(), scale, causal, stream)
+    return O
+
+
+# ---- tile-level vocabulary -------------------------------------------------------
+def coopmat_muladd_16x16x16(ab: str, acc: str, A: int, offA: int, strideA: int, B: int, offB: int, strideB: int,
+                            Cp: int, offC: int, strideC: int, D: int, offD: int, strideD: int, layout: int = 0,
+                            ntiles: int = 1, tile_step: int = 0, stream: Optional[int] = None) -> None:
+    """`copyto!(D, offD, strideD, muladd(a, b, c))` over 1-based offsets and element
+    strides; layout bits 0..3 mark A, B, C, D row-major."""
+    codes = {"f16": _lib.F16, "f32": _lib.F32, "i8": _lib.I8, "i32": _lib.I32, "u8": _lib.U8, "u32": _lib.U32}
+    _lib.call("lava_hip_coopmat_muladd_16x16x16", codes[ab], codes[acc], A, offA, strideA, B, offB, strideB, Cp,
+              offC, strideC, D, offD, strideD, layout, ntiles, tile_step, stream)
+
+
+def coopmat_perelement_rowcol(inp: int, out: int, tile: int, ntiles: int, stream: Optional[int] = None) -> None:
+    _lib.call("lava_hip_coopmat_perelement_rowcol", inp, out, tile, ntiles, stream)
+
+
+def coopmat_perelement_pair(m: int, o: int, out: int, tile: int, ntiles: int, stream: Optional[int] = None) -> None:
+    _lib.call("lava_hip_coopmat_perelement_pair", m, o, out, tile, ntiles, stream)
+
+
+def coopmat_reduce(inp: int, out: int, tile: int, mask: int, combine: str, ntiles: int,
+                   stream: Optional[int] = None) -> None:
+    comb = {"add": _lib.COMBINE_ADD, "max": _lib.COMBINE_MAX, "min": _lib.COMBINE_MIN}[combine]
+    _lib.call("lava_hip_coopmat_reduce", inp, out, tile, mask, comb, ntiles, stream)
+
+
+def coopmat_convert(inp: int, out: int, out_dtype: str, n: int, stream: Optional[int] = None) -> None:
+    code = {"f16": _lib.F16, "bf16": _lib.BF16}[out_dtype]
+    _lib.call("lava_hip_coopmat_convert", inp, out, code, n, stream)
+
+
+def dot4x8(a: int, b: int, y: int, n: int, stream: Optional[int] = None) -> None:
+    _lib.call("lava_hip_dot4x8", a, b, y, n, stream)
+
+
+# ---- seeded inputs on the device ------------------------------------------------------
+def fill_uniform(dst: HIPDeviceArray, seed: int, a: float, b: float, stream: Optional[int] = None) -> None:
+    _lib.call("lava_hip_fill_uniform", dst.ptr, dst.code, dst.size, seed, a, b, stream)
+
+
+def fill_normal(dst: HIPDeviceArray, seed: int, stream: Optional[int] = None) -> None:
+    _lib.call("lava_hip_fill_normal", dst.ptr, dst.code, dst.size, seed, stream)
+
+
+def fill_i8(dst: HIPDeviceArray, seed: int, symmetric: bool = False, stream: Optional[int] = None) -> None:
+    _lib.call("lava_hip_fill_i8", dst.ptr, dst.size, seed, int(bool(symmetric)), stream)

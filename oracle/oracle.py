@@ -1,0 +1,240 @@
+"""CPU oracle for Lava.jl's cooperative-matrix path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this module.  It is the checker, never the thing measured or shipped; the
+product (liblava_hip.so and the lava_hip package) never imports it.
+
+Each function names the reference definition it restates (paths relative to the
+Lava.jl tree); the arithmetic is in oracle/lava_oracle.c (fp64 / exact integer)
+or, for the tile-level definitions, plain numpy here.
+
+Pinning (see tests/test_oracle.py): every function below is checked against an
+independent source -- numpy/torch library routines (matmul, float16/bfloat16
+casts, softmax), closed forms (identity, constant, one-hot inputs), brute force
+on tiny inputs, or the reference's own known-answer definitions.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB = HERE / "liblava_oracle.so"
+
+F16, BF16, F32, I8, U8, I32 = 0, 1, 2, 3, 4, 5
+_CODES = {"f16": F16, "bf16": BF16, "f32": F32, "i8": I8, "u8": U8, "i32": I32}
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile liblava_oracle.so with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", str(HERE), "liblava_oracle.so"], check=True)
+    return LIB
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB.exists():
+            build()
+        L = C.CDLL(str(LIB))
+        vp, i64, u64, u32 = C.c_void_p, C.c_int64, C.c_uint64, C.c_uint32
+        L.oracle_rng_u64.restype = u64
+        L.oracle_rng_u64.argtypes = [u64, u64]
+        L.oracle_f32_to_f16.restype = C.c_uint16
+        L.oracle_f32_to_f16.argtypes = [C.c_float]
+        L.oracle_f32_to_bf16.restype = C.c_uint16
+        L.oracle_f32_to_bf16.argtypes = [C.c_float]
+        L.oracle_f16_to_f32.restype = C.c_float
+        L.oracle_f16_to_f32.argtypes = [C.c_uint16]
+        L.oracle_fill_uniform.argtypes = [vp, C.c_int, i64, u64, C.c_double, C.c_double]
+        L.oracle_fill_normal.argtypes = [vp, C.c_int, i64, u64]
+        L.oracle_fill_i8.argtypes = [vp, i64, u64, C.c_int]
+        L.oracle_gemm_rows.argtypes = [vp, C.c_int, vp, C.c_int, i64, i64, i64, i64, i64, u32, vp, i64, vp]
+        L.oracle_gemm_f32acc.argtypes = [vp, C.c_int, vp, C.c_int, i64, i64, i64, i64, u32, i64, vp]
+        L.oracle_gemm_i8_rows.argtypes = [vp, vp, i64, i64, i64, i64, u32, vp, i64, vp]
+        L.oracle_gemm_u8_rows.argtypes = [vp, vp, i64, i64, i64, i64, u32, vp, i64, vp]
+        L.oracle_w8a16_rows.argtypes = [vp, vp, vp, i64, i64, i64, i64, vp, i64, vp]
+        L.oracle_attn_rows.argtypes = [vp, vp, vp, i64, i64, vp, C.c_double, C.c_int, i64, i64, vp, i64, vp]
+        L.oracle_dot4x8.restype = C.c_int32
+        L.oracle_dot4x8.argtypes = [C.c_uint32, C.c_uint32]
+        L.oracle_dot4x8_array.argtypes = [vp, vp, vp, i64]
+        L.oracle_f32_to_f16_array.argtypes = [vp, vp, i64]
+        L.oracle_f32_to_bf16_array.argtypes = [vp, vp, i64]
+        L.oracle_num_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# ---- generator -------------------------------------------------------------------
+def rng_u64(seed: int, i: int) -> int:
+    return int(lib().oracle_rng_u64(seed, i))
+
+
+def fill_uniform(n: int, dtype: str, seed: int, a: float, b: float) -> np.ndarray:
+    """f16 -> float16 array; bf16 -> uint16 bit patterns; f32 -> float32."""
+    out = np.empty(n, dtype={"f16": np.float16, "bf16": np.uint16, "f32": np.float32}[dtype])
+    lib().oracle_fill_uniform(_p(out), _CODES[dtype], n, seed, a, b)
+    return out
+
+
+def fill_normal(n: int, dtype: str, seed: int) -> np.ndarray:
+    out = np.empty(n, dtype={"f16": np.float16, "bf16": np.uint16, "f32": np.float32}[dtype])
+    lib().oracle_fill_normal(_p(out), _CODES[dtype], n, seed)
+    return out
+
+
+def fill_i8(n: int, seed: int, symmetric: bool = False) -> np.ndarray:
+    out = np.empty(n, dtype=np.int8)
+    lib().oracle_fill_i8(_p(out), n, seed, int(symmetric))
+    return out
+
+
+# ---- conversions ------------------------------------------------------------------------
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_f16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_bf16_array(_p(x), _p(out), x.size)
+    return out
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def decode(a: np.ndarray, dtype: str) -> np.ndarray:
+    """Exact float64 values of an f16/bf16/f32 array."""
+    if dtype == "bf16":
+        return bf16_bits_to_f32(a).astype(np.float64)
+    return np.asarray(a).astype(np.float64)
+
+
+# ---- GEMM -------------------------------------------------------------------------------------
+def gemm_rows(A: np.ndarray, adt: str, B: np.ndarray, bdt: str, M: int, N: int, K: int, lda: int, ldb: int,
+              layout: int, rows) -> np.ndarray:
+    """Rows `rows` of C = A*B in fp64; A and B are flat storage arrays addressed by
+    layout (bit0 A row-major, bit1 B row-major)."""
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    out = np.empty((rows.size, N), dtype=np.float64)
+    A = np.ascontiguousarray(A)
+    B = np.ascontiguousarray(B)
+    lib().oracle_gemm_rows(_p(A), _CODES[adt], _p(B), _CODES[bdt], M, N, K, lda, ldb, layout, _p(rows), rows.size,
+                           _p(out))
+    return out
+
+
+def gemm_f32acc(A: np.ndarray, adt: str, B: np.ndarray, bdt: str, N: int, K: int, lda: int, ldb: int, layout: int,
+                nrows: int) -> np.ndarray:
+    """The CPU baseline: rows [0, nrows) of A*B accumulated in fp32, all host threads."""
+    out = np.empty((nrows, N), dtype=np.float32)
+    A = np.ascontiguousarray(A)
+    B = np.ascontiguousarray(B)
+    lib().oracle_gemm_f32acc(_p(A), _CODES[adt], _p(B), _CODES[bdt], N, K, lda, ldb, layout, nrows, _p(out))
+    return out
+
+
+def gemm_i8_rows(A: np.ndarray, B: np.ndarray, N: int, K: int, lda: int, ldb: int, layout: int, rows) -> np.ndarray:
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    out = np.empty((rows.size, N), dtype=np.int32)
+    lib().oracle_gemm_i8_rows(_p(np.ascontiguousarray(A, dtype=np.int8)), _p(np.ascontiguousarray(B, dtype=np.int8)),
+                              N, K, lda, ldb, layout, _p(rows), rows.size, _p(out))
+    return out
+
+
+def gemm_u8_rows(A: np.ndarray, B: np.ndarray, N: int, K: int, lda: int, ldb: int, layout: int, rows) -> np.ndarray:
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    out = np.empty((rows.size, N), dtype=np.uint32)
+    lib().oracle_gemm_u8_rows(_p(np.ascontiguousarray(A, dtype=np.uint8)),
+                              _p(np.ascontiguousarray(B, dtype=np.uint8)), N, K, lda, ldb, layout, _p(rows),
+                              rows.size, _p(out))
+    return out
+
+
+def w8a16_rows(X: np.ndarray, W: np.ndarray, s: np.ndarray, N: int, K: int, ldx: int, ldw: int, rows) -> np.ndarray:
+    rows = np.ascontiguousarray(rows, dtype=np.int64)
+    out = np.empty((rows.size, N), dtype=np.float64)
+    Xb = np.ascontiguousarray(X, dtype=np.float16).view(np.uint16)
+    sb = np.ascontiguousarray(s, dtype=np.float16).view(np.uint16)
+    lib().oracle_w8a16_rows(_p(Xb), _p(np.ascontiguousarray(W, dtype=np.int8)), _p(sb), N, K, ldx, ldw, _p(rows),
+                            rows.size, _p(out))
+    return out
+
+
+# ---- attention ------------------------------------------------------------------------------------
+def attn_rows(Q: np.ndarray, K: np.ndarray, V: np.ndarray, S: int, D: int, strides, scale: float, causal: bool,
+              b: int, h: int, qrows) -> np.ndarray:
+    """softmax(q K^T * scale + mask) V for query rows `qrows` of head (b, h), fp64.
+    Q/K/V are flat fp16 storage with element (e,l,h,b) at dot((e,l,h,b), strides)."""
+    qrows = np.ascontiguousarray(qrows, dtype=np.int64)
+    st = np.ascontiguousarray(strides, dtype=np.int64)
+    out = np.empty((qrows.size, D), dtype=np.float64)
+    Qb = np.ascontiguousarray(Q, dtype=np.float16).view(np.uint16)
+    Kb = np.ascontiguousarray(K, dtype=np.float16).view(np.uint16)
+    Vb = np.ascontiguousarray(V, dtype=np.float16).view(np.uint16)
+    lib().oracle_attn_rows(_p(Qb), _p(Kb), _p(Vb), S, D, _p(st), scale, int(causal), b, h, _p(qrows), qrows.size,
+                           _p(out))
+    return out
+
+
+# ---- scalar / tile vocabulary -----------------------------------------------------------------------
+def dot4x8(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint32)
+    b = np.ascontiguousarray(b, dtype=np.uint32)
+    out = np.empty(a.shape, dtype=np.int32)
+    lib().oracle_dot4x8_array(_p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def perelement_rowcol(m: np.ndarray) -> np.ndarray:
+    """f(row, col, e) = e * (row + 1) + col, row/col 0-based
+    (test/spirv/test_coopmat_perelement_inline.jl:20), in fp32."""
+    r = np.arange(m.shape[0], dtype=np.float32)[:, None]
+    c = np.arange(m.shape[1], dtype=np.float32)[None, :]
+    return (m.astype(np.float32) * (r + np.float32(1)) + c).astype(np.float32)
+
+
+def perelement_pair(m: np.ndarray, o: np.ndarray) -> np.ndarray:
+    """f(row, col, x, y) = max(x, y) + row - col over corresponding elements
+    (src/device/coopmat_intrinsics.jl:630-678), fp32."""
+    r = np.arange(m.shape[0], dtype=np.float32)[:, None]
+    c = np.arange(m.shape[1], dtype=np.float32)[None, :]
+    return ((np.maximum(m, o).astype(np.float32) + r) - c).astype(np.float32)
+
+
+def reduce_smear(m: np.ndarray, mask: int, combine: str) -> np.ndarray:
+    """coopmat_reduce: combine along rows (mask 1), columns (2) or both (3); the
+    result has m's shape with the value repeated (src/device/coopmat_intrinsics.jl:685-755)."""
+    f = {"add": np.sum, "max": np.max, "min": np.min}[combine]
+    x = m.astype(np.float64)
+    if mask & 1:
+        x = np.broadcast_to(f(x, axis=1, keepdims=True), x.shape)
+    if mask & 2:
+        x = np.broadcast_to(f(x, axis=0, keepdims=True), x.shape)
+    return np.array(x)
+
+
+def rel_frobenius(x: np.ndarray, ref: np.ndarray) -> float:
+    x = np.asarray(x, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    den = np.linalg.norm(ref)
+    return float(np.linalg.norm(x - ref) / (den if den > 0 else 1.0))
+
+
+def num_threads() -> int:
+    return int(lib().oracle_num_threads())

@@ -1,0 +1,69 @@
+"""Shared pytest set-up: paths, the `gpu` marker, and device detection.
+
+CPU tests (`-m "not gpu"`) cover the oracle against golden vectors and closed
+forms, the host mirror of the vocabulary, and the C ABI's exports and argument
+checks.  GPU tests (`-m gpu`) call liblava_hip.so through its C ABI and compare
+with the oracle.  A missing library fails a GPU test; only a missing GPU skips it.
+"""
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+PKG = REPO / "lava.jl_amd"
+for p in (str(REPO), str(PKG)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) and liblava_hip.so")
+
+
+_HAS_GPU = None
+
+
+def has_gpu() -> bool:
+    global _HAS_GPU
+    if _HAS_GPU is None:
+        import lava_hip
+        try:
+            _HAS_GPU = lava_hip.device_count() > 0
+        except FileNotFoundError:
+            raise
+        except Exception:
+            _HAS_GPU = False
+    return _HAS_GPU
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The lava_hip module, initialised on a gfx950; skips only when no GPU exists."""
+    import lava_hip
+    lava_hip.load()   # a missing library is a failure, not a skip
+    if not has_gpu():
+        pytest.skip("no GPU visible")
+    lava_hip.init()
+    return lava_hip
+
+
+@pytest.fixture(scope="session")
+def oracle():
+    from oracle import oracle as o
+    o.lib()
+    return o
+
+
+def announce(msg: str) -> None:
+    """Name the GPU case before running it, so a crash log says which one."""
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(12345)
