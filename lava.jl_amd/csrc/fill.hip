@@ -27,24 +27,26 @@ __device__ __forceinline__ void put(void* dst, int64_t i, float v) {
 
 template <typename T>
 __global__ void fill_uniform_kernel(void* dst, int64_t n, uint64_t seed, double a, double span) {
+    // the definition rounds the product and the sum separately: no fma contraction
+#pragma clang fp contract(off)
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
         const uint64_t k = rng_u64(seed, (uint64_t)i) >> 40;
-        // fma contraction would change the binary64 rounding: keep mul and add separate
-        const double t = __dmul_rn(span, (double)k * 5.9604644775390625e-08);
-        put<T>(dst, i, (float)__dadd_rn(a, t));
+        const double t = span * ((double)k * 5.9604644775390625e-08);
+        put<T>(dst, i, (float)(a + t));
     }
 }
 
 template <typename T>
 __global__ void fill_normal_kernel(void* dst, int64_t n, uint64_t seed) {
+#pragma clang fp contract(off)
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
         const uint64_t z = rng_u64(seed, (uint64_t)i);
         const double u1 = ((double)(z >> 32) + 0.5) * 2.3283064365386963e-10;
         const double u2 = ((double)(z & 0xffffffffull) + 0.5) * 2.3283064365386963e-10;
-        const double r = sqrt(__dmul_rn(-2.0, log(u1)));
-        put<T>(dst, i, (float)__dmul_rn(r, cos(__dmul_rn(6.283185307179586, u2))));
+        const double r = sqrt(-2.0 * log(u1));
+        put<T>(dst, i, (float)(r * cos(6.283185307179586 * u2)));
     }
 }
 

@@ -161,12 +161,14 @@ __global__ void w8a16_generic_kernel(const f16* __restrict__ X, const int8_t* __
     Y[yrow ? r * ldy + c : c * ldy + r] = s * (float)scale[c];
 }
 
-// Per-(device, stream) workspace for the split-K partials and tickets.  Tickets
-// are zeroed once when the buffer is created and returned to zero by the
-// workgroup that consumes them.
+// Per-(device, stream) workspace for the split-K partials and tickets, laid out
+// as [tickets | partials] so the tickets stay at offset 0 whatever the problem
+// size.  Tickets are zeroed when the buffer is created and returned to zero by
+// the workgroup that consumes them, so every later call finds them at zero.
 struct W8Workspace {
     void* buf = nullptr;
-    size_t bytes = 0;
+    size_t ticket_bytes = 0;
+    size_t partial_bytes = 0;
 };
 static std::mutex g_ws_mutex;
 static std::map<std::pair<int, void*>, W8Workspace> g_ws;
@@ -176,26 +178,27 @@ static int get_workspace(void* stream, size_t partial_bytes, size_t ticket_bytes
     LAVA_HIP_TRY(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     W8Workspace& ws = g_ws[{dev, stream}];
-    const size_t need = partial_bytes + ticket_bytes;
-    if (ws.bytes < need) {
+    if (ws.ticket_bytes < ticket_bytes || ws.partial_bytes < partial_bytes) {
+        const size_t tb = ((ticket_bytes > ws.ticket_bytes ? ticket_bytes : ws.ticket_bytes) + 255) / 256 * 256;
+        const size_t pb = partial_bytes > ws.partial_bytes ? partial_bytes : ws.partial_bytes;
         if (ws.buf) {
             LAVA_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
             LAVA_HIP_TRY(hipFree(ws.buf));
-            ws.buf = nullptr;
-            ws.bytes = 0;
+            ws = W8Workspace{};
         }
         void* p = nullptr;
-        LAVA_HIP_TRY(hipMalloc(&p, need));
-        int rc = lava_hip_fill_bytes(static_cast<char*>(p) + partial_bytes, 0, ticket_bytes, stream);
+        LAVA_HIP_TRY(hipMalloc(&p, tb + pb));
+        int rc = lava_hip_fill_bytes(p, 0, tb, stream);
         if (rc != LAVA_HIP_OK) {
             (void)hipFree(p);
             return rc;
         }
         ws.buf = p;
-        ws.bytes = need;
+        ws.ticket_bytes = tb;
+        ws.partial_bytes = pb;
     }
-    *partial = static_cast<float*>(ws.buf);
-    *tickets = reinterpret_cast<int*>(static_cast<char*>(ws.buf) + partial_bytes);
+    *tickets = static_cast<int*>(ws.buf);
+    *partial = reinterpret_cast<float*>(static_cast<char*>(ws.buf) + ws.ticket_bytes);
     return LAVA_HIP_OK;
 }
 

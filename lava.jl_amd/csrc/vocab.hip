@@ -63,6 +63,8 @@ __global__ void __launch_bounds__(64) muladd_tile_u8_kernel(const uint8_t* A, in
 // which depends on both indices and is not symmetric under swapping them.
 struct RowCol {
     __device__ float operator()(uint32_t row, uint32_t col, float e) const {
+        // two roundings, as the Julia callback computes it (no fused multiply-add)
+#pragma clang fp contract(off)
         return e * (float)(row + 1u) + (float)col;
     }
 };
