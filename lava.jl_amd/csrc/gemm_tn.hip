@@ -6,21 +6,24 @@
 // same loop at workgroup scope) laid out for CDNA4:
 //
 //  * one 256 x 256 tile of C per workgroup of 4 wavefronts (one per SIMD), each
-//    wavefront owning a 128 x 128 sub-tile = 8 x 8 MFMA 16x16 accumulators
-//    (256 fp32 registers per lane);
+//    wavefront owning a 128 x 128 sub-tile = 4 x 4 MFMA 32x32 accumulators
+//    (256 fp32 registers per lane, all in AGPRs);
 //  * K advances 128 bytes at a time (64 bf16/fp16 or 128 int8): A and B slices of
 //    256 rows x 128 bytes each, double-buffered in LDS (2 x 64 KB);
-//  * global -> LDS with global_load_lds_dwordx4: each lane moves 16 bytes straight
-//    into LDS, no register staging.  One wavefront instruction fills 1 KB = 8 LDS
+//  * global -> LDS with buffer_load_dwordx4 ... lds: each lane moves 16 bytes
+//    straight into LDS, no register staging, addressed by a buffer resource plus a
+//    32-bit lane offset (the wave-uniform parts in soffset).  One wavefront instruction fills 1 KB = 8 LDS
 //    rows; lane l writes row l / 8, 16-byte slot l % 8.  The slot a logical 16-byte
 //    chunk c of row r lands in is c ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 1),
 //    chosen by which global chunk each lane fetches, so the fragment reads
 //    (16 consecutive rows, one chunk column) spread over all banks;
-//  * fragments are 16 bytes per lane (ds_read_b128), one MFMA 16x16x32 (16-bit)
-//    or 16x16x64 (int8) each;
+//  * fragments are 16 bytes per lane (ds_read_b128), one MFMA 32x32x16 (16-bit)
+//    or 32x32x32 (int8) each; 4 sub-steps of 32 bytes of K per stage, each 16
+//    MFMAs, with the next sub-step's fragments read underneath (double-buffered
+//    fragment registers, 64 VGPRs) and the next stage's DMA issued at sub-step 0;
 //  * the MFMA's A operand is the B slice and its B operand the A slice, so each
-//    lane's accumulator holds 4 consecutive columns of one row of C: the epilogue
-//    is one 16-byte store per lane per accumulator;
+//    lane's accumulator holds runs of 4 consecutive columns of one row of C: the
+//    epilogue is 16-byte stores;
 //  * workgroups are renumbered XCD by XCD (xcd_tile) so that the tiles one XCD
 //    runs together share rows of A and columns of B in its L2.
 #include <hip/hip_runtime.h>
@@ -35,17 +38,44 @@ constexpr int TN_TILE = 256;    // rows of A / columns of B per workgroup
 constexpr int TN_KB = 128;      // bytes of K per stage
 constexpr int TN_SLICE = TN_TILE * TN_KB;  // 32 KB
 
-typedef __attribute__((address_space(3))) void lds_void;
+typedef int v4i __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ void dma16(const void* gsrc, lds_void* ldst) {
-    __builtin_amdgcn_global_load_lds(gsrc, ldst, 16, 0, 0);
+// Buffer resource over [base, base + bytes): untyped dword loads (gfx9 word 3:
+// DATA_FORMAT 32, stride 0).  Offsets past `bytes` read zero instead of faulting.
+__device__ __forceinline__ v4i make_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    v4i r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16 bytes per lane from rsrc + voffset + soffset straight into LDS at
+// lds + 16 * lane (buffer_load_dwordx4 ... lds, LDS base in m0).  Written as inline
+// asm so that the compiler does not treat it as a store to every LDS byte: its
+// waitcnt pass would otherwise wait for the load before the next LDS read of the
+// *other* stage.  Completion is waited for explicitly (s_waitcnt vmcnt(0)) before
+// the barrier that publishes the stage.  m0 is a reserved register nothing else in
+// these kernels uses, so it is set here and not declared as a clobber.
+__device__ __forceinline__ void dma16(const v4i& rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory");
 }
 
 template <typename T>
 __global__ void __launch_bounds__(256, 1)
     gemm_tn_kernel(const T* __restrict__ A, const T* __restrict__ B, typename Mfma16<T>::acc_elem* __restrict__ C,
                    int tiles_m, int tiles_n, int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc) {
-    using AccV = typename Mfma16<T>::acc_t;
+    using AccV = typename Mfma32<T>::acc_t;
+    typedef typename Mfma16<T>::acc_elem Acc;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TN_SLICE];  // [stage][A,B][row][128 B]
 
     const int lane = threadIdx.x & 63;
@@ -59,77 +89,140 @@ __global__ void __launch_bounds__(256, 1)
     const int lr = lane >> 3;
     const int c_even = (lane & 7) ^ lr;
     const int c_odd = c_even ^ 1;
-    const char* a_src = reinterpret_cast<const char*>(A) + ((int64_t)tm * TN_TILE + 64 * w + lr) * lda_b;
-    const char* b_src = reinterpret_cast<const char*>(B) + ((int64_t)tn * TN_TILE + 64 * w + lr) * ldb_b;
-    const int64_t a_step = 8 * lda_b, b_step = 8 * ldb_b;
+    // A slice rows tm*256 .. +256 and B slice rows tn*256 .. +256 as buffer resources;
+    // each lane keeps one 32-bit row offset per chunk parity, the row step (8 i rows)
+    // and the k offset are wave-uniform and travel in soffset.
+    const v4i rs_a =
+        make_rsrc(reinterpret_cast<const char*>(A) + (int64_t)tm * TN_TILE * lda_b, (uint32_t)(TN_TILE * lda_b));
+    const v4i rs_b =
+        make_rsrc(reinterpret_cast<const char*>(B) + (int64_t)tn * TN_TILE * ldb_b, (uint32_t)(TN_TILE * ldb_b));
+    const uint32_t a_row = (uint32_t)((64 * w + lr) * lda_b), b_row = (uint32_t)((64 * w + lr) * ldb_b);
+    const uint32_t a_off[2] = {a_row + 16u * c_even, a_row + 16u * c_odd};
+    const uint32_t b_off[2] = {b_row + 16u * c_even, b_row + 16u * c_odd};
+    const uint32_t a_step = (uint32_t)(8 * lda_b), b_step = (uint32_t)(8 * ldb_b);
+    const uint32_t lds0 = lds_addr(smem) + w * 64 * TN_KB;
 
-    auto issue = [&](int stage, int kt) {
-        uint8_t* a_dst = smem + stage * 2 * TN_SLICE + w * 64 * TN_KB;
-        uint8_t* b_dst = a_dst + TN_SLICE;
-        const int64_t kofs = (int64_t)kt * TN_KB;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = (i & 1) ? c_odd : c_even;
-            dma16(a_src + i * a_step + kofs + c * 16, (lds_void*)(a_dst + i * 1024));
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int c = (i & 1) ? c_odd : c_even;
-            dma16(b_src + i * b_step + kofs + c * 16, (lds_void*)(b_dst + i * 1024));
-        }
+    // DMA load q (0..15) of a k-tile into `stage`: q < 8 are A rows 8q.., q >= 8 B rows.
+    auto dma = [&](int q, int stage, uint32_t kofs) {
+        const int i = q & 7;
+        const uint32_t dst = lds0 + stage * 2 * TN_SLICE + (q >> 3) * TN_SLICE + i * 1024;
+        if (q < 8) dma16(rs_a, a_off[i & 1], i * a_step + kofs, dst);
+        else dma16(rs_b, b_off[i & 1], i * b_step + kofs, dst);
     };
 
-    // ---- fragment reads: row = base + 16 t + lane % 16; chunk = 4 s + lane / 16.
-    // swz(row) only depends on lane % 16, so every read of a lane uses one slot per s.
+    // ---- fragments: 32x32 MFMA operands, 16 bytes per lane.  Operand row = base +
+    // 32 t + lane % 32, chunk = 2 s + lane / 32 for k sub-step s (32 bytes of K).  swz(row)
+    // only depends on lane % 16 (bases are multiples of 16), so each sub-step reads one
+    // slot per lane.
     const int wm = w >> 1, wn = w & 1;
     const int swz = (lane & 7) ^ ((lane >> 3) & 1);
-    const int rd_row = lane & 15;
-    const int slot0 = (0 + (lane >> 4)) ^ swz;
-    const int slot1 = (4 + (lane >> 4)) ^ swz;
-    const int a_rd = (wm * 128 + rd_row) * TN_KB;
-    const int b_rd = TN_SLICE + (wn * 128 + rd_row) * TN_KB;
+    const int h = lane >> 5;
+    const int a_rd = (wm * 128 + (lane & 31)) * TN_KB;
+    const int b_rd = TN_SLICE + (wn * 128 + (lane & 31)) * TN_KB;
 
-    AccV acc[8][8];
+    AccV acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = AccV{0, 0, 0, 0};
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-    issue(0, 0);
+    struct Frags {
+        uint4 a[4], b[4];
+    };
+    auto read_frags = [&](Frags& f, const uint8_t* base, int s) {
+        const int slot = ((2 * s + h) ^ swz) * 16;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            f.b[t] = *reinterpret_cast<const uint4*>(base + b_rd + t * 32 * TN_KB + slot);
+            f.a[t] = *reinterpret_cast<const uint4*>(base + a_rd + t * 32 * TN_KB + slot);
+        }
+    };
+    // MFMA A operand = B slice (rows are columns n of C), B operand = A slice (rows m):
+    // the accumulator then holds C^T, 4 consecutive n per lane and register group.
+    auto mma = [&](const Frags& f, int i0, int i1) {
+#pragma unroll
+        for (int i = i0; i < i1; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = Mfma32<T>::run(f.b[j], f.a[i], acc[i][j]);
+    };
+
+    // Per k-tile (128 bytes of K = 4 sub-steps), branch-free so the interleave holds:
+    //   s = 0..2: 16 MFMAs on the current fragments while the next sub-step's 8 LDS
+    //             reads (and, at s = 0, the 16 DMA loads of the next tile) issue;
+    //   s = 3:    8 MFMAs; wait for this wave's DMA; barrier; then the next tile's
+    //             s = 0 reads under the last 8 MFMAs.
+    // On the last tile the "next" tile re-fetches the current one into the idle stage.
+    {
+#pragma unroll
+        for (int q = 0; q < 16; ++q) dma(q, 0, 0);
+    }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    Frags fa, fb;
+    read_frags(fa, smem, 0);
 
     for (int kt = 0; kt < ktiles; ++kt) {
-        const int stage = kt & 1;
-        if (kt + 1 < ktiles) issue(stage ^ 1, kt + 1);
-        const uint8_t* base = smem + stage * 2 * TN_SLICE;
+        const int st = kt & 1;
+        const uint8_t* base = smem + st * 2 * TN_SLICE;
+        const uint8_t* next = smem + (st ^ 1) * 2 * TN_SLICE;
+        const uint32_t kofs_next = (uint32_t)(kt + 1 < ktiles ? kt + 1 : kt) * TN_KB;
+        // s = 0: LDS reads of s = 1, then 16 MFMAs with one DMA load of the next tile after each
+        read_frags(fb, base, 1);
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const int slot = s ? slot1 : slot0;
-            uint4 af[8], bf[8];
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                af[t] = *reinterpret_cast<const uint4*>(base + a_rd + t * 16 * TN_KB + slot * 16);
-                bf[t] = *reinterpret_cast<const uint4*>(base + b_rd + t * 16 * TN_KB + slot * 16);
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] = Mfma32<T>::run(fa.b[j], fa.a[i], acc[i][j]);
+                dma(4 * i + j, st ^ 1, kofs_next);
             }
+        // s = 1, 2: next sub-step's LDS reads under 16 MFMAs
+        read_frags(fa, base, 2);
+        mma(fb, 0, 4);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc[i][j] = Mfma16<T>::run(bf[j], af[i], acc[i][j]);
+        for (int t = 0; t < 8; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(fb, base, 3);
+        mma(fa, 0, 4);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // s = 3: half the MFMAs, publish the next stage, its first reads under the other half
+        mma(fb, 0, 2);
+        __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(fa, next, 0);
+        mma(fb, 2, 4);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 3);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 3);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- epilogue: acc[i][j] lane holds C[m][n .. n + 3] with
-    // m = tile row + 128 wm + 16 i + lane % 16, n = tile col + 128 wn + 16 j + 4 (lane / 16).
-    typedef typename Mfma16<T>::acc_elem Acc;
-    Acc* crow = C + ((int64_t)tm * TN_TILE + wm * 128 + (lane & 15)) * ldc + (int64_t)tn * TN_TILE + wn * 128 +
-                4 * (lane >> 4);
+    // ---- epilogue: acc[i][j] register r of lane l is C[m][n] with
+    // m = tile row + 128 wm + 32 i + l % 32, n = tile col + 128 wn + 32 j + 8 (r / 4) + 4 (l / 32) + r % 4.
+    Acc* crow = C + ((int64_t)tm * TN_TILE + wm * 128 + (lane & 31)) * ldc + (int64_t)tn * TN_TILE + wn * 128 + 4 * h;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) *reinterpret_cast<AccV*>(crow + (int64_t)i * 16 * ldc + j * 16) = acc[i][j];
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                typedef Acc Acc4 __attribute__((ext_vector_type(4)));
+                const Acc4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                *reinterpret_cast<Acc4*>(crow + (int64_t)i * 32 * ldc + j * 32 + 8 * g) = v;
+            }
 }
 
 template <typename T>
@@ -140,6 +233,10 @@ bool tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, in
     if (M % TN_TILE || N % TN_TILE || K % ke) return false;
     if ((M / TN_TILE) * (N / TN_TILE) > 0x7fffffff || K / ke > 0x7fffffff) return false;
     if ((lda * (int64_t)sizeof(T)) % 16 || (ldb * (int64_t)sizeof(T)) % 16 || ldc % 4) return false;
+    // buffer offsets are 32-bit: a 256-row slab of A or B must span < 2 GiB
+    if ((int64_t)TN_TILE * lda * (int64_t)sizeof(T) >= ((int64_t)1 << 31) ||
+        (int64_t)TN_TILE * ldb * (int64_t)sizeof(T) >= ((int64_t)1 << 31))
+        return false;
     if (!aligned(A, 16) || !aligned(B, 16) || !aligned(C, 16)) return false;
     return true;
 }
