@@ -22,8 +22,8 @@
 //    MFMAs, with the next sub-step's fragments read underneath (double-buffered
 //    fragment registers, 64 VGPRs) and the next stage's DMA issued at sub-step 0;
 //  * the MFMA's A operand is the B slice and its B operand the A slice, so each
-//    lane's accumulator holds runs of 4 consecutive columns of one row of C: the
-//    epilogue is 16-byte stores;
+//    lane's accumulator holds runs of 4 consecutive columns of one row of C; the
+//    epilogue stages them through LDS and stores whole 512-byte row runs;
 //  * workgroups are renumbered XCD by XCD (xcd_tile) so that the tiles one XCD
 //    runs together share rows of A and columns of B in its L2.
 #include <hip/hip_runtime.h>
@@ -197,7 +197,7 @@ __global__ void __launch_bounds__(256, 1)
         // s = 3: half the MFMAs, publish the next stage, its first reads under the other half
         mma(fb, 0, 2);
         __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's part of the next tile landed
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         read_frags(fa, next, 0);
@@ -210,19 +210,40 @@ __global__ void __launch_bounds__(256, 1)
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- epilogue: acc[i][j] register r of lane l is C[m][n] with
-    // m = tile row + 128 wm + 32 i + l % 32, n = tile col + 128 wn + 32 j + 8 (r / 4) + 4 (l / 32) + r % 4.
-    Acc* crow = C + ((int64_t)tm * TN_TILE + wm * 128 + (lane & 31)) * ldc + (int64_t)tn * TN_TILE + wn * 128 + 4 * h;
+    // ---- epilogue through LDS, so that global stores are whole 512-byte row runs.
+    // acc[i][j] register r of lane l is C[m][n] with m = 128 wm + 32 i + l % 32 and
+    // n = 128 wn + 32 j + 8 (r / 4) + 4 (l / 32) + r % 4 within the tile.  Each wave
+    // stages 32 rows x 128 columns at a time (one i) in its own 16.5 KB of the idle
+    // stage buffers (4 waves: 66 KB of the 128 KB), rows padded to 528 bytes so the
+    // 32 rows of one column group land on distinct banks; then reads whole rows back:
+    // lanes 0..31 and 32..63 each cover one 512-byte row per instruction.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    constexpr int EP_PITCH = 128 * 4 + 16;
+    const int rr = lane & 31;
+    uint8_t* ep = smem + w * (32 * EP_PITCH);
+    typedef Acc Acc4 __attribute__((ext_vector_type(4)));
+    Acc* cbase = C + ((int64_t)tm * TN_TILE + wm * 128) * ldc + (int64_t)tn * TN_TILE + wn * 128;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                typedef Acc Acc4 __attribute__((ext_vector_type(4)));
                 const Acc4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                *reinterpret_cast<Acc4*>(crow + (int64_t)i * 32 * ldc + j * 32 + 8 * g) = v;
+                *reinterpret_cast<Acc4*>(ep + rr * EP_PITCH + (32 * j + 8 * g + 4 * h) * 4) = v;
             }
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's staged rows are in LDS
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const int row = 2 * t + h;                       // 0..31 of this i
+            const Acc4 v = *reinterpret_cast<const Acc4*>(ep + row * EP_PITCH + rr * 16);
+            *reinterpret_cast<Acc4*>(cbase + (int64_t)(32 * i + row) * ldc + 4 * rr) = v;
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next i overwrites
+        __builtin_amdgcn_wave_barrier();
+    }
 }
 
 template <typename T>
