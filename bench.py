@@ -150,9 +150,12 @@ def cpu_baseline_gemm(n=8192, budget_s=12.0):
     A = o.fill_uniform(max_rows * n, "bf16", 0x4C415641 + 256, -1.0, 1.0)   # the first rows of A
     B = o.fill_uniform(n * n, "bf16", 0x4C415641 + 257, -1.0, 1.0)    # B column-major, n x n
     t0 = time.perf_counter()
-    o.gemm_f32acc(A, "bf16", B, "bf16", n, n, n, n, 1, 4)
-    probe = time.perf_counter() - t0
-    rows = int(max(4, min(max_rows, 4 * budget_s / max(probe, 1e-3))))
+    o.gemm_f32acc(A, "bf16", B, "bf16", n, n, n, n, 1, 0)          # decoding B alone
+    t_decode = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    o.gemm_f32acc(A, "bf16", B, "bf16", n, n, n, n, 1, 64)
+    per_row = max(time.perf_counter() - t0 - t_decode, 1e-4) / 64
+    rows = int(max(16, min(max_rows, (budget_s - t_decode) / per_row)))
     t0 = time.perf_counter()
     o.gemm_f32acc(A, "bf16", B, "bf16", n, n, n, n, 1, rows)
     dt = time.perf_counter() - t0
@@ -169,7 +172,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline",
-                    choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096"])
+                    choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
+                             "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -241,6 +245,20 @@ def main():
                     "dtype": "f16", "config": {"workload": "fp16 GEMM 256^3, A and B row-major (BASELINE configs[0])"},
                     "kernel_ms": round(kms, 5),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
+
+    elif args.workload == "copy":
+        # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain 1 GiB device copy
+        nbytes = 1 << 30
+        src = lh.HIPDeviceArray("u8", (nbytes,))
+        dst = lh.HIPDeviceArray("u8", (nbytes,))
+        src.fill_bytes(1)
+        lh.synchronize()
+        kms, wms = timed(lh, lambda: lh._lib.call("lava_hip_memcpy_d2d", dst.ptr, src.ptr, nbytes, stream), K, W,
+                         stream)
+        out.update({"value": round(2 * nbytes / (kms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 4),
+                    "dtype": "u8", "config": {"workload": "device copy of 1 GiB (read + write bytes)"},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("hbm", 2 * nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s", 2 * nbytes)})
 
     if args.workload in ("headline", "gemm_bf16") and not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_gemm()

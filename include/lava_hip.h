@@ -81,6 +81,7 @@ int lava_hip_malloc(void** ptr, size_t bytes);
 int lava_hip_free(void* ptr);
 int lava_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int lava_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+/* Device-to-device copy by a kernel (graph-capture safe), asynchronous on `stream`. */
 int lava_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 /* Byte fill by a kernel (not hipMemsetAsync), so it is safe under graph capture. */
 int lava_hip_fill_bytes(void* dst, uint8_t value, size_t bytes, void* stream);

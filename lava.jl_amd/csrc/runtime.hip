@@ -56,6 +56,23 @@ __global__ void fill_bytes_kernel(uint8_t* __restrict__ dst, uint8_t value, size
     for (size_t b = head + nv * 16 + i; b < n; b += stride) dst[b] = value;
 }
 
+// Device-to-device copy as a kernel (not an SDMA transfer): safe under graph
+// capture and visible to the shader counters.  16-byte moves when both ends are
+// 16-byte aligned, bytes otherwise.
+__global__ void copy_bytes_kernel(uint8_t* __restrict__ dst, const uint8_t* __restrict__ src, size_t n) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const size_t i0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if ((((uintptr_t)dst | (uintptr_t)src) & 15) == 0) {
+        const size_t nv = n / 16;
+        const uint4* s4 = reinterpret_cast<const uint4*>(src);
+        uint4* d4 = reinterpret_cast<uint4*>(dst);
+        for (size_t v = i0; v < nv; v += stride) d4[v] = s4[v];
+        for (size_t b = nv * 16 + i0; b < n; b += stride) dst[b] = src[b];
+    } else {
+        for (size_t b = i0; b < n; b += stride) dst[b] = src[b];
+    }
+}
+
 }  // namespace lava
 
 using namespace lava;
@@ -137,7 +154,12 @@ int lava_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
 int lava_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
     if (bytes == 0) return LAVA_HIP_OK;
     LAVA_ARG(dst != nullptr && src != nullptr, "memcpy_d2d: null pointer");
-    LAVA_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, as_stream(stream)));
+    size_t blocks = (bytes / 16 + 255) / 256;
+    if (blocks < 1) blocks = 1;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(copy_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
+                       static_cast<uint8_t*>(dst), static_cast<const uint8_t*>(src), bytes);
+    LAVA_LAUNCH_CHECK("copy_bytes_kernel");
     return LAVA_HIP_OK;
 }
 
