@@ -241,6 +241,287 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FaParams p) {
         }
 }
 
+// ---------------------------------------------------------------------------
+// Version 3 (the fast path): 8 wavefronts x 32 queries = 256 queries per
+// workgroup; K and V blocks of 64 keys move global -> LDS by buffer_load ... lds,
+// so no VGPRs stage them and each block is loaded once per 256 queries; V^T
+// operands come from the row-major V tile through ds_read_b64_tr_b16.
+//
+// Ping-pong schedule.  Each wavefront alternates an MFMA phase (O += V^T P^T for
+// the previous block, then S^T = K Q^T for this one: 32 MFMAs) and a softmax
+// phase (VALU only), with a workgroup barrier after every phase.  Wavefronts 4-7
+// start one phase late, so each SIMD (holding wavefronts w and w + 4) always has
+// one wavefront in its MFMA phase and the other in its softmax phase, and the
+// matrix core and the VALU work at the same time instead of taking turns.
+//
+// K and V have three LDS stages each.  The MFMA phase of iteration kb issues the
+// DMA of K block kb + 2 and V block kb + 1 (4 instructions per wavefront) and each
+// phase ends with s_waitcnt vmcnt(4), so a wavefront's DMAs have landed by the end
+// of its next MFMA phase; the barrier after it publishes them.  The stage a DMA
+// overwrites was last read by the late wavefronts one phase before it is issued.
+//
+// LDS layout: K [64 keys][256 B] and V [64 keys][256 B] per stage, 16-byte chunks
+// XOR-swizzled -- K by key % 16 (a fragment read is 32 keys x one chunk), V by
+// 4 (key % 4) (a transposing read is 4 keys x 32 bytes per 16-lane group) -- so
+// neither read pattern has bank conflicts.
+//
+// ds_read_b64_tr_b16: in a 16-lane group, output lane i value j is the 16-bit word
+// at (address of source lane 4 j + i / 4) + 2 (i % 4).  Source lane 4 jj + q points
+// at V[key0 + jj][d0 + 4 q], so output lane i receives V[key0 .. key0 + 3][d0 + i]:
+// four keys of one head-dimension column, the k-slots of the V^T operand.
+//
+// Lazy rescaling: the running maximum moves (and O, L are rescaled) only when a
+// block's maximum exceeds it by more than 2^8; P = exp2(s - m) then stays <= 256,
+// exact enough in fp16, and O / L is unchanged in exact arithmetic.
+constexpr int F3_WAVES = 8;
+constexpr int F3_BQ = 32 * F3_WAVES;        // 256 queries per workgroup
+constexpr int F3_BK = 64;
+constexpr int F3_STAGES = 3;
+constexpr int F3_TILE = F3_BK * FA_D * 2;   // 16 KB: one K or V block
+constexpr float F3_RESCALE = 8.0f;
+
+typedef int f3_v4i __attribute__((ext_vector_type(4)));
+typedef short f3_s16x4 __attribute__((ext_vector_type(4)));
+typedef short f3_s16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f3_v4i f3_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    f3_v4i r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
+    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+// 16 bytes per lane from rsrc + voffset + soffset into LDS at lds + 16 * lane.
+// Inline asm so that the compiler does not wait for it before unrelated LDS
+// reads; completion is waited for explicitly (s_waitcnt vmcnt) before the barrier
+// that publishes a stage.  m0 is reserved and set here.
+__device__ __forceinline__ void f3_dma16(const f3_v4i& rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory");
+}
+
+__device__ __forceinline__ uint32_t f3_lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+__device__ __forceinline__ f3_s16x4 f3_read_tr(const uint8_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) f3_s16x4*)(const __attribute__((address_space(3))) uint8_t*)p);
+}
+
+// All waits for the DMAs of the phase before last, then the workgroup barrier.
+__device__ __forceinline__ void f3_phase_end() {
+    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    __syncthreads();
+}
+
+template <bool CAUSAL>
+__global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p) {
+    __shared__ __attribute__((aligned(1024))) uint8_t kbuf[F3_STAGES][F3_TILE];   // [stage][key][256 B]
+    __shared__ __attribute__((aligned(1024))) uint8_t vbuf[F3_STAGES][F3_TILE];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool late = w >= F3_WAVES / 2;        // one phase behind its SIMD partner w - 4
+    const int nqb = p.S / F3_BQ;
+    const int nbh = p.H * p.B;
+    int bid = blockIdx.x;
+    const int total = nqb * nbh;
+    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+    const int bh = bid / nqb;
+    const int qb = CAUSAL ? (nqb - 1 - bid % nqb) : bid % nqb;
+    const int hh = bh % p.H, bb = bh / p.H;
+    const int64_t head = (int64_t)hh * p.sh + (int64_t)bb * p.sb;
+    f16* Ob = p.O + (int64_t)hh * p.osh + (int64_t)bb * p.osb;
+
+    const int q0 = qb * F3_BQ + w * 32;         // this wave's first query
+    const int r32 = lane & 31, h = lane >> 5;
+    const int my_q = q0 + r32;
+
+    // Q^T as B operand: lane (query my_q, half h) holds d = 16 ks + 8 h + [0, 8)
+    f16x8 qf[8];
+    {
+        const f16* qrow = p.Q + head + (int64_t)my_q * p.sl + 8 * h;
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
+    }
+
+    // ---- LDS-DMA: wave w moves rows [8 w, 8 w + 8) of a K or V tile in two
+    // instructions: instruction i covers rows 8 w + 4 i + lane / 16, physical chunk lane % 16.
+    const uint32_t row_bytes = (uint32_t)(p.sl * 2);
+    const f3_v4i rk = f3_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
+    const f3_v4i rv = f3_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
+    uint32_t voff_k[2], voff_v[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int row = 8 * w + 4 * i + (lane >> 4);
+        const int pc = lane & 15;
+        voff_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ (row & 15));
+        voff_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ (4 * (row & 3)));
+    }
+    const uint32_t lds_k = f3_lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * 256;
+    const uint32_t lds_v = f3_lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * 256;
+    const int nkb = CAUSAL ? (qb * F3_BQ + F3_BQ) / F3_BK : p.S / F3_BK;
+    // block j -> stage j % F3_STAGES; blocks past the end re-read the last one so
+    // that every MFMA phase issues the same number of DMAs (the vmcnt accounting)
+    auto issue = [&](const f3_v4i& rsrc, const uint32_t* voff, uint32_t lds, int j) {
+        const int src = j < nkb ? j : nkb - 1;
+        const uint32_t soff = (uint32_t)src * F3_BK * row_bytes;
+        const uint32_t dst = lds + (uint32_t)(j % F3_STAGES) * F3_TILE;
+        f3_dma16(rsrc, voff[0], soff, dst);
+        f3_dma16(rsrc, voff[1], soff, dst + 1024);
+    };
+
+    // K fragment (kt, ks): row 32 kt + r32, logical chunk 2 ks + h, stored at chunk ^ (row % 16)
+    int k_off[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) k_off[ks] = r32 * 256 + (((2 * ks + h) ^ (lane & 15)) << 4);
+    // V^T fragment (dt, kk = 32 kt + 16 ks, read t = 0/1): source lane jj = (lane % 16) / 4,
+    // q = lane % 4, dh = (lane / 16) % 2 addresses V[kk + 8 t + 4 h + jj][32 dt + 16 dh + 4 q],
+    // logical chunk 4 dt + 2 dh + q / 2 stored at chunk ^ 4 jj (jj = key % 4 as kk % 8 == 0).
+    int v_off[4];
+    {
+        const int jj = (lane & 15) >> 2, q = lane & 3, dh = (lane >> 4) & 1;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            v_off[dt] = (4 * h + jj) * 256 + (((4 * (dt ^ jj)) + 2 * dh + (q >> 1)) << 4) + ((q & 1) << 3);
+    }
+
+    f32x16 o[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
+    float m_run = -INFINITY;   // running max of the scaled scores (log2 units)
+    float l_run = 0.f;         // this lane's partial row sum
+    const float c = p.scale_log2;
+    f32x16 st[2];              // S^T of the current block: st[kt] register r = key 32 kt + 8 (r / 4) + 4 h + r % 4
+    f16x8 pf[2][2];            // P^T of the previous block, B operand [kt][ks]: keys 32 kt + 16 ks + 8 (i / 4) + 4 h + i % 4
+
+    issue(rk, voff_k, lds_k, 0);
+    // Consume Q here so the compiler's own wait for its loads happens once, before
+    // the loop, instead of as vmcnt waits inside it (which would also cover the
+    // DMAs issued in the loop, since it does not count those).
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        const uint4 u = __builtin_bit_cast(uint4, qf[ks]);
+        asm volatile("" ::"v"(u.x), "v"(u.y), "v"(u.z), "v"(u.w));
+    }
+    issue(rk, voff_k, lds_k, 1);
+    issue(rv, voff_v, lds_v, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (late) __builtin_amdgcn_s_barrier();
+
+    for (int kb = 0; kb <= nkb; ++kb) {
+        // ================= MFMA phase =================
+        issue(rk, voff_k, lds_k, kb + 2);
+        issue(rv, voff_v, lds_v, kb + 1);
+        if (kb > 0 && (!CAUSAL || (kb - 1) * F3_BK <= q0 + 31)) {
+            // O^T += V^T P^T for block kb - 1
+            const uint8_t* vbase = &vbuf[(kb - 1) % F3_STAGES][0];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt) {
+                        const int kk = 32 * kt + 16 * ks;
+                        const f3_s16x4 lo = f3_read_tr(vbase + v_off[dt] + kk * 256);
+                        const f3_s16x4 hi = f3_read_tr(vbase + v_off[dt] + (kk + 8) * 256);
+                        const f3_s16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf), pf[kt][ks],
+                                                                       o[dt], 0, 0, 0);
+                    }
+        }
+        const bool active = kb < nkb && (!CAUSAL || kb * F3_BK <= q0 + 31);
+        if (active) {
+            // S^T = K Q^T for block kb
+            const uint8_t* kbase = &kbuf[kb % F3_STAGES][0];
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) st[kt][r] = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt) {
+                    const f16x8 kf = *reinterpret_cast<const f16x8*>(kbase + k_off[ks] + kt * 32 * 256);
+                    st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], st[kt], 0, 0, 0);
+                }
+        }
+        f3_phase_end();
+
+        // ================= softmax phase =================
+        if (active) {
+            const int key0 = kb * F3_BK;
+            if (CAUSAL && key0 + F3_BK - 1 > q0) {
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * h + (r & 3);
+                        st[kt][r] = key > my_q ? -INFINITY : st[kt][r];
+                    }
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[kt][r]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+            if (__builtin_amdgcn_ballot_w64(mx > m_run + F3_RESCALE)) {
+                const float m_new = fmaxf(m_run, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+                m_run = m_new;
+            }
+            const float mneg = -m_run;
+            float lsum = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    f16x8 pv;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const float e = __builtin_amdgcn_exp2f(fmaf(st[kt][8 * ks + i], c, mneg));
+                        lsum += e;
+                        pv[i] = (f16)e;
+                    }
+                    pf[kt][ks] = pv;
+                }
+            l_run += lsum;
+        }
+        f3_phase_end();
+    }
+    if (!late) __builtin_amdgcn_s_barrier();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // ---- O / L, fp16.  o[dt] register r: d = 32 dt + 8 (r / 4) + 4 h + r % 4 of query my_q.
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = 1.f / l_tot;
+    f16* orow = Ob + (int64_t)my_q * p.osl;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+            const int d = 32 * dt + 8 * g4 + 4 * h;
+            f16x4 v = {(f16)(o[dt][4 * g4 + 0] * inv), (f16)(o[dt][4 * g4 + 1] * inv),
+                       (f16)(o[dt][4 * g4 + 2] * inv), (f16)(o[dt][4 * g4 + 3] * inv)};
+            *reinterpret_cast<f16x4*>(orow + d) = v;
+        }
+}
+
 // Any D <= 256, any S: one thread per query row, online softmax in fp32 over every
 // key (the clamped/ragged path; not the fast one).
 __global__ void flash_generic_kernel(FaParams p, int D) {
@@ -320,6 +601,17 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     fast = fast && aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8);
     const int64_t blocks = (S / FA_BQ) * H * B;
     fast = fast && blocks <= 0x7fffffff;
+    const bool fast3 = fast && S % F3_BQ == 0 && scale > 0.f && S * strides[1] * 2 < ((int64_t)1 << 31) &&
+                       (S / F3_BQ) * H * B <= 0x7fffffff;
+    if (fast3) {
+        const dim3 grid((unsigned)((S / F3_BQ) * H * B));
+        if (p.causal)
+            hipLaunchKernelGGL(flash_fwd3_kernel<true>, grid, dim3(64 * F3_WAVES), 0, s, p);
+        else
+            hipLaunchKernelGGL(flash_fwd3_kernel<false>, grid, dim3(64 * F3_WAVES), 0, s, p);
+        LAVA_LAUNCH_CHECK("flash_fwd3_kernel");
+        return LAVA_HIP_OK;
+    }
     if (fast) {
         if (p.causal)
             hipLaunchKernelGGL(flash_fwd_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, s, p);
