@@ -279,6 +279,12 @@ constexpr int F3_BK = 64;
 constexpr int F3_STAGES = 3;
 constexpr int F3_TILE = F3_BK * FA_D * 2;   // 16 KB: one K or V block
 constexpr float F3_RESCALE = 8.0f;
+constexpr int F3_PREFETCH = 4;        // MFMA-phase operations between an LDS read and its use
+
+template <bool B>
+struct f3_tag {
+    static constexpr bool value = B;
+};
 
 typedef int f3_v4i __attribute__((ext_vector_type(4)));
 typedef short f3_s16x4 __attribute__((ext_vector_type(4)));
@@ -312,6 +318,18 @@ __device__ __forceinline__ uint32_t f3_lds_addr(const void* p) {
 __device__ __forceinline__ f3_s16x4 f3_read_tr(const uint8_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
         (__attribute__((address_space(3))) f3_s16x4*)(const __attribute__((address_space(3))) uint8_t*)p);
+}
+
+// Empty asm uses that pin a value's computation before this point: without them the
+// compiler sinks the softmax's exp / convert / sum (used only by the next phase's
+// MFMAs) across the barrier into the MFMA phase, which undoes the ping-pong.
+__device__ __forceinline__ void f3_pin(const f16x8& v) {
+    const uint4 u = __builtin_bit_cast(uint4, v);
+    asm volatile("" ::"v"(u.x), "v"(u.y), "v"(u.z), "v"(u.w));
+}
+__device__ __forceinline__ void f3_pin(const f32x16& v) {
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) asm volatile("" ::"v"(v[i]), "v"(v[i + 1]), "v"(v[i + 2]), "v"(v[i + 3]));
 }
 
 // All waits for the DMAs of the phase before last, then the workgroup barrier.
@@ -403,6 +421,49 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     f32x16 st[2];              // S^T of the current block: st[kt] register r = key 32 kt + 8 (r / 4) + 4 h + r % 4
     f16x8 pf[2][2];            // P^T of the previous block, B operand [kt][ks]: keys 32 kt + 16 ks + 8 (i / 4) + 4 h + i % 4
 
+    // The MFMA phase as one list of 32 operations -- ops [0, 16): O^T += V^T P^T for
+    // the previous block (kt = i / 8, ks = i / 4 % 2, dt = i % 4); ops [16, 32):
+    // S^T = K Q^T (ks = (i - 16) / 2, kt = i % 2) -- whose LDS operand reads run
+    // F3_PREFETCH operations ahead of the MFMAs (the partner wavefront is in its
+    // softmax phase, so nothing else hides the LDS latency).
+    auto read_op = [&](int i, const uint8_t* vbase, const uint8_t* kbase) -> f16x8 {
+        if (i < 16) {
+            const int kk = 32 * (i >> 3) + 16 * ((i >> 2) & 1), dt = i & 3;
+            const f3_s16x4 lo = f3_read_tr(vbase + v_off[dt] + kk * 256);
+            const f3_s16x4 hi = f3_read_tr(vbase + v_off[dt] + (kk + 8) * 256);
+            return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
+        const int j = i - 16;
+        return *reinterpret_cast<const f16x8*>(kbase + k_off[j >> 1] + (j & 1) * 32 * 256);
+    };
+    auto mma_op = [&](int i, f16x8 a) {
+        if (i < 16) {
+            o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[i >> 3][(i >> 2) & 1], o[i & 3], 0, 0, 0);
+        } else {
+            const int j = i - 16;
+            st[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[j >> 1], j < 2 ? f32x16{} : st[j & 1], 0, 0, 0);
+        }
+    };
+    auto mfma_phase = [&](auto pv_tag, auto s_tag, const uint8_t* vbase, const uint8_t* kbase) {
+        constexpr int first = decltype(pv_tag)::value ? 0 : 16;
+        constexpr int last = decltype(s_tag)::value ? 32 : 16;
+        f16x8 buf[F3_PREFETCH];
+#pragma unroll
+        for (int t = 0; t < F3_PREFETCH; ++t)
+            if (first + t < last) buf[t] = read_op(first + t, vbase, kbase);
+#pragma unroll
+        for (int i = first; i < last; ++i) {
+            const f16x8 a = buf[(i - first) % F3_PREFETCH];
+            if (i + F3_PREFETCH < last) buf[(i - first) % F3_PREFETCH] = read_op(i + F3_PREFETCH, vbase, kbase);
+            mma_op(i, a);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (decltype(s_tag)::value) {
+            f3_pin(st[0]);
+            f3_pin(st[1]);
+        }
+    };
+
     issue(rk, voff_k, lds_k, 0);
     // Consume Q here so the compiler's own wait for its loads happens once, before
     // the loop, instead of as vmcnt waits inside it (which would also cover the
@@ -418,90 +479,95 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     __syncthreads();
     if (late) __builtin_amdgcn_s_barrier();
 
-    for (int kb = 0; kb <= nkb; ++kb) {
-        // ================= MFMA phase =================
+    // Online softmax of block kb (base 2, the scale folded into the exponent's fma):
+    // masks the diagonal block, rescales O and L when the maximum moves (lazily),
+    // and leaves P^T in pf for the next MFMA phase.
+    auto softmax = [&](int kb) {
+        const int key0 = kb * F3_BK;
+        if (CAUSAL && key0 + F3_BK - 1 > q0) {
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * h + (r & 3);
+                    st[kt][r] = key > my_q ? -INFINITY : st[kt][r];
+                }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[kt][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
+        if (__builtin_amdgcn_ballot_w64(mx > m_run + F3_RESCALE)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+            m_run = m_new;
+        }
+        const float mneg = -m_run;
+        float lsum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                f16x8 pv;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float e = __builtin_amdgcn_exp2f(fmaf(st[kt][8 * ks + i], c, mneg));
+                    lsum += e;
+                    pv[i] = (f16)e;
+                }
+                pf[kt][ks] = pv;
+            }
+        l_run += lsum;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) f3_pin(pf[kt][ks]);
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) f3_pin(o[dt]);
+        asm volatile("" ::"v"(l_run), "v"(m_run));
+    };
+    // Every MFMA phase issues the DMAs of K block kb + 2 and V block kb + 1: the
+    // tiles are loaded cooperatively, so each wavefront issues its share of every
+    // one, active or not, and passes the same barriers.
+    auto dma = [&](int kb) {
         issue(rk, voff_k, lds_k, kb + 2);
         issue(rv, voff_v, lds_v, kb + 1);
-        if (kb > 0 && (!CAUSAL || (kb - 1) * F3_BK <= q0 + 31)) {
-            // O^T += V^T P^T for block kb - 1
-            const uint8_t* vbase = &vbuf[(kb - 1) % F3_STAGES][0];
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int dt = 0; dt < 4; ++dt) {
-                        const int kk = 32 * kt + 16 * ks;
-                        const f3_s16x4 lo = f3_read_tr(vbase + v_off[dt] + kk * 256);
-                        const f3_s16x4 hi = f3_read_tr(vbase + v_off[dt] + (kk + 8) * 256);
-                        const f3_s16x8 vf = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-                        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, vf), pf[kt][ks],
-                                                                       o[dt], 0, 0, 0);
-                    }
-        }
-        const bool active = kb < nkb && (!CAUSAL || kb * F3_BK <= q0 + 31);
-        if (active) {
-            // S^T = K Q^T for block kb
-            const uint8_t* kbase = &kbuf[kb % F3_STAGES][0];
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) st[kt][r] = 0.f;
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks)
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt) {
-                    const f16x8 kf = *reinterpret_cast<const f16x8*>(kbase + k_off[ks] + kt * 32 * 256);
-                    st[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qf[ks], st[kt], 0, 0, 0);
-                }
-        }
-        f3_phase_end();
+    };
+    auto vb = [&](int kb) { return &vbuf[(kb + F3_STAGES - 1) % F3_STAGES][0]; };   // V of block kb - 1
+    auto kbuf_of = [&](int kb) { return &kbuf[kb % F3_STAGES][0]; };
+    // this wavefront's last block with an unmasked key
+    const int last = CAUSAL ? min(nkb - 1, (q0 + 31) / F3_BK) : nkb - 1;
 
-        // ================= softmax phase =================
-        if (active) {
-            const int key0 = kb * F3_BK;
-            if (CAUSAL && key0 + F3_BK - 1 > q0) {
-#pragma unroll
-                for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * h + (r & 3);
-                        st[kt][r] = key > my_q ? -INFINITY : st[kt][r];
-                    }
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[kt][r]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c;
-            if (__builtin_amdgcn_ballot_w64(mx > m_run + F3_RESCALE)) {
-                const float m_new = fmaxf(m_run, mx);
-                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-                l_run *= alpha;
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
-                m_run = m_new;
-            }
-            const float mneg = -m_run;
-            float lsum = 0.f;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks) {
-                    f16x8 pv;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        const float e = __builtin_amdgcn_exp2f(fmaf(st[kt][8 * ks + i], c, mneg));
-                        lsum += e;
-                        pv[i] = (f16)e;
-                    }
-                    pf[kt][ks] = pv;
-                }
-            l_run += lsum;
-        }
+    // iteration 0: S only
+    dma(0);
+    mfma_phase(f3_tag<false>{}, f3_tag<true>{}, vb(0), kbuf_of(0));
+    f3_phase_end();
+    softmax(0);
+    f3_phase_end();
+    // iterations 1 .. last: O += V^T P^T for block kb - 1, then S for block kb
+    for (int kb = 1; kb <= last; ++kb) {
+        dma(kb);
+        mfma_phase(f3_tag<true>{}, f3_tag<true>{}, vb(kb), kbuf_of(kb));
+        f3_phase_end();
+        softmax(kb);
+        f3_phase_end();
+    }
+    // iteration last + 1: the final O update
+    dma(last + 1);
+    mfma_phase(f3_tag<true>{}, f3_tag<false>{}, vb(last + 1), kbuf_of(last + 1));
+    f3_phase_end();
+    f3_phase_end();
+    // remaining iterations (causal: blocks past this wavefront's queries)
+    for (int kb = last + 2; kb <= nkb; ++kb) {
+        dma(kb);
+        f3_phase_end();
         f3_phase_end();
     }
     if (!late) __builtin_amdgcn_s_barrier();
