@@ -320,16 +320,16 @@ __device__ __forceinline__ f3_s16x4 f3_read_tr(const uint8_t* p) {
         (__attribute__((address_space(3))) f3_s16x4*)(const __attribute__((address_space(3))) uint8_t*)p);
 }
 
-// Empty asm uses that pin a value's computation before this point: without them the
+// Asm uses (a comment: the backend drops empty asm) that pin a value's computation before this point: without them the
 // compiler sinks the softmax's exp / convert / sum (used only by the next phase's
 // MFMAs) across the barrier into the MFMA phase, which undoes the ping-pong.
 __device__ __forceinline__ void f3_pin(const f16x8& v) {
     const uint4 u = __builtin_bit_cast(uint4, v);
-    asm volatile("" ::"v"(u.x), "v"(u.y), "v"(u.z), "v"(u.w));
+    asm volatile("; pin" ::"v"(u.x), "v"(u.y), "v"(u.z), "v"(u.w));
 }
 __device__ __forceinline__ void f3_pin(const f32x16& v) {
 #pragma unroll
-    for (int i = 0; i < 16; i += 4) asm volatile("" ::"v"(v[i]), "v"(v[i + 1]), "v"(v[i + 2]), "v"(v[i + 3]));
+    for (int i = 0; i < 16; i += 4) asm volatile("; pin" ::"v"(v[i]), "v"(v[i + 1]), "v"(v[i + 2]), "v"(v[i + 3]));
 }
 
 // All waits for the DMAs of the phase before last, then the workgroup barrier.
@@ -531,7 +531,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
             for (int ks = 0; ks < 2; ++ks) f3_pin(pf[kt][ks]);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) f3_pin(o[dt]);
-        asm volatile("" ::"v"(l_run), "v"(m_run));
+        asm volatile("; pin" ::"v"(l_run), "v"(m_run));
     };
     // Every MFMA phase issues the DMAs of K block kb + 2 and V block kb + 1: the
     // tiles are loaded cooperatively, so each wavefront issues its share of every
