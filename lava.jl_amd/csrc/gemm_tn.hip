@@ -20,7 +20,9 @@
 //  * fragments are 16 bytes per lane (ds_read_b128), one MFMA 32x32x16 (16-bit)
 //    or 32x32x32 (int8) each; 4 sub-steps of 32 bytes of K per stage, each 16
 //    MFMAs, with the next sub-step's fragments read underneath (double-buffered
-//    fragment registers, 64 VGPRs) and the next stage's DMA issued at sub-step 0;
+//    fragment registers, 64 VGPRs) and the next stage's 16 DMA loads issued one per
+//    two MFMAs over sub-steps 0 and 1 (a wavefront's vector-memory issue takes
+//    ~40-70 cycles per 1 KB instruction; one per MFMA would stall the MFMA stream);
 //  * the MFMA's A operand is the B slice and its B operand the A slice, so each
 //    lane's accumulator holds runs of 4 consecutive columns of one row of C; the
 //    epilogue stages them through LDS and stores whole 512-byte row runs;
@@ -150,7 +152,7 @@ __global__ void __launch_bounds__(256, 1)
 
     // Per k-tile (128 bytes of K = 4 sub-steps), branch-free so the interleave holds:
     //   s = 0..2: 16 MFMAs on the current fragments while the next sub-step's 8 LDS
-    //             reads (and, at s = 0, the 16 DMA loads of the next tile) issue;
+    //             reads (and, at s = 0 and 1, 8 DMA loads of the next tile each) issue;
     //   s = 3:    8 MFMAs; wait for this wave's DMA; barrier; then the next tile's
     //             s = 0 reads under the last 8 MFMAs.
     // On the last tile the "next" tile re-fetches the current one into the idle stage.
@@ -175,17 +177,20 @@ __global__ void __launch_bounds__(256, 1)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 acc[i][j] = Mfma32<T>::run(fa.b[j], fa.a[i], acc[i][j]);
-                dma(4 * i + j, st ^ 1, kofs_next);
+                if (j & 1) dma(2 * i + (j >> 1), st ^ 1, kofs_next);
+                __builtin_amdgcn_sched_barrier(0);
             }
-        // s = 1, 2: next sub-step's LDS reads under 16 MFMAs
+        // s = 1: the other 8 DMA loads (one per two MFMAs) and s = 2's LDS reads under 16 MFMAs
         read_frags(fa, base, 2);
-        mma(fb, 0, 4);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
-        }
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[i][j] = Mfma32<T>::run(fb.b[j], fb.a[i], acc[i][j]);
+                if (j & 1) dma(8 + 2 * i + (j >> 1), st ^ 1, kofs_next);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         read_frags(fb, base, 3);
         mma(fa, 0, 4);
 #pragma unroll
