@@ -16,10 +16,15 @@
 //    (0x6400 | (w ^ 0x80) is the fp16 value 1152 + w; subtract 1152);
 //  * X (16 x 32 per step, fp16) is the A operand, read straight from global/L2;
 //  * 4 wavefronts per workgroup split the workgroup's K range and reduce through
-//    LDS; `splits` workgroups split K further and the last one to finish (atomic
-//    ticket) adds the partials in a fixed order, applies s[c] and writes Y, so the
-//    result does not depend on arrival order;
-//  * the scale multiply is the fused per-element epilogue.
+//    LDS; to occupy every CU (N / 128 column blocks alone leave most of them idle)
+//    `splits` workgroups split K further, each writing its partial block, and a
+//    second small kernel on the same stream adds the splits in a fixed order,
+//    applies s[c] and writes Y -- deterministic, and free of the device-scope
+//    fences a last-arriver reduction needs (on a multi-XCD part each such fence
+//    writes back the XCD's L2, which cost ~7x the whole weight stream);
+//  * the weight rows of up to W8_DEPTH K steps are in flight ahead of the MFMAs;
+//  * the scale multiply is the fused per-element epilogue (in the reduction when
+//    K is split).
 #include <hip/hip_runtime.h>
 
 #include <map>
@@ -33,6 +38,7 @@ namespace lava {
 constexpr int W8_COLS = 128;   // columns per workgroup
 constexpr int W8_KSTEP = 32;   // k per MFMA step
 constexpr int W8_WAVES = 4;
+constexpr int W8_DEPTH = 4;   // K steps of weights in flight per wavefront
 
 __device__ __forceinline__ uint32_t w8_pair(uint32_t lo_row, uint32_t hi_row, int byte) {
     // [lo_row.byte, 0, hi_row.byte, 0] -> two fp16 values 1152 + w, then subtract 1152
@@ -43,10 +49,9 @@ __device__ __forceinline__ uint32_t w8_pair(uint32_t lo_row, uint32_t hi_row, in
 template <int KSTEPS>
 __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
                                                     const f16* __restrict__ scale, float* __restrict__ Y,
-                                                    float* __restrict__ partial, int* __restrict__ tickets, int M,
-                                                    int N, int64_t ldx, int64_t ldw, int64_t ldy, int splits) {
+                                                    float* __restrict__ partial, int M, int N, int64_t ldx,
+                                                    int64_t ldw, int64_t ldy, int splits) {
     __shared__ __attribute__((aligned(16))) float red[W8_WAVES][16][W8_COLS];
-    __shared__ int is_last;
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int q = lane & 15, g = lane >> 4;
@@ -68,15 +73,27 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
 
     const f16x8 bias = {(f16)-1152.f, (f16)-1152.f, (f16)-1152.f, (f16)-1152.f,
                         (f16)-1152.f, (f16)-1152.f, (f16)-1152.f, (f16)-1152.f};
-#pragma unroll 2
-    for (int s = 0; s < KSTEPS; ++s) {
-        u32x2 rows[8];
+    // Weight rows and X for W8_DEPTH steps are in flight ahead of the MFMAs (a ring in
+    // registers): the stream is latency-bound otherwise, one HBM round trip per step.
+    constexpr int DEPTH = KSTEPS < W8_DEPTH ? KSTEPS : W8_DEPTH;
+    u32x2 ring[DEPTH][8];
+    uint4 xring[DEPTH];
+    auto load_step = [&](int s, u32x2* rows, uint4& xa) {
 #pragma unroll
         for (int r = 0; r < 8; ++r)
             rows[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(wp + ((int64_t)s * W8_KSTEP + r) * ldw));
-        uint4 xa = make_uint4(0, 0, 0, 0);
+        xa = make_uint4(0, 0, 0, 0);
         if (xrow_ok) xa = *reinterpret_cast<const uint4*>(xp + s * W8_KSTEP);
-        const f16x8 a = __builtin_bit_cast(f16x8, xa);
+    };
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) load_step(s, ring[s], xring[s]);
+#pragma unroll
+    for (int s = 0; s < KSTEPS; ++s) {
+        u32x2 rows[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) rows[r] = ring[s % DEPTH][r];
+        const f16x8 a = __builtin_bit_cast(f16x8, xring[s % DEPTH]);
+        if (s + DEPTH < KSTEPS) load_step(s + DEPTH, ring[s % DEPTH], xring[s % DEPTH]);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const int byte = t & 3;
@@ -113,35 +130,35 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
 
     const int grow = m0 + row;
     if (splits > 1) {
+        // partial block of this split: [split][mb * 16 + row][N], summed by w8a16_reduce_kernel
         float* mine = partial + (((int64_t)split * gridDim.z + mb) * 16 + row) * N + n0 + c8;
 #pragma unroll
         for (int i = 0; i < 8; i += 4) *reinterpret_cast<float4*>(mine + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            const int ticket = atomicAdd(&tickets[mb * gridDim.x + cb], 1);
-            is_last = (ticket == splits - 1);
-        }
-        __syncthreads();
-        if (!is_last) return;
-        __threadfence();
-        // fixed-order sum of all splits
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.f;
-        for (int sp = 0; sp < splits; ++sp) {
-            const float* p = partial + (((int64_t)sp * gridDim.z + mb) * 16 + row) * N + n0 + c8;
-            const f32x4 a = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
-            const f32x4 b = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
-            v[0] += a[0]; v[1] += a[1]; v[2] += a[2]; v[3] += a[3];
-            v[4] += b[0]; v[5] += b[1]; v[6] += b[2]; v[7] += b[3];
-        }
-        if (tid == 0) tickets[mb * gridDim.x + cb] = 0;   // ready for the next call
+        return;
     }
     if (grow < M) {
         float* yp = Y + (int64_t)grow * ldy + n0 + c8;
 #pragma unroll
         for (int i = 0; i < 8; ++i) yp[i] = v[i] * (float)scale[n0 + c8 + i];
     }
+}
+
+// Y[r, c] = s[c] * sum over splits (in split order) of the partial blocks; 4 columns per thread.
+__global__ void __launch_bounds__(256) w8a16_reduce_kernel(const float* __restrict__ partial,
+                                                           const f16* __restrict__ scale, float* __restrict__ Y,
+                                                           int M, int N, int64_t ldy, int splits, int64_t rows_pad) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // (row, 4-column group)
+    const int64_t groups = N / 4;
+    if (idx >= (int64_t)M * groups) return;
+    const int64_t r = idx / groups, c = (idx % groups) * 4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < splits; ++sp) {
+        const f32x4 p = *reinterpret_cast<const f32x4*>(partial + ((int64_t)sp * rows_pad + r) * N + c);
+        acc[0] += p[0]; acc[1] += p[1]; acc[2] += p[2]; acc[3] += p[3];
+    }
+    float* yp = Y + r * ldy + c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) yp[i] = acc[i] * (float)scale[c + i];
 }
 
 // Any layout, any shape: one thread per output element, fp32 sums.
@@ -161,44 +178,32 @@ __global__ void w8a16_generic_kernel(const f16* __restrict__ X, const int8_t* __
     Y[yrow ? r * ldy + c : c * ldy + r] = s * (float)scale[c];
 }
 
-// Per-(device, stream) workspace for the split-K partials and tickets, laid out
-// as [tickets | partials] so the tickets stay at offset 0 whatever the problem
-// size.  Tickets are zeroed when the buffer is created and returned to zero by
-// the workgroup that consumes them, so every later call finds them at zero.
+// Per-(device, stream) workspace for the split-K partial blocks, grown on demand;
+// calls on one stream are ordered, so they can share it.
 struct W8Workspace {
     void* buf = nullptr;
-    size_t ticket_bytes = 0;
-    size_t partial_bytes = 0;
+    size_t bytes = 0;
 };
 static std::mutex g_ws_mutex;
 static std::map<std::pair<int, void*>, W8Workspace> g_ws;
 
-static int get_workspace(void* stream, size_t partial_bytes, size_t ticket_bytes, float** partial, int** tickets) {
+static int get_workspace(void* stream, size_t partial_bytes, float** partial) {
     int dev = 0;
     LAVA_HIP_TRY(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     W8Workspace& ws = g_ws[{dev, stream}];
-    if (ws.ticket_bytes < ticket_bytes || ws.partial_bytes < partial_bytes) {
-        const size_t tb = ((ticket_bytes > ws.ticket_bytes ? ticket_bytes : ws.ticket_bytes) + 255) / 256 * 256;
-        const size_t pb = partial_bytes > ws.partial_bytes ? partial_bytes : ws.partial_bytes;
+    if (ws.bytes < partial_bytes) {
         if (ws.buf) {
             LAVA_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
             LAVA_HIP_TRY(hipFree(ws.buf));
             ws = W8Workspace{};
         }
         void* p = nullptr;
-        LAVA_HIP_TRY(hipMalloc(&p, tb + pb));
-        int rc = lava_hip_fill_bytes(p, 0, tb, stream);
-        if (rc != LAVA_HIP_OK) {
-            (void)hipFree(p);
-            return rc;
-        }
+        LAVA_HIP_TRY(hipMalloc(&p, partial_bytes));
         ws.buf = p;
-        ws.ticket_bytes = tb;
-        ws.partial_bytes = pb;
+        ws.bytes = partial_bytes;
     }
-    *tickets = static_cast<int*>(ws.buf);
-    *partial = reinterpret_cast<float*>(static_cast<char*>(ws.buf) + ws.ticket_bytes);
+    *partial = static_cast<float*>(ws.buf);
     return LAVA_HIP_OK;
 }
 
@@ -228,26 +233,25 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
                       ldw % 8 == 0 && ldx % 8 == 0 && aligned(W, 8) && aligned(X, 16) && N <= 0x7fffffff &&
                       M <= 0x7fffffff;
     if (fast) {
-        // split K so that there are >= 2 workgroups per CU where K allows
+        // split K (at most 4 ways: the partial blocks cost 8 * splits bytes per output
+        // element of extra traffic) until the grid covers the 256 CUs
         const int64_t cblocks = N / W8_COLS, mblocks = (M + 15) / 16;
         const int64_t kwave_steps = K / (W8_WAVES * W8_KSTEP);   // steps per wave at 1 split
         int splits = 1;
-        while (splits < 16 && cblocks * mblocks * splits < 512 && kwave_steps % (2 * splits) == 0 &&
+        while (splits < 4 && cblocks * mblocks * splits < 256 && kwave_steps % (2 * splits) == 0 &&
                kwave_steps / (2 * splits) >= 2)
             splits *= 2;
         const int64_t ksteps = kwave_steps / splits;
         LAVA_REQUIRE(mblocks <= 65535 && cblocks <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: grid too large");
         float* partial = nullptr;
-        int* tickets = nullptr;
         if (splits > 1) {
-            rc = get_workspace(stream, (size_t)splits * (size_t)mblocks * 16 * (size_t)N * sizeof(float),
-                               (size_t)(cblocks * mblocks) * sizeof(int), &partial, &tickets);
+            rc = get_workspace(stream, (size_t)splits * (size_t)mblocks * 16 * (size_t)N * sizeof(float), &partial);
             if (rc != LAVA_HIP_OK) return rc;
         }
         const dim3 grid((unsigned)cblocks, (unsigned)splits, (unsigned)mblocks);
 #define LAVA_W8_LAUNCH(KS)                                                                                           \
     hipLaunchKernelGGL(w8a16_kernel<KS>, grid, dim3(256), 0, s, (const f16*)X, (const int8_t*)W, (const f16*)scale, \
-                       (float*)Y, partial, tickets, (int)M, (int)N, ldx, ldw, ldy, splits)
+                       (float*)Y, partial, (int)M, (int)N, ldx, ldw, ldy, splits)
         switch (ksteps) {
         case 1: LAVA_W8_LAUNCH(1); break;
         case 2: LAVA_W8_LAUNCH(2); break;
@@ -259,6 +263,14 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
         }
 #undef LAVA_W8_LAUNCH
         LAVA_LAUNCH_CHECK("w8a16_kernel");
+        if (splits > 1) {
+            const int64_t threads = M * (N / 4);
+            LAVA_REQUIRE((threads + 255) / 256 <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: problem too large");
+            hipLaunchKernelGGL(w8a16_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                               (const float*)partial, (const f16*)scale, (float*)Y, (int)M, (int)N, ldy, splits,
+                               mblocks * 16);
+            LAVA_LAUNCH_CHECK("w8a16_reduce_kernel");
+        }
         return LAVA_HIP_OK;
     }
 generic : {
