@@ -140,13 +140,14 @@ def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6):
 
 
 # ---------------------------------------------------------------- CPU baseline
-def cpu_baseline_gemm(n=8192, budget_s=12.0):
+def cpu_baseline_gemm(n=8192, budget_s=20.0):
     """The oracle's fp32-accumulate GEMM (a port of the tile loop, not the Lava
     path: Julia/Mantle/lavapipe are not on the GPU box) on all host threads, over
-    a bounded number of rows of the same 8192^3 bf16 problem."""
+    as many rows of the same 8192^3 bf16 problem as fit the time budget (all of
+    them on a 16-core host)."""
     sys.path.insert(0, str(REPO))
     from oracle import oracle as o
-    max_rows = 2048
+    max_rows = n
     A = o.fill_uniform(max_rows * n, "bf16", 0x4C415641 + 256, -1.0, 1.0)   # the first rows of A
     B = o.fill_uniform(n * n, "bf16", 0x4C415641 + 257, -1.0, 1.0)    # B column-major, n x n
     t0 = time.perf_counter()
