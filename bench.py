@@ -8,7 +8,8 @@ in the same JSON line with its own roofline.  Inputs are the seeded synthetic
 tensors of the parity tests, generated on the device and resident in HBM
 before timing starts.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256]
+  python bench.py [--gpus 1] [--steps K] [--warmup W]
+                  [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|copy]
 
 A step is one kernel launch over the whole problem.  Kernel time comes from HIP
 events recorded on the launch stream around the K timed launches; wall time
@@ -86,6 +87,24 @@ def bench_gemm(lh, dt, n, steps, warmup, stream, cfg):
     kern_ms, wall_ms = timed(lh, lambda: lh.gemm(C, A, B, stream=stream), steps, warmup, stream)
     flop = 2.0 * n ** 3
     return flop, kern_ms, wall_ms
+
+
+def bench_gemm_ex(lh, n, steps, warmup, stream, cfg):
+    """The fused epilogue at the headline shape: D (bf16) = gelu_tanh(A*B + bias + residual),
+    bias one fp32 value per row, residual fp32 M x N."""
+    A = lh.HIPDeviceArray("bf16", (n, n), order="C")
+    B = lh.HIPDeviceArray("bf16", (n, n), order="F")
+    D = lh.HIPDeviceArray("bf16", (n, n), order="C")
+    bias = lh.HIPDeviceArray("f32", (n,))
+    res = lh.HIPDeviceArray("f32", (n, n), order="C")
+    lh.fill_uniform(A, lh.seed(cfg, 0), -1.0, 1.0)
+    lh.fill_uniform(B, lh.seed(cfg, 1), -1.0, 1.0)
+    lh.fill_uniform(bias, lh.seed(cfg, 2), -1.0, 1.0)
+    lh.fill_uniform(res, lh.seed(cfg, 3), -1.0, 1.0)
+    lh.synchronize()
+    kern_ms, wall_ms = timed(lh, lambda: lh.gemm_ex(D, A, B, bias=bias, residual=res, act="gelu_tanh",
+                                                    stream=stream), steps, warmup, stream)
+    return 2.0 * n ** 3, kern_ms, wall_ms
 
 
 def bench_gemm_layout(lh, dt, n, layout, steps, warmup, stream, cfg):
@@ -174,7 +193,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
-                             "copy"])
+                             "gemm_ex_bf16", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -216,6 +235,13 @@ def main():
         flop, kms, wms = bench_gemm(lh, "bf16", 4096, K, W, stream, 1)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16", "config": {"workload": "bf16 GEMM 4096^3 A row-major B column-major"},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "gemm_ex_bf16":
+        flop, kms, wms = bench_gemm_ex(lh, 8192, K, W, stream, 1)
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "bf16", "config": {"workload": "bf16 GEMM 8192^3 with the fused epilogue: D bf16 = "
+                                                            "gelu_tanh(A*B + bias[row] + residual), bias and residual fp32"},
                     "kernel_ms": round(kms, 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "attn":

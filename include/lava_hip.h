@@ -195,6 +195,29 @@ int lava_hip_gemm_bf16_f32(const void* A, const void* B, void* C, int64_t M, int
 int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
 
+/* ---- fused GEMM epilogue: activations (elementwise epilogues that Lava writes with
+ * coopmat_length / getcomp / setcomp, src/device/coopmat_intrinsics.jl:322-400) ---- */
+#define LAVA_HIP_ACT_NONE 0
+#define LAVA_HIP_ACT_RELU 1
+#define LAVA_HIP_ACT_GELU_TANH 2 /* 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) */
+#define LAVA_HIP_ACT_GELU_ERF 3  /* 0.5 x (1 + erf(x / sqrt(2))) */
+
+/* GEMM with the epilogue family fused into the store:
+ *   D = act(A B + (bias + residual)), narrowed RNE to D's type.
+ * The accumulator init is Lava's `accinit`: a stride-0 accumulator load of the bias (one
+ * fp32 value per row m of D) plus the residual (fp32, M x N, laid out like D with leading
+ * dimension ldr), summed with coopmat_add (src/device/coopmat_intrinsics.jl:435-464;
+ * src/compiler/spirv/coopmat.jl:870-885); `act` is the getcomp/setcomp epilogue; the
+ * fp16 / bf16 output is coopmat_convert of the fp32 accumulator, RNE
+ * (src/compiler/spirv/coopmat.jl:163-182, 783-824).
+ * ab_dtype: LAVA_HIP_F16 or LAVA_HIP_BF16 (A and B); d_dtype: LAVA_HIP_F32, LAVA_HIP_F16 or
+ * LAVA_HIP_BF16.  bias and residual may each be NULL (ldr is then unused); layout as for the
+ * plain GEMM, bit 2 giving D's and the residual's layout.  The plain entry points are this
+ * call with no bias, no residual, LAVA_HIP_ACT_NONE and an fp32 D. */
+int lava_hip_gemm_ex(int ab_dtype, int d_dtype, const void* A, const void* B, void* D, int64_t M, int64_t N,
+                     int64_t K, int64_t lda, int64_t ldb, int64_t ldd, uint32_t layout, const float* bias,
+                     const float* residual, int64_t ldr, int act, void* stream);
+
 /* The 16x16x16 subgroup-tile GEMM written directly in the vocabulary, one
  * wavefront per 16x16 tile of C, loading straight from global as
  * docs/src/device.md:81-88 does (fp16 in, fp32 out).  M, N, K multiples of 16. */

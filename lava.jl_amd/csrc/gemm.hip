@@ -14,10 +14,10 @@ using namespace lava;
 
 namespace {
 
-template <typename T>
+template <typename T, typename OutT = typename Mfma16<T>::acc_elem, bool EPI = false>
 int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-               int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
-    using Acc = typename Mfma16<T>::acc_elem;
+               int64_t ldb, int64_t ldc, uint32_t layout, void* stream, Epilogue epi = Epilogue{}) {
+    using Acc = OutT;
     LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative extent (M=%lld N=%lld K=%lld)", name, (long long)M,
              (long long)N, (long long)K);
     LAVA_ARG(layout <= 7u, "%s: layout %u has bits beyond A/B/C row-major", name, layout);
@@ -50,12 +50,32 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
         const bool ar = arow;
         arow = !brow;
         brow = !ar;
+        // the kernels now write D^T: the per-m bias runs along its columns; the residual,
+        // column-major like D, is read as its row-major transpose with the same ldr
+        epi.bias_on_cols = 1;
     }
     hipStream_t s = as_stream(stream);
     Acc* c = static_cast<Acc*>(C);
     if (arow && !brow && tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc))
-        return launch_gemm_tn<T>(a, b, c, M, N, K, lda, ldb, ldc, s);
-    return launch_gemm_staged<T>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s);
+        return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi);
+    return launch_gemm_staged<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
+}
+
+template <typename T, typename OutT>
+int gemm_ex_entry(const void* A, const void* B, void* D, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                  int64_t ldd, uint32_t layout, const float* bias, const float* residual, int64_t ldr, int act,
+                  void* stream) {
+    LAVA_ARG(act >= EPI_NONE && act <= EPI_GELU_ERF, "gemm_ex: unknown activation %d", act);
+    LAVA_ARG(aligned(bias, 4) && aligned(residual, 4), "gemm_ex: bias / residual not 4-byte aligned");
+    if (residual != nullptr && M > 0 && N > 0)
+        LAVA_ARG(ldr >= ((layout & 4u) ? N : M), "gemm_ex: ldr = %lld is smaller than %s", (long long)ldr,
+                 (layout & 4u) ? "N" : "M");
+    Epilogue epi;
+    epi.bias = bias;
+    epi.residual = residual;
+    epi.ldr = ldr;
+    epi.act = act;
+    return gemm_entry<T, OutT, true>("gemm_ex", A, B, D, M, N, K, lda, ldb, ldd, layout, stream, epi);
 }
 
 }  // namespace
@@ -75,6 +95,24 @@ int lava_hip_gemm_bf16_f32(const void* A, const void* B, void* C, int64_t M, int
 int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
     return gemm_entry<int8_t>("gemm_i8_i32", A, B, C, M, N, K, lda, ldb, ldc, layout, stream);
+}
+
+int lava_hip_gemm_ex(int ab_dtype, int d_dtype, const void* A, const void* B, void* D, int64_t M, int64_t N,
+                     int64_t K, int64_t lda, int64_t ldb, int64_t ldd, uint32_t layout, const float* bias,
+                     const float* residual, int64_t ldr, int act, void* stream) {
+    LAVA_ARG(ab_dtype == LAVA_HIP_F16 || ab_dtype == LAVA_HIP_BF16, "gemm_ex: A/B dtype %d is not f16 or bf16",
+             ab_dtype);
+    LAVA_ARG(d_dtype == LAVA_HIP_F32 || d_dtype == LAVA_HIP_F16 || d_dtype == LAVA_HIP_BF16,
+             "gemm_ex: D dtype %d is not f32, f16 or bf16", d_dtype);
+    const bool h = ab_dtype == LAVA_HIP_F16;
+    if (d_dtype == LAVA_HIP_F32)
+        return h ? gemm_ex_entry<f16, float>(A, B, D, M, N, K, lda, ldb, ldd, layout, bias, residual, ldr, act, stream)
+                 : gemm_ex_entry<bf16, float>(A, B, D, M, N, K, lda, ldb, ldd, layout, bias, residual, ldr, act, stream);
+    if (d_dtype == LAVA_HIP_F16)
+        return h ? gemm_ex_entry<f16, f16>(A, B, D, M, N, K, lda, ldb, ldd, layout, bias, residual, ldr, act, stream)
+                 : gemm_ex_entry<bf16, f16>(A, B, D, M, N, K, lda, ldb, ldd, layout, bias, residual, ldr, act, stream);
+    return h ? gemm_ex_entry<f16, bf16>(A, B, D, M, N, K, lda, ldb, ldd, layout, bias, residual, ldr, act, stream)
+             : gemm_ex_entry<bf16, bf16>(A, B, D, M, N, K, lda, ldb, ldd, layout, bias, residual, ldr, act, stream);
 }
 
 int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,

@@ -98,4 +98,59 @@ __device__ __forceinline__ void xcd_tile(int b, int tiles_m, int tiles_n, int gr
     tn = r / gm;
 }
 
+// ---- fused GEMM epilogue: D = act(A B + (bias + residual)), then narrowed to D's type.
+// Lava starts the accumulator from bias + residual (`accinit`: a stride-0
+// accumulator load of the bias plus the residual at its leading dimension, summed
+// with coopmat_add, src/device/coopmat_intrinsics.jl:435-464), applies elementwise
+// epilogues through getcomp / setcomp (:322-400) and narrows with coopmat_convert
+// (RNE, src/compiler/spirv/coopmat.jl:783-824).  Here the same terms are added to the
+// finished accumulator in the store: the same sum, in another fp32 order.
+enum EpiAct : int { EPI_NONE = 0, EPI_RELU = 1, EPI_GELU_TANH = 2, EPI_GELU_ERF = 3 };
+
+struct Epilogue {
+    const float* bias = nullptr;       // nullptr, or one value per row (per column if bias_on_cols) of D
+    const float* residual = nullptr;   // nullptr, or a matrix laid out like D (row-major here) with ldr
+    int64_t ldr = 0;
+    int bias_on_cols = 0;              // D was transposed to row-major: the bias then runs along columns
+    int act = EPI_NONE;
+};
+
+// Inline elementary functions (a library call here would have to save the 256
+// accumulator registers that are still live around the epilogue):
+// e^x through v_exp_f32; tanh(u) = sign(u) (1 - e^{-2|u|}) / (1 + e^{-2|u|});
+// erf by Abramowitz & Stegun, Handbook of Mathematical Functions, 7.1.26
+// (|error| <= 1.5e-7 over the real line).
+__device__ __forceinline__ float epi_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float epi_tanh(float u) {
+    const float e = epi_exp(-2.f * fabsf(u));
+    return copysignf((1.f - e) / (1.f + e), u);
+}
+__device__ __forceinline__ float epi_erf(float x) {
+    const float ax = fabsf(x);
+    const float t = 1.f / (1.f + 0.3275911f * ax);
+    const float p = ((((1.061405429f * t - 1.453152027f) * t + 1.421413741f) * t - 0.284496736f) * t + 0.254829592f) * t;
+    return copysignf(1.f - p * epi_exp(-ax * ax), x);
+}
+
+__device__ __forceinline__ float epi_act(int act, float v) {
+    switch (act) {
+    case EPI_RELU: return v > 0.f ? v : 0.f;
+    case EPI_GELU_TANH: {
+        // 0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3)))
+        const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+        return 0.5f * v * (1.f + epi_tanh(u));
+    }
+    case EPI_GELU_ERF: return 0.5f * v * (1.f + epi_erf(v * 0.7071067811865476f));   // 0.5 x (1 + erf(x / sqrt 2))
+    default: return v;
+    }
+}
+
+// The finished accumulator value of D[m][n] (row-major frame of the kernel) through the epilogue.
+__device__ __forceinline__ float epi_apply(const Epilogue& e, int64_t m, int64_t n, float acc) {
+    float init = 0.f;
+    if (e.bias) init = e.bias[e.bias_on_cols ? n : m];
+    if (e.residual) init += e.residual[m * e.ldr + n];
+    return epi_act(e.act, acc + init);
+}
+
 }  // namespace lava

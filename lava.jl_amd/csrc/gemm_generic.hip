@@ -11,17 +11,18 @@
 //    tile of C, fragments loaded straight from global memory.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "gemm_common.hpp"
 #include "gemm_kernels.hpp"
 #include "lava_hip_internal.hpp"
 
 namespace lava {
 
-template <typename T, bool AROW, bool BROW>
+template <typename T, bool AROW, bool BROW, typename OutT, bool EPI>
 __global__ void __launch_bounds__(256) gemm_staged_kernel(const T* __restrict__ A, const T* __restrict__ B,
-                                                          typename Mfma16<T>::acc_elem* __restrict__ C, int64_t M,
-                                                          int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                                                          int64_t ldc) {
+                                                          OutT* __restrict__ C, int64_t M, int64_t N, int64_t K,
+                                                          int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi) {
     using Acc = typename Mfma16<T>::acc_elem;
     using AccV = typename Mfma16<T>::acc_t;
     constexpr int KE = Mfma16<T>::k;        // elements per K-slice (64 bytes)
@@ -84,7 +85,13 @@ __global__ void __launch_bounds__(256) gemm_staged_kernel(const T* __restrict__ 
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 const int64_t gm = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q;
-                if (gm < M && gn < N) C[gm * ldc + gn] = (Acc)acc[i][j][q];
+                if (gm < M && gn < N) {
+                    if constexpr (!EPI && std::is_same<OutT, Acc>::value)
+                        C[gm * ldc + gn] = (Acc)acc[i][j][q];
+                    else
+                        C[gm * ldc + gn] =
+                            narrow<OutT>(EPI ? epi_apply(epi, gm, gn, (float)acc[i][j][q]) : (float)acc[i][j][q]);
+                }
             }
         }
 }
@@ -106,29 +113,39 @@ __global__ void __launch_bounds__(256) coopmat_tiles_kernel(const f16* __restric
     store(C + (crow ? tm * 16 * ldc + tn * 16 : tn * 16 * ldc + tm * 16), ldc, crow, c);
 }
 
-template <typename T>
-int launch_gemm_staged(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
-                       int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, hipStream_t s) {
+template <typename T, typename OutT, bool EPI>
+int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                       int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi) {
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
     if (arow && brow)
-        hipLaunchKernelGGL((gemm_staged_kernel<T, true, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc);
+        hipLaunchKernelGGL((gemm_staged_kernel<T, true, true, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K,
+                           lda, ldb, ldc, epi);
     else if (arow)
-        hipLaunchKernelGGL((gemm_staged_kernel<T, true, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc);
+        hipLaunchKernelGGL((gemm_staged_kernel<T, true, false, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K,
+                           lda, ldb, ldc, epi);
     else if (brow)
-        hipLaunchKernelGGL((gemm_staged_kernel<T, false, true>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb, ldc);
+        hipLaunchKernelGGL((gemm_staged_kernel<T, false, true, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K,
+                           lda, ldb, ldc, epi);
     else
-        hipLaunchKernelGGL((gemm_staged_kernel<T, false, false>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda, ldb,
-                           ldc);
+        hipLaunchKernelGGL((gemm_staged_kernel<T, false, false, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K,
+                           lda, ldb, ldc, epi);
     LAVA_LAUNCH_CHECK("gemm_staged_kernel");
     return LAVA_HIP_OK;
 }
 
-template int launch_gemm_staged<f16>(const f16*, const f16*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                     int64_t, bool, bool, hipStream_t);
-template int launch_gemm_staged<bf16>(const bf16*, const bf16*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                      int64_t, bool, bool, hipStream_t);
-template int launch_gemm_staged<int8_t>(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, int64_t,
-                                        int64_t, int64_t, bool, bool, hipStream_t);
+#define LAVA_STAGED_INST(T, O, E)                                                                              \
+    template int launch_gemm_staged<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t, \
+                                             int64_t, bool, bool, hipStream_t, const Epilogue&);
+LAVA_STAGED_INST(f16, float, false)
+LAVA_STAGED_INST(bf16, float, false)
+LAVA_STAGED_INST(int8_t, int32_t, false)
+LAVA_STAGED_INST(f16, float, true)
+LAVA_STAGED_INST(f16, f16, true)
+LAVA_STAGED_INST(f16, bf16, true)
+LAVA_STAGED_INST(bf16, float, true)
+LAVA_STAGED_INST(bf16, f16, true)
+LAVA_STAGED_INST(bf16, bf16, true)
+#undef LAVA_STAGED_INST
 
 int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s) {

@@ -6,10 +6,11 @@
 
 namespace lava {
 
-// Any layout, any shape; C row-major with ldc.
-template <typename T>
-int launch_gemm_staged(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
-                       int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, hipStream_t s);
+// Any layout, any shape; C row-major with ldc.  OutT / EPI: the output type and the
+// fused epilogue (see Epilogue); <T, acc type, false> is the plain GEMM.
+template <typename T, typename OutT, bool EPI>
+int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                       int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi);
 
 // The 16x16x16 vocabulary-tile GEMM (fp16 -> fp32); M, N, K multiples of 16.
 int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
@@ -20,8 +21,8 @@ int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_
 template <typename T>
 bool tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                       int64_t ldb, int64_t ldc);
-template <typename T>
-int launch_gemm_tn(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
-                   int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s);
+template <typename T, typename OutT, bool EPI>
+int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                   int64_t ldc, hipStream_t s, const Epilogue& epi);
 
 }  // namespace lava

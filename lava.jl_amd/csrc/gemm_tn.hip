@@ -30,6 +30,8 @@
 //    runs together share rows of A and columns of B in its L2.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "gemm_common.hpp"
 #include "gemm_kernels.hpp"
 #include "lava_hip_internal.hpp"
@@ -72,10 +74,10 @@ __device__ __forceinline__ void dma16(const v4i& rsrc, uint32_t voffset, uint32_
                  : "memory");
 }
 
-template <typename T>
+template <typename T, typename OutT, bool EPI>
 __global__ void __launch_bounds__(256, 1)
-    gemm_tn_kernel(const T* __restrict__ A, const T* __restrict__ B, typename Mfma16<T>::acc_elem* __restrict__ C,
-                   int tiles_m, int tiles_n, int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc) {
+    gemm_tn_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
+                   int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi) {
     using AccV = typename Mfma32<T>::acc_t;
     typedef typename Mfma16<T>::acc_elem Acc;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TN_SLICE];  // [stage][A,B][row][128 B]
@@ -228,9 +230,11 @@ __global__ void __launch_bounds__(256, 1)
     const int rr = lane & 31;
     uint8_t* ep = smem + w * (32 * EP_PITCH);
     typedef Acc Acc4 __attribute__((ext_vector_type(4)));
-    Acc* cbase = C + ((int64_t)tm * TN_TILE + wm * 128) * ldc + (int64_t)tn * TN_TILE + wn * 128;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    const int64_t row0 = (int64_t)tm * TN_TILE + wm * 128, col0 = (int64_t)tn * TN_TILE + wn * 128;
+    OutT* cbase = C + row0 * ldc + col0;
+    // one row quarter i at a time; i is a template constant so that acc stays in registers
+    auto quarter = [&](auto itag) {
+        constexpr int i = decltype(itag)::value;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -244,11 +248,29 @@ __global__ void __launch_bounds__(256, 1)
         for (int t = 0; t < 16; ++t) {
             const int row = 2 * t + h;                       // 0..31 of this i
             const Acc4 v = *reinterpret_cast<const Acc4*>(ep + row * EP_PITCH + rr * 16);
-            *reinterpret_cast<Acc4*>(cbase + (int64_t)(32 * i + row) * ldc + 4 * rr) = v;
+            OutT* dst = cbase + (int64_t)(32 * i + row) * ldc + 4 * rr;
+            if constexpr (!EPI && std::is_same<OutT, Acc>::value) {
+                *reinterpret_cast<Acc4*>(dst) = v;
+            } else {
+                // the fused epilogue on 4 consecutive columns of one row, narrowed (RNE) to D's type
+                typedef OutT Out4 __attribute__((ext_vector_type(4)));
+                Out4 o;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    float x = (float)v[k];
+                    if constexpr (EPI) x = epi_apply(epi, row0 + 32 * i + row, col0 + 4 * rr + k, x);
+                    o[k] = narrow<OutT>(x);
+                }
+                *reinterpret_cast<Out4*>(dst) = o;
+            }
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next i overwrites
         __builtin_amdgcn_wave_barrier();
-    }
+    };
+    quarter(std::integral_constant<int, 0>{});
+    quarter(std::integral_constant<int, 1>{});
+    quarter(std::integral_constant<int, 2>{});
+    quarter(std::integral_constant<int, 3>{});
 }
 
 template <typename T>
@@ -267,13 +289,13 @@ bool tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, in
     return true;
 }
 
-template <typename T>
-int launch_gemm_tn(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
-                   int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s) {
+template <typename T, typename OutT, bool EPI>
+int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                   int64_t ldc, hipStream_t s, const Epilogue& epi) {
     const int tiles_m = (int)(M / TN_TILE), tiles_n = (int)(N / TN_TILE);
     const int ktiles = (int)(K / (TN_KB / (int64_t)sizeof(T)));
-    hipLaunchKernelGGL(gemm_tn_kernel<T>, dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s, A, B, C, tiles_m,
-                       tiles_n, ktiles, lda * (int64_t)sizeof(T), ldb * (int64_t)sizeof(T), ldc);
+    hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s, A, B,
+                       C, tiles_m, tiles_n, ktiles, lda * (int64_t)sizeof(T), ldb * (int64_t)sizeof(T), ldc, epi);
     LAVA_LAUNCH_CHECK("gemm_tn_kernel");
     return LAVA_HIP_OK;
 }
@@ -284,11 +306,18 @@ template bool tn_gemm_eligible<bf16>(const void*, const void*, const void*, int6
                                      int64_t, int64_t);
 template bool tn_gemm_eligible<int8_t>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t,
                                        int64_t, int64_t);
-template int launch_gemm_tn<f16>(const f16*, const f16*, float*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                 hipStream_t);
-template int launch_gemm_tn<bf16>(const bf16*, const bf16*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                  int64_t, hipStream_t);
-template int launch_gemm_tn<int8_t>(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, int64_t,
-                                    int64_t, int64_t, hipStream_t);
+#define LAVA_TN_INST(T, O, E)                                                                                      \
+    template int launch_gemm_tn<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, \
+                                         hipStream_t, const Epilogue&);
+LAVA_TN_INST(f16, float, false)
+LAVA_TN_INST(bf16, float, false)
+LAVA_TN_INST(int8_t, int32_t, false)
+LAVA_TN_INST(f16, float, true)
+LAVA_TN_INST(f16, f16, true)
+LAVA_TN_INST(f16, bf16, true)
+LAVA_TN_INST(bf16, float, true)
+LAVA_TN_INST(bf16, f16, true)
+LAVA_TN_INST(bf16, bf16, true)
+#undef LAVA_TN_INST
 
 }  // namespace lava

@@ -9,7 +9,7 @@ from ._lib import InvalidArgument, LavaHIPError, NoDevice, Unsupported, load
 from .device import Event, HIPDeviceArray, Stream, device_count, synchronize
 from .kernels import (coopmat_convert, coopmat_gemm_tiles, coopmat_muladd_16x16x16, coopmat_perelement_pair,
                       coopmat_perelement_rowcol, coopmat_reduce, dot4x8, fill_i8, fill_normal, fill_uniform,
-                      flash_attn_fwd, flash_attn_fwd_raw, gemm, gemm_raw, w8a16, w8a16_raw)
+                      flash_attn_fwd, flash_attn_fwd_raw, gemm, gemm_ex, gemm_ex_raw, gemm_raw, w8a16, w8a16_raw)
 from .vocabulary import (Accumulator, CoopMatReduce, DeviceCaps, MatrixA, MatrixB, MatrixShape, SubgroupScope,
                          WorkgroupScope, bestshape, caps, isbetter, library_shapes, matrix_shapes, supports,
                          supports_coopmat_perelement, supports_coopmat_reduce, supports_flexible_coopmat_shapes,

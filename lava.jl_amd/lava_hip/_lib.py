@@ -19,6 +19,7 @@ ERR_NO_DEVICE = -4
 
 # element type codes
 F16, BF16, F32, I8, U8, I32, U32 = 0, 1, 2, 3, 4, 5, 6
+ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2, 3
 
 A_ROWMAJOR, B_ROWMAJOR, C_ROWMAJOR = 1, 2, 4
 
@@ -88,6 +89,7 @@ PROTOTYPES: dict[str, tuple] = {
     "lava_hip_gemm_bf16_f32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_gemm_i8_i32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_coopmat_gemm_f16_tiles": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
+    "lava_hip_gemm_ex": (ci, [ci, ci, vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp, vp, i64, ci, vp]),
     "lava_hip_gemm_w8a16": (ci, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_flash_attn_fwd_f16": (ci, [vp, vp, vp, vp, i64, i64, i64, i64, C.POINTER(i64),
                                          C.POINTER(i64), C.c_float, ci, vp]),

@@ -49,6 +49,47 @@ def gemm(C_: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray, stream: Optio
     return C_
 
 
+_ACTS = {"none": _lib.ACT_NONE, "relu": _lib.ACT_RELU, "gelu_tanh": _lib.ACT_GELU_TANH,
+         "gelu_erf": _lib.ACT_GELU_ERF}
+_DCODE = {"f16": _lib.F16, "bf16": _lib.BF16, "f32": _lib.F32}
+
+
+def gemm_ex_raw(ab: str, d: str, A: int, B: int, D: int, M: int, N: int, K: int, lda: int, ldb: int, ldd: int,
+                layout: int, bias: int = 0, residual: int = 0, ldr: int = 0, act: str = "none",
+                stream: Optional[int] = None) -> None:
+    """D = act(A*B + (bias + residual)) narrowed to `d`, on raw device addresses."""
+    if act not in _ACTS:
+        raise ValueError(f"act must be one of {sorted(_ACTS)}")
+    if ab not in ("f16", "bf16") or d not in _DCODE:
+        raise _lib.Unsupported(_lib.ERR_UNSUPPORTED, f"no fused GEMM for {ab} -> {d}")
+    _lib.call("lava_hip_gemm_ex", _DCODE[ab], _DCODE[d], A, B, D, M, N, K, lda, ldb, ldd, layout, bias or None,
+              residual or None, ldr, _ACTS[act], stream)
+
+
+def gemm_ex(D: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray, bias: Optional[HIPDeviceArray] = None,
+            residual: Optional[HIPDeviceArray] = None, act: str = "none",
+            stream: Optional[int] = None) -> HIPDeviceArray:
+    """`D = act(A*B + (bias + residual))` with D fp32, fp16 or bf16: the GEMM epilogue family
+    fused into the store -- Lava's `accinit` (bias at stride 0, one value per row of D, plus
+    the residual, src/device/coopmat_intrinsics.jl:435-464), an elementwise getcomp/setcomp
+    epilogue (relu, gelu_tanh, gelu_erf) and the narrowing coopmat_convert (RNE)."""
+    if A.dtype != B.dtype:
+        raise ValueError(f"A is {A.dtype}, B is {B.dtype}")
+    M, K = A.dims
+    K2, N = B.dims
+    if K2 != K or D.dims != (M, N):
+        raise ValueError(f"shape mismatch: A {A.dims}, B {B.dims}, D {D.dims}")
+    if bias is not None and (bias.dtype != "f32" or bias.size != M):
+        raise ValueError("bias must be an f32 vector of length M (one value per row of D)")
+    if residual is not None and (residual.dtype != "f32" or residual.dims != (M, N) or residual.order != D.order):
+        raise ValueError("residual must be an f32 M x N array in D's order")
+    layout = (1 if A.order == "C" else 0) | (2 if B.order == "C" else 0) | (4 if D.order == "C" else 0)
+    gemm_ex_raw(A.dtype, D.dtype, A.ptr, B.ptr, D.ptr, M, N, K, _ld(A), _ld(B), _ld(D), layout,
+                bias.ptr if bias is not None else 0, residual.ptr if residual is not None else 0,
+                _ld(residual) if residual is not None else 0, act, stream)
+    return D
+
+
 def coopmat_gemm_tiles(C_: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray,
                        stream: Optional[int] = None) -> HIPDeviceArray:
     """The 16x16x16 vocabulary-tile GEMM of docs/src/device.md:81-88 (fp16 -> fp32)."""

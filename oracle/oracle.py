@@ -20,6 +20,8 @@ import os
 import subprocess
 from pathlib import Path
 
+import math
+
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
@@ -227,6 +229,50 @@ def reduce_smear(m: np.ndarray, mask: int, combine: str) -> np.ndarray:
     if mask & 2:
         x = np.broadcast_to(f(x, axis=0, keepdims=True), x.shape)
     return np.array(x)
+
+
+# ---- GEMM epilogue ----------------------------------------------------------------------------
+def gelu_tanh(x: np.ndarray) -> np.ndarray:
+    """0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))), fp64."""
+    x = np.asarray(x, dtype=np.float64)
+    return 0.5 * x * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x ** 3)))
+
+
+def gelu_erf(x: np.ndarray) -> np.ndarray:
+    """0.5 x (1 + erf(x / sqrt 2)), fp64 (math.erf per element)."""
+    x = np.asarray(x, dtype=np.float64)
+    erf = np.frompyfunc(math.erf, 1, 1)
+    return 0.5 * x * (1.0 + erf(x / math.sqrt(2.0)).astype(np.float64))
+
+
+ACTS = {"none": lambda x: x, "relu": lambda x: np.maximum(x, 0.0), "gelu_tanh": gelu_tanh, "gelu_erf": gelu_erf}
+
+
+def gemm_epilogue(c: np.ndarray, bias=None, residual=None, act: str = "none") -> np.ndarray:
+    """D = act(C + (bias[row] + residual)) in fp64, C = A*B.  The accumulator init is
+    Lava's `accinit`: bias loaded at stride 0 (one value per row, every column reading
+    the same vector) plus the residual, summed with coopmat_add
+    (src/device/coopmat_intrinsics.jl:435-464); act is the elementwise getcomp/setcomp
+    epilogue (:322-400)."""
+    init = np.zeros(c.shape, dtype=np.float64)
+    if bias is not None:
+        init = init + np.asarray(bias, dtype=np.float64)[:, None]
+    if residual is not None:
+        init = init + np.asarray(residual, dtype=np.float64)
+    return ACTS[act](np.asarray(c, dtype=np.float64) + init)
+
+
+def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
+    """fp64 -> fp32 -> dtype (RNE at each step, coopmat_convert of the fp32 accumulator,
+    src/compiler/spirv/coopmat.jl:783-824), returned as fp64 values."""
+    x32 = np.asarray(x, dtype=np.float32)
+    if dtype == "f32":
+        return x32.astype(np.float64)
+    if dtype == "f16":
+        return x32.astype(np.float16).astype(np.float64)
+    if dtype == "bf16":
+        return bf16_bits_to_f32(f32_to_bf16_bits(x32)).astype(np.float64)
+    raise ValueError(dtype)
 
 
 def rel_frobenius(x: np.ndarray, ref: np.ndarray) -> float:

@@ -276,3 +276,39 @@ def test_perelement_and_reduce_definitions(oracle, golden):
     assert np.all(both == 0)
     p = oracle.perelement_pair(m, m.T.copy())
     assert p[2, 5] == max(m[2, 5], m[5, 2]) + 2 - 5
+
+
+# ---------------------------------------------------------------- GEMM epilogue
+def test_gelu_closed_forms(oracle):
+    """erf form: gelu(x) = x Phi(x) -- Phi(1) = 0.8413447460685429 (standard normal
+    CDF at 1), gelu(0) = 0, gelu(x) -> x and -> 0 far out; the tanh form is the
+    published approximation, within 1e-3 of the erf form on [-6, 6]."""
+    x = np.array([0.0, 1.0, -1.0, 8.0, -8.0])
+    ge = oracle.gelu_erf(x)
+    assert ge[0] == 0.0
+    assert abs(ge[1] - 0.8413447460685429) < 1e-15
+    assert abs(ge[2] - (-1.0 + 0.8413447460685429)) < 1e-15   # gelu(-x) = gelu(x) - x
+    assert abs(ge[3] - 8.0) < 1e-12 and abs(ge[4]) < 1e-12
+    t = np.linspace(-6, 6, 1201)
+    assert np.abs(oracle.gelu_tanh(t) - oracle.gelu_erf(t)).max() < 1e-3
+    assert abs(oracle.gelu_tanh(np.array([1.0]))[0] - 0.8411919906082768) < 1e-15
+
+
+def test_gemm_epilogue_accinit_axes(oracle):
+    """bias is one value per row (a stride-0 accumulator load: every column reads the
+    same vector), the residual is added elementwise, the activation comes last."""
+    c = np.arange(12, dtype=np.float64).reshape(3, 4) - 6.0
+    bias = np.array([10.0, -20.0, 0.5])
+    res = np.full((3, 4), 0.25)
+    d = oracle.gemm_epilogue(c, bias, res, "relu")
+    np.testing.assert_array_equal(d, np.maximum(c + bias[:, None] + 0.25, 0.0))
+    # planted mistake: a bias broadcast along columns gives a different matrix
+    assert not np.array_equal(d, np.maximum(c + np.resize(bias, 4)[None, :] + 0.25, 0.0))
+    np.testing.assert_array_equal(oracle.gemm_epilogue(c), c)
+
+
+def test_round_to_rne(oracle):
+    x = np.array([1.0 + 2.0 ** -9, 1.0 + 3 * 2.0 ** -9, 65504.0, 1.0 + 2.0 ** -11])
+    assert oracle.round_to(x[:2], "bf16").tolist() == [1.0, 1.0078125]
+    assert oracle.round_to(x[2:], "f16").tolist() == [65504.0, 1.0]   # tie to even
+    assert oracle.round_to(np.array([0.1]), "f32")[0] == float(np.float32(0.1))
