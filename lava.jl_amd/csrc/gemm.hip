@@ -75,6 +75,7 @@ int gemm_ex_entry(const void* A, const void* B, void* D, int64_t M, int64_t N, i
     epi.residual = residual;
     epi.ldr = ldr;
     epi.act = act;
+    epi.vec4 = aligned(bias, 16) && aligned(residual, 16) && ldr % 4 == 0;
     return gemm_entry<T, OutT, true>("gemm_ex", A, B, D, M, N, K, lda, ldb, ldd, layout, stream, epi);
 }
 

@@ -233,8 +233,33 @@ __global__ void __launch_bounds__(256, 1)
     const int64_t row0 = (int64_t)tm * TN_TILE + wm * 128, col0 = (int64_t)tn * TN_TILE + wn * 128;
     OutT* cbase = C + row0 * ldc + col0;
     // one row quarter i at a time; i is a template constant so that acc stays in registers
+    typedef float F4 __attribute__((ext_vector_type(4)));
     auto quarter = [&](auto itag) {
         constexpr int i = decltype(itag)::value;
+        // The epilogue's init terms for the 16 rows x 4 columns this lane finishes, all
+        // requested before the staging so that their HBM latency overlaps it (loaded one
+        // row at a time inside the store loop they cost one round trip per row).
+        F4 rin[EPI ? 16 : 1];
+        float bin[EPI ? 16 : 1];
+        F4 bcol = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (EPI) {
+            const int64_t n = col0 + 4 * rr;
+            if (epi.bias && epi.bias_on_cols) {
+                const float* p = epi.bias + n;
+                bcol = epi.vec4 ? *reinterpret_cast<const F4*>(p) : F4{p[0], p[1], p[2], p[3]};
+            }
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int64_t m = row0 + 32 * i + 2 * t + h;
+                rin[t] = F4{0.f, 0.f, 0.f, 0.f};
+                bin[t] = 0.f;
+                if (epi.residual) {
+                    const float* p = epi.residual + m * epi.ldr + n;
+                    rin[t] = epi.vec4 ? *reinterpret_cast<const F4*>(p) : F4{p[0], p[1], p[2], p[3]};
+                }
+                if (epi.bias && !epi.bias_on_cols) bin[t] = epi.bias[m];
+            }
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -244,25 +269,39 @@ __global__ void __launch_bounds__(256, 1)
             }
         __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's staged rows are in LDS
         __builtin_amdgcn_wave_barrier();
+        auto store_rows = [&](auto acttag) {
+            constexpr int ACT = decltype(acttag)::value;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const int row = 2 * t + h;                       // 0..31 of this i
-            const Acc4 v = *reinterpret_cast<const Acc4*>(ep + row * EP_PITCH + rr * 16);
-            OutT* dst = cbase + (int64_t)(32 * i + row) * ldc + 4 * rr;
-            if constexpr (!EPI && std::is_same<OutT, Acc>::value) {
-                *reinterpret_cast<Acc4*>(dst) = v;
-            } else {
-                // the fused epilogue on 4 consecutive columns of one row, narrowed (RNE) to D's type
-                typedef OutT Out4 __attribute__((ext_vector_type(4)));
-                Out4 o;
+            for (int t = 0; t < 16; ++t) {
+                const int row = 2 * t + h;                       // 0..31 of this i
+                const Acc4 v = *reinterpret_cast<const Acc4*>(ep + row * EP_PITCH + rr * 16);
+                OutT* dst = cbase + (int64_t)(32 * i + row) * ldc + 4 * rr;
+                if constexpr (!EPI && std::is_same<OutT, Acc>::value) {
+                    *reinterpret_cast<Acc4*>(dst) = v;
+                } else {
+                    // the fused epilogue on 4 consecutive columns of one row, narrowed (RNE) to D's type
+                    typedef OutT Out4 __attribute__((ext_vector_type(4)));
+                    Out4 o;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    float x = (float)v[k];
-                    if constexpr (EPI) x = epi_apply(epi, row0 + 32 * i + row, col0 + 4 * rr + k, x);
-                    o[k] = narrow<OutT>(x);
+                    for (int k = 0; k < 4; ++k) {
+                        float x = (float)v[k];
+                        // the same fp32 sums as epi_apply: (bias + residual), then acc + that
+                        if constexpr (EPI) x = epi_act_c<ACT>(x + ((bin[t] + bcol[k]) + rin[t][k]));
+                        o[k] = narrow<OutT>(x);
+                    }
+                    *reinterpret_cast<Out4*>(dst) = o;
                 }
-                *reinterpret_cast<Out4*>(dst) = o;
             }
+        };
+        if constexpr (EPI) {
+            switch (epi.act) {   // uniform: one branch per quarter, none per element
+            case EPI_RELU: store_rows(std::integral_constant<int, EPI_RELU>{}); break;
+            case EPI_GELU_TANH: store_rows(std::integral_constant<int, EPI_GELU_TANH>{}); break;
+            case EPI_GELU_ERF: store_rows(std::integral_constant<int, EPI_GELU_ERF>{}); break;
+            default: store_rows(std::integral_constant<int, EPI_NONE>{}); break;
+            }
+        } else {
+            store_rows(std::integral_constant<int, EPI_NONE>{});
         }
         __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next i overwrites
         __builtin_amdgcn_wave_barrier();
