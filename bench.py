@@ -9,7 +9,8 @@ tensors of the parity tests, generated on the device and resident in HBM
 before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-                  [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|copy]
+                  [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|
+                              gemm_bf16_ragged|copy]
 
 A step is one kernel launch over the whole problem.  Kernel time comes from HIP
 events recorded on the launch stream around the K timed launches; wall time
@@ -72,11 +73,12 @@ def roofline(bound, achieved, peak, unit, traffic):
 
 
 # ---------------------------------------------------------------- workloads
-def bench_gemm(lh, dt, n, steps, warmup, stream, cfg):
-    A = lh.HIPDeviceArray(dt, (n, n), order="C")
-    B = lh.HIPDeviceArray(dt, (n, n), order="F")
+def bench_gemm(lh, dt, n, steps, warmup, stream, cfg, shape=None):
+    M, N, Kd = shape if shape is not None else (n, n, n)
+    A = lh.HIPDeviceArray(dt, (M, Kd), order="C")
+    B = lh.HIPDeviceArray(dt, (Kd, N), order="F")
     acc = "i32" if dt == "i8" else "f32"
-    C = lh.HIPDeviceArray(acc, (n, n), order="C")
+    C = lh.HIPDeviceArray(acc, (M, N), order="C")
     if dt == "i8":
         lh.fill_i8(A, lh.seed(cfg, 0))
         lh.fill_i8(B, lh.seed(cfg, 1))
@@ -85,7 +87,7 @@ def bench_gemm(lh, dt, n, steps, warmup, stream, cfg):
         lh.fill_uniform(B, lh.seed(cfg, 1), -1.0, 1.0)
     lh.synchronize()
     kern_ms, wall_ms = timed(lh, lambda: lh.gemm(C, A, B, stream=stream), steps, warmup, stream)
-    flop = 2.0 * n ** 3
+    flop = 2.0 * M * N * Kd
     return flop, kern_ms, wall_ms
 
 
@@ -193,7 +195,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
-                             "gemm_ex_bf16", "copy"])
+                             "gemm_ex_bf16", "gemm_bf16_ragged", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -235,6 +237,13 @@ def main():
         flop, kms, wms = bench_gemm(lh, "bf16", 4096, K, W, stream, 1)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16", "config": {"workload": "bf16 GEMM 4096^3 A row-major B column-major"},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "gemm_bf16_ragged":
+        flop, kms, wms = bench_gemm(lh, "bf16", 0, K, W, stream, 1, shape=(8000, 8000, 8000))
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "bf16", "config": {"workload": "bf16 GEMM M=N=K=8000 (not a tile multiple: "
+                                                            "zero-clamped loads, bounds-checked store)"},
                     "kernel_ms": round(kms, 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_ex_bf16":

@@ -3,7 +3,8 @@
 // A column-major C is handled as its row-major transpose, C^T = B^T A^T, which
 // swaps the operands and flips their layouts; so every kernel writes row-major C.
 // The compute-bound shapes with K-contiguous operands (A row-major, B
-// column-major: the bf16 configuration) take the TN kernel; everything else the
+// column-major: the bf16 configuration) take the TN kernel -- whole tiles, or any
+// M and N and K a multiple of 16 bytes with zero-clamped loads; everything else the
 // staged kernel.
 #include <hip/hip_runtime.h>
 
@@ -56,8 +57,8 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     }
     hipStream_t s = as_stream(stream);
     Acc* c = static_cast<Acc*>(C);
-    if (arow && !brow && tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc))
-        return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi);
+    const int fit = arow && !brow ? tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT)) : TN_NO;
+    if (fit != TN_NO) return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, fit == TN_RAGGED);
     return launch_gemm_staged<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
 }
 

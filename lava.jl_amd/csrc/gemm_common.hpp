@@ -116,6 +116,14 @@ struct Epilogue {
     int vec4 = 0;                      // bias and residual 16-byte aligned, ldr % 4 == 0: 4 columns per load
 };
 
+// The extents a RAGGED TN launch checks against: M, N, K in bytes, and whether C rows
+// take 4-element vector stores (ldc % 4 == 0, C aligned to 4 elements).
+struct TnBounds {
+    int64_t m = 0, n = 0;
+    int kb = 0;
+    int cvec = 0;
+};
+
 // Inline elementary functions (a library call here would have to save the 256
 // accumulator registers that are still live around the epilogue):
 // e^x through v_exp_f32; tanh(u) = sign(u) (1 - e^{-2|u|}) / (1 + e^{-2|u|});

@@ -17,12 +17,14 @@ int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_
                          int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s);
 
 // The fast path: A row-major (M x K), B column-major (K x N) -- both K-contiguous --
-// C row-major.  Requires tn_gemm_eligible().
+// C row-major.  tn_gemm_eligible() says whether it applies: TN_FULL for whole 256 x 256
+// tiles and 64-element K steps, TN_RAGGED for other extents (K a multiple of 16 bytes).
+enum TnFit : int { TN_NO = 0, TN_FULL = 1, TN_RAGGED = 2 };
 template <typename T>
-bool tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-                      int64_t ldb, int64_t ldc);
+int tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                     int64_t ldb, int64_t ldc, size_t c_elem);
 template <typename T, typename OutT, bool EPI>
 int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                   int64_t ldc, hipStream_t s, const Epilogue& epi);
+                   int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged);
 
 }  // namespace lava

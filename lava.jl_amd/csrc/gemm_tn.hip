@@ -27,7 +27,13 @@
 //    lane's accumulator holds runs of 4 consecutive columns of one row of C; the
 //    epilogue stages them through LDS and stores whole 512-byte row runs;
 //  * workgroups are renumbered XCD by XCD (xcd_tile) so that the tiles one XCD
-//    runs together share rows of A and columns of B in its L2.
+//    runs together share rows of A and columns of B in its L2;
+//  * ragged extents (the RAGGED instances; Lava's TENSOR_CLAMP_CONSTANT layout with
+//    the default zero, src/vocabulary/tensor.jl:44-51): a lane whose row lies past M
+//    (A) or N (B), or whose 16-byte K chunk lies past K, gets a lane offset beyond the
+//    buffer resource's range, so its load reads zero instead of memory; the store and
+//    the epilogue's operand loads are bounds-checked.  K must be a multiple of the
+//    16-byte chunk (8 f16/bf16, 16 int8) so that a chunk is wholly in or out.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -74,10 +80,10 @@ __device__ __forceinline__ void dma16(const v4i& rsrc, uint32_t voffset, uint32_
                  : "memory");
 }
 
-template <typename T, typename OutT, bool EPI>
+template <typename T, typename OutT, bool EPI, bool RAGGED>
 __global__ void __launch_bounds__(256, 1)
     gemm_tn_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
-                   int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi) {
+                   int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi, TnBounds bnd) {
     using AccV = typename Mfma32<T>::acc_t;
     typedef typename Mfma16<T>::acc_elem Acc;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TN_SLICE];  // [stage][A,B][row][128 B]
@@ -96,22 +102,40 @@ __global__ void __launch_bounds__(256, 1)
     // A slice rows tm*256 .. +256 and B slice rows tn*256 .. +256 as buffer resources;
     // each lane keeps one 32-bit row offset per chunk parity, the row step (8 i rows)
     // and the k offset are wave-uniform and travel in soffset.
+    // Rows of this tile inside the matrix: all 256 unless RAGGED and the tile is the last.
+    int a_rows = TN_TILE, b_rows = TN_TILE;
+    if constexpr (RAGGED) {
+        a_rows = (int)(bnd.m - (int64_t)tm * TN_TILE < TN_TILE ? bnd.m - (int64_t)tm * TN_TILE : TN_TILE);
+        b_rows = (int)(bnd.n - (int64_t)tn * TN_TILE < TN_TILE ? bnd.n - (int64_t)tn * TN_TILE : TN_TILE);
+    }
     const v4i rs_a =
-        make_rsrc(reinterpret_cast<const char*>(A) + (int64_t)tm * TN_TILE * lda_b, (uint32_t)(TN_TILE * lda_b));
+        make_rsrc(reinterpret_cast<const char*>(A) + (int64_t)tm * TN_TILE * lda_b, (uint32_t)(a_rows * lda_b));
     const v4i rs_b =
-        make_rsrc(reinterpret_cast<const char*>(B) + (int64_t)tn * TN_TILE * ldb_b, (uint32_t)(TN_TILE * ldb_b));
+        make_rsrc(reinterpret_cast<const char*>(B) + (int64_t)tn * TN_TILE * ldb_b, (uint32_t)(b_rows * ldb_b));
     const uint32_t a_row = (uint32_t)((64 * w + lr) * lda_b), b_row = (uint32_t)((64 * w + lr) * ldb_b);
     const uint32_t a_off[2] = {a_row + 16u * c_even, a_row + 16u * c_odd};
     const uint32_t b_off[2] = {b_row + 16u * c_even, b_row + 16u * c_odd};
     const uint32_t a_step = (uint32_t)(8 * lda_b), b_step = (uint32_t)(8 * ldb_b);
     const uint32_t lds0 = lds_addr(smem) + w * 64 * TN_KB;
+    // RAGGED: instruction i's row is inside the tile iff 8 i < *_lim; chunk parity p's
+    // last byte is inside K iff kofs + kend[p] <= K bytes.  A masked lane's offset is
+    // OOB_OFS: past every range here (num_records < 2^31), and OOB_OFS + soffset
+    // (< 2^31) does not wrap, whether or not the range check counts soffset.
+    const int a_lim = a_rows - 64 * w - lr, b_lim = b_rows - 64 * w - lr;
+    const int kend[2] = {16 * c_even + 16, 16 * c_odd + 16};
+    constexpr uint32_t OOB_OFS = 0x80000000u;
 
     // DMA load q (0..15) of a k-tile into `stage`: q < 8 are A rows 8q.., q >= 8 B rows.
     auto dma = [&](int q, int stage, uint32_t kofs) {
         const int i = q & 7;
         const uint32_t dst = lds0 + stage * 2 * TN_SLICE + (q >> 3) * TN_SLICE + i * 1024;
-        if (q < 8) dma16(rs_a, a_off[i & 1], i * a_step + kofs, dst);
-        else dma16(rs_b, b_off[i & 1], i * b_step + kofs, dst);
+        uint32_t off = q < 8 ? a_off[i & 1] : b_off[i & 1];
+        if constexpr (RAGGED) {
+            const bool in = 8 * i < (q < 8 ? a_lim : b_lim) && (int)kofs + kend[i & 1] <= bnd.kb;
+            off = in ? off : OOB_OFS;
+        }
+        if (q < 8) dma16(rs_a, off, i * a_step + kofs, dst);
+        else dma16(rs_b, off, i * b_step + kofs, dst);
     };
 
     // ---- fragments: 32x32 MFMA operands, 16 bytes per lane.  Operand row = base +
@@ -232,6 +256,12 @@ __global__ void __launch_bounds__(256, 1)
     typedef Acc Acc4 __attribute__((ext_vector_type(4)));
     const int64_t row0 = (int64_t)tm * TN_TILE + wm * 128, col0 = (int64_t)tn * TN_TILE + wn * 128;
     OutT* cbase = C + row0 * ldc + col0;
+    // columns of this lane's 4-column group inside the matrix (RAGGED: 0..4)
+    int cols_in = 4;
+    if constexpr (RAGGED) {
+        const int64_t left = bnd.n - (col0 + 4 * rr);
+        cols_in = left >= 4 ? 4 : (left > 0 ? (int)left : 0);
+    }
     // one row quarter i at a time; i is a template constant so that acc stays in registers
     typedef float F4 __attribute__((ext_vector_type(4)));
     auto quarter = [&](auto itag) {
@@ -244,19 +274,23 @@ __global__ void __launch_bounds__(256, 1)
         F4 bcol = {0.f, 0.f, 0.f, 0.f};
         if constexpr (EPI) {
             const int64_t n = col0 + 4 * rr;
-            if (epi.bias && epi.bias_on_cols) {
-                const float* p = epi.bias + n;
-                bcol = epi.vec4 ? *reinterpret_cast<const F4*>(p) : F4{p[0], p[1], p[2], p[3]};
-            }
+            // 4 floats at p, or those of them inside the matrix (columns < N)
+            auto ld4 = [&](const float* p) {
+                if (epi.vec4 && cols_in == 4) return *reinterpret_cast<const F4*>(p);
+                F4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k < cols_in) r[k] = p[k];
+                return r;
+            };
+            if (epi.bias && epi.bias_on_cols) bcol = ld4(epi.bias + n);
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
                 const int64_t m = row0 + 32 * i + 2 * t + h;
                 rin[t] = F4{0.f, 0.f, 0.f, 0.f};
                 bin[t] = 0.f;
-                if (epi.residual) {
-                    const float* p = epi.residual + m * epi.ldr + n;
-                    rin[t] = epi.vec4 ? *reinterpret_cast<const F4*>(p) : F4{p[0], p[1], p[2], p[3]};
-                }
+                if (RAGGED && m >= bnd.m) continue;
+                if (epi.residual) rin[t] = ld4(epi.residual + m * epi.ldr + n);
                 if (epi.bias && !epi.bias_on_cols) bin[t] = epi.bias[m];
             }
         }
@@ -276,8 +310,15 @@ __global__ void __launch_bounds__(256, 1)
                 const int row = 2 * t + h;                       // 0..31 of this i
                 const Acc4 v = *reinterpret_cast<const Acc4*>(ep + row * EP_PITCH + rr * 16);
                 OutT* dst = cbase + (int64_t)(32 * i + row) * ldc + 4 * rr;
+                if (RAGGED && row0 + 32 * i + row >= bnd.m) continue;
                 if constexpr (!EPI && std::is_same<OutT, Acc>::value) {
-                    *reinterpret_cast<Acc4*>(dst) = v;
+                    if (!RAGGED || (cols_in == 4 && bnd.cvec)) {
+                        *reinterpret_cast<Acc4*>(dst) = v;
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (k < cols_in) dst[k] = v[k];
+                    }
                 } else {
                     // the fused epilogue on 4 consecutive columns of one row, narrowed (RNE) to D's type
                     typedef OutT Out4 __attribute__((ext_vector_type(4)));
@@ -289,7 +330,13 @@ __global__ void __launch_bounds__(256, 1)
                         if constexpr (EPI) x = epi_act_c<ACT>(x + ((bin[t] + bcol[k]) + rin[t][k]));
                         o[k] = narrow<OutT>(x);
                     }
-                    *reinterpret_cast<Out4*>(dst) = o;
+                    if (!RAGGED || (cols_in == 4 && bnd.cvec)) {
+                        *reinterpret_cast<Out4*>(dst) = o;
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (k < cols_in) dst[k] = o[k];
+                    }
                 }
             }
         };
@@ -313,41 +360,57 @@ __global__ void __launch_bounds__(256, 1)
 }
 
 template <typename T>
-bool tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-                      int64_t ldb, int64_t ldc) {
-    const int64_t ke = TN_KB / (int64_t)sizeof(T);
-    if (M <= 0 || N <= 0 || K <= 0) return false;
-    if (M % TN_TILE || N % TN_TILE || K % ke) return false;
-    if ((M / TN_TILE) * (N / TN_TILE) > 0x7fffffff || K / ke > 0x7fffffff) return false;
-    if ((lda * (int64_t)sizeof(T)) % 16 || (ldb * (int64_t)sizeof(T)) % 16 || ldc % 4) return false;
+int tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                     int64_t ldb, int64_t ldc, size_t c_elem) {
+    const int64_t ke = TN_KB / (int64_t)sizeof(T), chunk = 16 / (int64_t)sizeof(T);
+    if (M <= 0 || N <= 0 || K <= 0 || K % chunk) return TN_NO;
+    const int64_t tiles_m = (M + TN_TILE - 1) / TN_TILE, tiles_n = (N + TN_TILE - 1) / TN_TILE;
+    if (tiles_m * tiles_n > 0x7fffffff || (K + ke - 1) / ke > 0x7fffffff || K * (int64_t)sizeof(T) > 0x7fffffff)
+        return TN_NO;
+    if ((lda * (int64_t)sizeof(T)) % 16 || (ldb * (int64_t)sizeof(T)) % 16) return TN_NO;
     // buffer offsets are 32-bit: a 256-row slab of A or B must span < 2 GiB
     if ((int64_t)TN_TILE * lda * (int64_t)sizeof(T) >= ((int64_t)1 << 31) ||
         (int64_t)TN_TILE * ldb * (int64_t)sizeof(T) >= ((int64_t)1 << 31))
-        return false;
-    if (!aligned(A, 16) || !aligned(B, 16) || !aligned(C, 16)) return false;
-    return true;
+        return TN_NO;
+    if (!aligned(A, 16) || !aligned(B, 16)) return TN_NO;
+    if (M % TN_TILE == 0 && N % TN_TILE == 0 && K % ke == 0 && ldc % 4 == 0 && aligned(C, 4 * c_elem))
+        return TN_FULL;
+    // ragged: worth the 256 x 256 tiles once the product is no longer launch-bound
+    return M * N >= (int64_t)TN_TILE * TN_TILE ? TN_RAGGED : TN_NO;
 }
 
 template <typename T, typename OutT, bool EPI>
 int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                   int64_t ldc, hipStream_t s, const Epilogue& epi) {
-    const int tiles_m = (int)(M / TN_TILE), tiles_n = (int)(N / TN_TILE);
-    const int ktiles = (int)(K / (TN_KB / (int64_t)sizeof(T)));
-    hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s, A, B,
-                       C, tiles_m, tiles_n, ktiles, lda * (int64_t)sizeof(T), ldb * (int64_t)sizeof(T), ldc, epi);
+                   int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged) {
+    const int tiles_m = (int)((M + TN_TILE - 1) / TN_TILE), tiles_n = (int)((N + TN_TILE - 1) / TN_TILE);
+    const int64_t ke = TN_KB / (int64_t)sizeof(T);
+    const int ktiles = (int)((K + ke - 1) / ke);
+    TnBounds bnd;
+    bnd.m = M;
+    bnd.n = N;
+    bnd.kb = (int)(K * (int64_t)sizeof(T));
+    bnd.cvec = ldc % 4 == 0 && aligned(C, 4 * sizeof(OutT));
+    if (ragged)
+        hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
+                           A, B, C, tiles_m, tiles_n, ktiles, lda * (int64_t)sizeof(T), ldb * (int64_t)sizeof(T), ldc,
+                           epi, bnd);
+    else
+        hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI, false>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
+                           s, A, B, C, tiles_m, tiles_n, ktiles, lda * (int64_t)sizeof(T), ldb * (int64_t)sizeof(T),
+                           ldc, epi, bnd);
     LAVA_LAUNCH_CHECK("gemm_tn_kernel");
     return LAVA_HIP_OK;
 }
 
-template bool tn_gemm_eligible<f16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                    int64_t);
-template bool tn_gemm_eligible<bf16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t,
-                                     int64_t, int64_t);
-template bool tn_gemm_eligible<int8_t>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t,
-                                       int64_t, int64_t);
+template int tn_gemm_eligible<f16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                   int64_t, size_t);
+template int tn_gemm_eligible<bf16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t,
+                                    int64_t, int64_t, size_t);
+template int tn_gemm_eligible<int8_t>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t,
+                                      int64_t, int64_t, size_t);
 #define LAVA_TN_INST(T, O, E)                                                                                      \
     template int launch_gemm_tn<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, \
-                                         hipStream_t, const Epilogue&);
+                                         hipStream_t, const Epilogue&, bool);
 LAVA_TN_INST(f16, float, false)
 LAVA_TN_INST(bf16, float, false)
 LAVA_TN_INST(int8_t, int32_t, false)
