@@ -174,6 +174,63 @@ int lava_hip_coopmat_convert(const float* in, void* out, int out_dtype, int64_t 
 /* y[i] = dot4x8(a[i], b[i]) (src/vocabulary/vocabulary.jl:31-35). */
 int lava_hip_dot4x8(const uint32_t* a, const uint32_t* b, int32_t* y, int64_t n, void* stream);
 
+/* ---- tensor addressing (src/vocabulary/tensor.jl:1-115; lowered in
+ * src/device/tensor_intrinsics.jl) ---- */
+/* Clamp modes, the values of TENSOR_CLAMP_UNDEFINED / _CONSTANT / _TO_EDGE (tensor.jl:44-51). */
+#define LAVA_HIP_CLAMP_UNDEFINED 0u
+#define LAVA_HIP_CLAMP_CONSTANT 1u
+#define LAVA_HIP_CLAMP_TO_EDGE 2u
+
+/* A TensorLayout as plain data: what tensor_layout(Val(rank), Val(clamp)) followed by
+ * tensor_setdim, tensor_setstride, tensor_setclampvalue and tensor_slice builds
+ * (tensor.jl:52-93).  Arrays are outermost first, innermost last, first `rank` entries
+ * used.  dim: extents; stride: element strides (a packed tensor has stride[rank-1] = 1);
+ * off / size: the slice, 0-based (off may be negative); clampbits: the clamp constant's
+ * bits in the matrix's component type, zero-extended (tensor_clampbits, tensor.jl:83-85).
+ * The matrix's (row, col) is the slice's coordinate in the last two dimensions; outer
+ * dimensions must have slice size 1. */
+typedef struct lava_hip_tensor_layout {
+    int32_t rank;
+    uint32_t clamp;
+    uint32_t clampbits;
+    int32_t dim[4];
+    int32_t stride[4];
+    int32_t off[4];
+    int32_t size[4];
+} lava_hip_tensor_layout;
+
+/* Fragment shapes of the tile entry points (MatrixA R x K, MatrixB K x C, Accumulator). */
+#define LAVA_HIP_TILE_A_16x16 0
+#define LAVA_HIP_TILE_B_16x16 1
+#define LAVA_HIP_TILE_ACC_16x16 2
+#define LAVA_HIP_TILE_ACC_32x32 3
+#define LAVA_HIP_TILE_A_32x16 4
+#define LAVA_HIP_TILE_B_16x32 5
+
+/* m = tensor_load(object, src, layout[, view]) on one fragment, then stored row-major to
+ * `out` (R x C, dtype LAVA_HIP_F16 or LAVA_HIP_F32).  `object` (R x C, row-major) is the
+ * matrix whose values elements outside the slice keep; elements inside the slice but
+ * outside the tensor read the clamp constant (CONSTANT, UNDEFINED) or the nearest element
+ * (TO_EDGE).  transpose != 0 loads through the (1, 0) TensorView.
+ * Replaces lava_tensor_load (src/device/tensor_intrinsics.jl:258-320) and KernelInterface's
+ * tensor_load (tensor.jl:98-105). */
+int lava_hip_tensor_load_tile(int dtype, int shape, const void* src, const lava_hip_tensor_layout* layout,
+                              int transpose, const void* object, void* out, void* stream);
+
+/* tensor_store(m, dst, layout[, view]) of the fragment read row-major from `in`: only
+ * elements inside both the slice and the tensor are written (the clamping store,
+ * src/device/tensor_intrinsics.jl:329-402; tensor.jl:107-108). */
+int lava_hip_tensor_store_tile(int dtype, int shape, const void* in, void* dst, const lava_hip_tensor_layout* layout,
+                               int transpose, void* stream);
+
+/* D (16 x 16 fp32, row-major) = A * B, with A (fp16 MatrixA 16x16) and B (fp16 MatrixB
+ * 16x16) loaded through layouts (B optionally through the transposing view).  With B's
+ * layout TENSOR_CLAMP_CONSTANT and a clamp value of one, the columns of B past the tensor
+ * read one and those columns of D are the row sums of A: the attention V-padding trick of
+ * src/device/tensor_intrinsics.jl:139-155. */
+int lava_hip_tensor_muladd_16x16x16(const void* A, const lava_hip_tensor_layout* layout_a, const void* B,
+                                    const lava_hip_tensor_layout* layout_b, int transpose_b, float* D, void* stream);
+
 /* ========================================================================= */
 /* Kernels                                                                    */
 /* ========================================================================= */
@@ -194,6 +251,16 @@ int lava_hip_gemm_bf16_f32(const void* A, const void* B, void* C, int64_t M, int
  * exact with two's-complement wrap of the 32-bit accumulator. */
 int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
+
+/* The coopmat2 (tensor-addressed, workgroup-scope) GEMM: C = fp16(A B), fp32 accumulate.
+ * A (M x K) and B (K x N) fp16 row-major, read straight from memory through zero-clamped
+ * layouts sliced per 128 x 128 block with K steps of 64, so any M, N, K works unpadded;
+ * C row-major M x N (ldc >= N) or, with transpose_c != 0, C^T stored row-major N x M
+ * (ldc >= M) through the transposing view.  Extents and leading dimensions < 2^31.
+ * Replaces `gemm_cm2!` / test/glsl/coopmat2_gemm_regs.comp:37-84 (push block
+ * {pa, pb, pc, M, N, K}), with the view store of tensor_intrinsics.jl:371-402. */
+int lava_hip_gemm_cm2_f16(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                          int64_t ldb, int64_t ldc, int transpose_c, void* stream);
 
 /* ---- fused GEMM epilogue: activations (elementwise epilogues that Lava writes with
  * coopmat_length / getcomp / setcomp, src/device/coopmat_intrinsics.jl:322-400) ---- */

@@ -180,9 +180,10 @@ def supports_flexible_coopmat_shapes(backend=None) -> bool:
 
 
 def supports_tensor_addressing(backend=None) -> bool:
-    """No SPV_NV_tensor_addressing equivalent is exposed at the device level; the
-    kernels clamp their own tile loads instead."""
-    return False
+    """The tensor-addressing vocabulary (layouts, clamp modes, slices, the transposing
+    view; tensor.jl:109-115) is implemented natively: lava_tensor.hpp on the device,
+    lava_hip.tensor on the host."""
+    return True
 
 
 _CAPS_FIELDS = ("coopmat", "tile", "subgroup", "coopmatsubgroup", "sharedbudget", "workgrouplimit", "cores",

@@ -275,6 +275,69 @@ def round_to(x: np.ndarray, dtype: str) -> np.ndarray:
     raise ValueError(dtype)
 
 
+# ---- tensor addressing (src/vocabulary/tensor.jl:44-108; src/device/tensor_intrinsics.jl:
+# 139-155 clamp value, 258-320 load, 329-402 store), element by element.
+CLAMP_UNDEFINED, CLAMP_CONSTANT, CLAMP_TO_EDGE = 0, 1, 2
+
+
+def _tensor_outer(l: dict):
+    """Offset of the slice's outer (rank > 2) block and whether it lies in the tensor."""
+    o, inside = 0, True
+    for d in range(l["rank"] - 2):
+        t = l["off"][d]
+        if l["clamp"] == CLAMP_TO_EDGE and l["dim"][d] > 0:
+            t = min(max(t, 0), l["dim"][d] - 1)
+        inside = inside and 0 <= t < l["dim"][d]
+        o += t * l["stride"][d]
+    return o, inside
+
+
+def _tensor_elem(l: dict, outer: int, outer_in: bool, i0: int, i1: int):
+    """(offset, inside) of slice element (i0, i1) of the last two dimensions, or None
+    when it lies outside the slice."""
+    d0, d1 = l["rank"] - 2, l["rank"] - 1
+    if i0 >= l["size"][d0] or i1 >= l["size"][d1]:
+        return None
+    t0, t1 = l["off"][d0] + i0, l["off"][d1] + i1
+    inside = outer_in and 0 <= t0 < l["dim"][d0] and 0 <= t1 < l["dim"][d1]
+    if not inside and l["clamp"] == CLAMP_TO_EDGE and outer_in and l["dim"][d0] > 0 and l["dim"][d1] > 0:
+        t0 = min(max(t0, 0), l["dim"][d0] - 1)
+        t1 = min(max(t1, 0), l["dim"][d1] - 1)
+        inside = True
+    return outer + t0 * l["stride"][d0] + t1 * l["stride"][d1], inside
+
+
+def tensor_load(obj: np.ndarray, src: np.ndarray, l: dict, clamp_value, transpose: bool = False) -> np.ndarray:
+    """tensor_load(obj, src, layout[, view]): matrix element (r, c) is slice element
+    (r, c), or (c, r) through the transposing view; outside the slice it keeps obj's
+    value; inside the slice but outside the tensor it reads `clamp_value` (CONSTANT,
+    UNDEFINED) or the nearest element (TO_EDGE).  `src` is the flat memory the layout
+    addresses."""
+    out = obj.copy()
+    outer, outer_in = _tensor_outer(l)
+    for r in range(obj.shape[0]):
+        for c in range(obj.shape[1]):
+            e = _tensor_elem(l, outer, outer_in, c if transpose else r, r if transpose else c)
+            if e is None:
+                continue
+            out[r, c] = src[e[0]] if e[1] else clamp_value
+    return out
+
+
+def tensor_store(m: np.ndarray, dst: np.ndarray, l: dict, transpose: bool = False) -> np.ndarray:
+    """tensor_store(m, dst, layout[, view]): writes the elements inside both the slice and
+    the tensor (a clamping store never clamps to the edge); returns the new memory."""
+    out = dst.copy()
+    ls = dict(l, clamp=CLAMP_CONSTANT)
+    outer, outer_in = _tensor_outer(ls)
+    for r in range(m.shape[0]):
+        for c in range(m.shape[1]):
+            e = _tensor_elem(ls, outer, outer_in, c if transpose else r, r if transpose else c)
+            if e is not None and e[1]:
+                out[e[0]] = m[r, c]
+    return out
+
+
 def rel_frobenius(x: np.ndarray, ref: np.ndarray) -> float:
     x = np.asarray(x, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)

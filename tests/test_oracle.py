@@ -312,3 +312,107 @@ def test_round_to_rne(oracle):
     assert oracle.round_to(x[:2], "bf16").tolist() == [1.0, 1.0078125]
     assert oracle.round_to(x[2:], "f16").tolist() == [65504.0, 1.0]   # tie to even
     assert oracle.round_to(np.array([0.1]), "f32")[0] == float(np.float32(0.1))
+
+
+# ---- tensor addressing --------------------------------------------------------------
+def _layout(dims, strides=None, off=None, size=None, clamp=1, rank=None):
+    rank = rank or len(dims)
+    if strides is None:
+        strides, s = [0] * rank, 1
+        for i in range(rank - 1, -1, -1):
+            strides[i] = s
+            s *= dims[i]
+    return {"rank": rank, "clamp": clamp, "dim": list(dims), "stride": list(strides),
+            "off": list(off or [0] * rank), "size": list(size or dims)}
+
+
+def test_tensor_load_inside_is_submatrix(oracle):
+    """A slice inside the tensor is the submatrix, for a packed and a padded (ld 37) tensor."""
+    for ld in (30, 37):
+        mem = np.arange(20 * ld, dtype=np.float64)
+        l = _layout((20, 30), (ld, 1), (3, 5), (16, 16))
+        got = oracle.tensor_load(np.zeros((16, 16)), mem, l, -1.0)
+        np.testing.assert_array_equal(got, mem.reshape(20, ld)[3:19, 5:21])
+
+
+@pytest.mark.parametrize("mode,pad", [(1, "constant"), (2, "edge")])
+def test_tensor_load_clamp_modes_are_pads(oracle, mode, pad):
+    """CONSTANT reads the clamp value outside the tensor, TO_EDGE the nearest element:
+    exactly numpy.pad's constant and edge modes, for slices over every edge."""
+    mem = np.arange(20 * 30, dtype=np.float64) * 0.5 + 1.0
+    t = mem.reshape(20, 30)
+    kw = {"constant_values": 7.0} if pad == "constant" else {}
+    padded = np.pad(t, 16, mode=pad, **kw)
+    for off in [(-3, 20), (10, -7), (-16, -16), (15, 25), (19, 29), (40, 2)]:
+        l = _layout((20, 30), (30, 1), off, (16, 16), clamp=mode)
+        got = oracle.tensor_load(np.zeros((16, 16)), mem, l, 7.0)
+        r, c = off[0] + 16, off[1] + 16
+        want = np.full((16, 16), 7.0) if pad == "constant" and r >= padded.shape[0] else None
+        if want is None:
+            block = padded[max(r, 0):r + 16, max(c, 0):c + 16]
+            if block.shape != (16, 16):   # beyond numpy's 16-element pad: extend it by its own rule
+                block = np.pad(t, 64, mode=pad, **kw)[r + 48:r + 64, c + 48:c + 64]
+            want = block
+        np.testing.assert_array_equal(got, want, err_msg=f"off={off} mode={pad}")
+
+
+def test_tensor_load_transposing_view(oracle):
+    """Through the (1, 0) view, matrix (r, c) reads slice (c, r): an 8 x 16 matrix from a
+    16 x 8 slice is that slice transposed; without the view the same load differs."""
+    mem = np.arange(20 * 30, dtype=np.float64)
+    l = _layout((20, 30), (30, 1), (2, 4), (16, 8))
+    got = oracle.tensor_load(np.zeros((8, 16)), mem, l, 0.0, transpose=True)
+    np.testing.assert_array_equal(got, mem.reshape(20, 30)[2:18, 4:12].T)
+    plain = oracle.tensor_load(np.zeros((8, 16)), mem, dict(l, size=[8, 16]), 0.0)
+    assert not np.array_equal(plain, got)
+
+
+def test_tensor_load_keeps_object_outside_slice(oracle):
+    mem = np.arange(20 * 30, dtype=np.float64)
+    obj = np.full((16, 16), -5.0)
+    l = _layout((20, 30), (30, 1), (1, 2), (10, 12))
+    got = oracle.tensor_load(obj, mem, l, 0.0)
+    np.testing.assert_array_equal(got[:10, :12], mem.reshape(20, 30)[1:11, 2:14])
+    assert np.all(got[10:, :] == -5.0) and np.all(got[:, 12:] == -5.0)
+
+
+def test_tensor_load_rank3_outer_block(oracle):
+    """A rank-3 slice picks its outer block by offset; an outer offset past the tensor reads
+    the clamp value (CONSTANT) or the last block (TO_EDGE)."""
+    mem = np.arange(4 * 20 * 30, dtype=np.float64)
+    t = mem.reshape(4, 20, 30)
+    l = _layout((4, 20, 30), None, (2, 3, 5), (1, 16, 16))
+    np.testing.assert_array_equal(oracle.tensor_load(np.zeros((16, 16)), mem, l, 0.0), t[2, 3:19, 5:21])
+    out = dict(l, off=[5, 3, 5])
+    assert np.all(oracle.tensor_load(np.zeros((16, 16)), mem, out, 9.0) == 9.0)
+    np.testing.assert_array_equal(oracle.tensor_load(np.zeros((16, 16)), mem, dict(out, clamp=2), 9.0),
+                                  t[3, 3:19, 5:21])
+
+
+def test_tensor_store_writes_inside_only(oracle):
+    """The clamping store writes slice ∩ tensor; through the view, the transpose."""
+    dst = np.full(20 * 30, -1.0)
+    m = np.arange(256, dtype=np.float64).reshape(16, 16)
+    l = _layout((20, 30), (30, 1), (10, 20), (16, 16), clamp=2)   # a store never clamps to the edge
+    got = oracle.tensor_store(m, dst, l).reshape(20, 30)
+    want = np.full((20, 30), -1.0)
+    want[10:20, 20:30] = m[:10, :10]
+    np.testing.assert_array_equal(got, want)
+    got_t = oracle.tensor_store(m, dst, l, transpose=True).reshape(20, 30)
+    want_t = np.full((20, 30), -1.0)
+    want_t[10:20, 20:30] = m.T[:10, :10]
+    np.testing.assert_array_equal(got_t, want_t)
+
+
+def test_tensor_clamp_one_gives_row_sums(oracle):
+    """The V-padding identity: with V's columns past the tensor read as one, those columns
+    of P V are the row sums of P."""
+    rng = np.random.default_rng(3)
+    P = rng.random((16, 16))
+    E = 10
+    V = rng.random(16 * E)
+    l = _layout((16, E), (E, 1), (0, 0), (16, 16))
+    Vp = oracle.tensor_load(np.zeros((16, 16)), V, l, 1.0)
+    D = P @ Vp
+    np.testing.assert_allclose(D[:, :E], P @ V.reshape(16, E), rtol=1e-14)
+    np.testing.assert_allclose(D[:, E:], np.repeat(P.sum(axis=1, keepdims=True), 16 - E, axis=1), rtol=1e-14)
