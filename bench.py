@@ -10,7 +10,7 @@ before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|
-                              gemm_bf16_ragged|gemm_cm2_f16|copy]
+                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|copy]
 
 A step is one kernel launch over the whole problem.  Kernel time comes from HIP
 events recorded on the launch stream around the K timed launches; wall time
@@ -109,15 +109,16 @@ def bench_gemm_ex(lh, n, steps, warmup, stream, cfg):
     return 2.0 * n ** 3, kern_ms, wall_ms
 
 
-def bench_gemm_cm2(lh, n, steps, warmup, stream, cfg):
-    """The coopmat2 GEMM: fp16 A, B row-major, fp16 C, tensor-addressed loads from memory."""
+def bench_gemm_cm2(lh, n, steps, warmup, stream, cfg, vocabulary=False):
+    """The coopmat2 GEMM: fp16 A, B row-major, fp16 C (the tile kernel, or the
+    tensor-vocabulary form)."""
     A = lh.HIPDeviceArray("f16", (n, n), order="C")
     B = lh.HIPDeviceArray("f16", (n, n), order="C")
     Cm = lh.HIPDeviceArray("f16", (n, n), order="C")
     lh.fill_uniform(A, lh.seed(cfg, 0), -1.0, 1.0)
     lh.fill_uniform(B, lh.seed(cfg, 1), -1.0, 1.0)
     lh.synchronize()
-    kern_ms, wall_ms = timed(lh, lambda: lh.gemm_cm2(Cm, A, B, stream=stream), steps, warmup, stream)
+    kern_ms, wall_ms = timed(lh, lambda: lh.gemm_cm2(Cm, A, B, vocabulary=vocabulary, stream=stream), steps, warmup, stream)
     return 2.0 * n ** 3, kern_ms, wall_ms
 
 
@@ -207,7 +208,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
-                             "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "copy"])
+                             "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -258,12 +259,20 @@ def main():
                                                             "zero-clamped loads, bounds-checked store)"},
                     "kernel_ms": round(kms, 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "gemm_bf16_nn":
+        flop, kms, wms = bench_gemm_layout(lh, "bf16", 8192, 1 | 2 | 4, K, W, stream, 1)
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "bf16", "config": {"workload": "bf16 GEMM 8192^3, A and B row-major (B read through "
+                                                            "transposing LDS reads)"},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_cm2_f16":
         flop, kms, wms = bench_gemm_cm2(lh, 4096, K, W, stream, 1)
+        _, vkms, _ = bench_gemm_cm2(lh, 4096, K, W, stream, 1, vocabulary=True)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
-                    "dtype": "f16", "config": {"workload": "coopmat2 GEMM 4096^3 fp16 -> fp16, A and B row-major, "
-                                                           "tensor-addressed loads"},
+                    "dtype": "f16", "config": {"workload": "coopmat2 GEMM 4096^3 fp16 -> fp16, A and B row-major"},
                     "kernel_ms": round(kms, 4),
+                    "vocabulary_form_tflops": round(flop / (vkms * 1e-3) / 1e12, 2),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_ex_bf16":
         flop, kms, wms = bench_gemm_ex(lh, 8192, K, W, stream, 1)

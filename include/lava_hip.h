@@ -253,14 +253,18 @@ int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
 
 /* The coopmat2 (tensor-addressed, workgroup-scope) GEMM: C = fp16(A B), fp32 accumulate.
- * A (M x K) and B (K x N) fp16 row-major, read straight from memory through zero-clamped
- * layouts sliced per 128 x 128 block with K steps of 64, so any M, N, K works unpadded;
- * C row-major M x N (ldc >= N) or, with transpose_c != 0, C^T stored row-major N x M
- * (ldc >= M) through the transposing view.  Extents and leading dimensions < 2^31.
+ * A (M x K) and B (K x N) fp16 row-major, zero-clamped so that any M, N, K works unpadded;
+ * C row-major M x N (ldc >= N) or, with LAVA_HIP_CM2_TRANSPOSE_C, C^T stored row-major
+ * N x M (ldc >= M) through the transposing view.  Extents and leading dimensions < 2^31.
+ * Default: the 256 x 256 tile kernel (buffer-resource loads that read zero past the
+ * extent); LAVA_HIP_CM2_VOCABULARY: the shader's own form in the tensor vocabulary
+ * (128 x 128 blocks, K steps of 64, tensor_load / tensor_store per fragment).
  * Replaces `gemm_cm2!` / test/glsl/coopmat2_gemm_regs.comp:37-84 (push block
  * {pa, pb, pc, M, N, K}), with the view store of tensor_intrinsics.jl:371-402. */
+#define LAVA_HIP_CM2_TRANSPOSE_C 1u
+#define LAVA_HIP_CM2_VOCABULARY 2u
 int lava_hip_gemm_cm2_f16(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-                          int64_t ldb, int64_t ldc, int transpose_c, void* stream);
+                          int64_t ldb, int64_t ldc, uint32_t flags, void* stream);
 
 /* ---- fused GEMM epilogue: activations (elementwise epilogues that Lava writes with
  * coopmat_length / getcomp / setcomp, src/device/coopmat_intrinsics.jl:322-400) ---- */

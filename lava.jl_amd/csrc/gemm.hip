@@ -2,10 +2,11 @@
 //
 // A column-major C is handled as its row-major transpose, C^T = B^T A^T, which
 // swaps the operands and flips their layouts; so every kernel writes row-major C.
-// The compute-bound shapes with K-contiguous operands (A row-major, B
-// column-major: the bf16 configuration) take the TN kernel -- whole tiles, or any
-// M and N and K a multiple of 16 bytes with zero-clamped loads; everything else the
-// staged kernel.
+// Compute-bound shapes take the 256 x 256 tile kernel (gemm_tn_kernel.hpp) in any
+// operand layout for 16-bit types (K-contiguous operands read directly, M/N-contiguous
+// ones through transposing LDS reads) and with both operands K-contiguous for int8 --
+// whole tiles, or ragged extents with zero-clamped loads; the rest (small products,
+// extents that split a 16-byte chunk, other int8 layouts) the staged kernel.
 #include <hip/hip_runtime.h>
 
 #include "gemm_kernels.hpp"
@@ -57,8 +58,9 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     }
     hipStream_t s = as_stream(stream);
     Acc* c = static_cast<Acc*>(C);
-    const int fit = arow && !brow ? tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT)) : TN_NO;
-    if (fit != TN_NO) return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, fit == TN_RAGGED);
+    const int fit = tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
+    if (fit != TN_NO)
+        return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, fit == TN_RAGGED, arow, !brow);
     return launch_gemm_staged<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
 }
 

@@ -16,15 +16,17 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
 int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s);
 
-// The fast path: A row-major (M x K), B column-major (K x N) -- both K-contiguous --
-// C row-major.  tn_gemm_eligible() says whether it applies: TN_FULL for whole 256 x 256
-// tiles and 64-element K steps, TN_RAGGED for other extents (K a multiple of 16 bytes).
+// The fast path, C row-major: A and B each K-contiguous (A row-major, B column-major)
+// or, for 16-bit types, M/N-contiguous (A column-major, B row-major).
+// tn_gemm_eligible() says whether it applies: TN_FULL for whole 256 x 256 tiles and
+// 64-element K steps, TN_RAGGED for other extents (a K-contiguous operand needs K a
+// multiple of 16 bytes, an M/N-contiguous one M or N a multiple of 8).
 enum TnFit : int { TN_NO = 0, TN_FULL = 1, TN_RAGGED = 2 };
 template <typename T>
 int tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-                     int64_t ldb, int64_t ldc, size_t c_elem);
+                     int64_t ldb, int64_t ldc, size_t c_elem, bool ak, bool bk);
 template <typename T, typename OutT, bool EPI>
 int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                   int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged);
+                   int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged, bool ak, bool bk);
 
 }  // namespace lava

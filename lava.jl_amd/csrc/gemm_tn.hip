@@ -1,416 +1,41 @@
-// gemm_tn.hip -- the compute-bound GEMM: A row-major, B column-major, C row-major.
-//
-// This is the staged cooperative-matrix GEMM (src/device/coopmat_intrinsics.jl:
-// 104-148 stages A and B through workgroup memory and reads A RowMajor and B
-// ColumnMajor from the same block; test/glsl/coopmat2_gemm_regs.comp:46-84 is the
-// same loop at workgroup scope) laid out for CDNA4:
-//
-//  * one 256 x 256 tile of C per workgroup of 4 wavefronts (one per SIMD), each
-//    wavefront owning a 128 x 128 sub-tile = 4 x 4 MFMA 32x32 accumulators
-//    (256 fp32 registers per lane, all in AGPRs);
-//  * K advances 128 bytes at a time (64 bf16/fp16 or 128 int8): A and B slices of
-//    256 rows x 128 bytes each, double-buffered in LDS (2 x 64 KB);
-//  * global -> LDS with buffer_load_dwordx4 ... lds: each lane moves 16 bytes
-//    straight into LDS, no register staging, addressed by a buffer resource plus a
-//    32-bit lane offset (the wave-uniform parts in soffset).  One wavefront instruction fills 1 KB = 8 LDS
-//    rows; lane l writes row l / 8, 16-byte slot l % 8.  The slot a logical 16-byte
-//    chunk c of row r lands in is c ^ swz(r), swz(r) = (r & 7) ^ ((r >> 3) & 1),
-//    chosen by which global chunk each lane fetches, so the fragment reads
-//    (16 consecutive rows, one chunk column) spread over all banks;
-//  * fragments are 16 bytes per lane (ds_read_b128), one MFMA 32x32x16 (16-bit)
-//    or 32x32x32 (int8) each; 4 sub-steps of 32 bytes of K per stage, each 16
-//    MFMAs, with the next sub-step's fragments read underneath (double-buffered
-//    fragment registers, 64 VGPRs) and the next stage's 16 DMA loads issued one per
-//    two MFMAs over sub-steps 0 and 1 (a wavefront's vector-memory issue takes
-//    ~40-70 cycles per 1 KB instruction; one per MFMA would stall the MFMA stream);
-//  * the MFMA's A operand is the B slice and its B operand the A slice, so each
-//    lane's accumulator holds runs of 4 consecutive columns of one row of C; the
-//    epilogue stages them through LDS and stores whole 512-byte row runs;
-//  * workgroups are renumbered XCD by XCD (xcd_tile) so that the tiles one XCD
-//    runs together share rows of A and columns of B in its L2;
-//  * ragged extents (the RAGGED instances; Lava's TENSOR_CLAMP_CONSTANT layout with
-//    the default zero, src/vocabulary/tensor.jl:44-51): a lane whose row lies past M
-//    (A) or N (B), or whose 16-byte K chunk lies past K, gets a lane offset beyond the
-//    buffer resource's range, so its load reads zero instead of memory; the store and
-//    the epilogue's operand loads are bounds-checked.  K must be a multiple of the
-//    16-byte chunk (8 f16/bf16, 16 int8) so that a chunk is wholly in or out.
-#include <hip/hip_runtime.h>
-
-#include <type_traits>
-
-#include "gemm_common.hpp"
-#include "gemm_kernels.hpp"
-#include "lava_hip_internal.hpp"
+// gemm_tn.hip -- the compute-bound GEMM: eligibility, the layout dispatcher and the
+// instances with both operands K-contiguous (A row-major, B column-major: the bf16
+// configuration, and every int8 product).  The kernel is gemm_tn_kernel.hpp; the
+// other operand forms are instantiated in gemm_tn_{nk,kn,nn}.hip.
+#include "gemm_tn_kernel.hpp"
 
 namespace lava {
 
-constexpr int TN_TILE = 256;    // rows of A / columns of B per workgroup
-constexpr int TN_KB = 128;      // bytes of K per stage
-constexpr int TN_SLICE = TN_TILE * TN_KB;  // 32 KB
+LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_EXTERN, false, true)
+LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_EXTERN, true, false)
+LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_EXTERN, false, false)
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-// Buffer resource over [base, base + bytes): untyped dword loads (gfx9 word 3:
-// DATA_FORMAT 32, stride 0).  Offsets past `bytes` read zero instead of faulting.
-__device__ __forceinline__ v4i make_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    v4i r;
-    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-    r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
-    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
-    r[3] = 0x00020000;
-    return r;
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// 16 bytes per lane from rsrc + voffset + soffset straight into LDS at
-// lds + 16 * lane (buffer_load_dwordx4 ... lds, LDS base in m0).  Written as inline
-// asm so that the compiler does not treat it as a store to every LDS byte: its
-// waitcnt pass would otherwise wait for the load before the next LDS read of the
-// *other* stage.  Completion is waited for explicitly (s_waitcnt vmcnt(0)) before
-// the barrier that publishes the stage.  m0 is a reserved register nothing else in
-// these kernels uses, so it is set here and not declared as a clobber.
-__device__ __forceinline__ void dma16(const v4i& rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :
-                 : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
-                 : "memory");
-}
-
-template <typename T, typename OutT, bool EPI, bool RAGGED>
-__global__ void __launch_bounds__(256, 1)
-    gemm_tn_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
-                   int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi, TnBounds bnd) {
-    using AccV = typename Mfma32<T>::acc_t;
-    typedef typename Mfma16<T>::acc_elem Acc;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TN_SLICE];  // [stage][A,B][row][128 B]
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    int tm, tn;
-    xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
-
-    // ---- global -> LDS: wave w fills rows [64w, 64w + 64) of each slice, 8 rows per instruction.
-    // Instruction i covers rows 64w + 8i + lane / 8; lane's slot is lane % 8; the
-    // logical chunk fetched is slot ^ swz(row) = (lane % 8) ^ (lane / 8) ^ (i & 1).
-    const int lr = lane >> 3;
-    const int c_even = (lane & 7) ^ lr;
-    const int c_odd = c_even ^ 1;
-    // A slice rows tm*256 .. +256 and B slice rows tn*256 .. +256 as buffer resources;
-    // each lane keeps one 32-bit row offset per chunk parity, the row step (8 i rows)
-    // and the k offset are wave-uniform and travel in soffset.
-    // Rows of this tile inside the matrix: all 256 unless RAGGED and the tile is the last.
-    int a_rows = TN_TILE, b_rows = TN_TILE;
-    if constexpr (RAGGED) {
-        a_rows = (int)(bnd.m - (int64_t)tm * TN_TILE < TN_TILE ? bnd.m - (int64_t)tm * TN_TILE : TN_TILE);
-        b_rows = (int)(bnd.n - (int64_t)tn * TN_TILE < TN_TILE ? bnd.n - (int64_t)tn * TN_TILE : TN_TILE);
-    }
-    const v4i rs_a =
-        make_rsrc(reinterpret_cast<const char*>(A) + (int64_t)tm * TN_TILE * lda_b, (uint32_t)(a_rows * lda_b));
-    const v4i rs_b =
-        make_rsrc(reinterpret_cast<const char*>(B) + (int64_t)tn * TN_TILE * ldb_b, (uint32_t)(b_rows * ldb_b));
-    const uint32_t a_row = (uint32_t)((64 * w + lr) * lda_b), b_row = (uint32_t)((64 * w + lr) * ldb_b);
-    const uint32_t a_off[2] = {a_row + 16u * c_even, a_row + 16u * c_odd};
-    const uint32_t b_off[2] = {b_row + 16u * c_even, b_row + 16u * c_odd};
-    const uint32_t a_step = (uint32_t)(8 * lda_b), b_step = (uint32_t)(8 * ldb_b);
-    const uint32_t lds0 = lds_addr(smem) + w * 64 * TN_KB;
-    // RAGGED: instruction i's row is inside the tile iff 8 i < *_lim; chunk parity p's
-    // last byte is inside K iff kofs + kend[p] <= K bytes.  A masked lane's offset is
-    // OOB_OFS: past every range here (num_records < 2^31), and OOB_OFS + soffset
-    // (< 2^31) does not wrap, whether or not the range check counts soffset.
-    const int a_lim = a_rows - 64 * w - lr, b_lim = b_rows - 64 * w - lr;
-    const int kend[2] = {16 * c_even + 16, 16 * c_odd + 16};
-    constexpr uint32_t OOB_OFS = 0x80000000u;
-
-    // DMA load q (0..15) of a k-tile into `stage`: q < 8 are A rows 8q.., q >= 8 B rows.
-    auto dma = [&](int q, int stage, uint32_t kofs) {
-        const int i = q & 7;
-        const uint32_t dst = lds0 + stage * 2 * TN_SLICE + (q >> 3) * TN_SLICE + i * 1024;
-        uint32_t off = q < 8 ? a_off[i & 1] : b_off[i & 1];
-        if constexpr (RAGGED) {
-            const bool in = 8 * i < (q < 8 ? a_lim : b_lim) && (int)kofs + kend[i & 1] <= bnd.kb;
-            off = in ? off : OOB_OFS;
-        }
-        if (q < 8) dma16(rs_a, off, i * a_step + kofs, dst);
-        else dma16(rs_b, off, i * b_step + kofs, dst);
-    };
-
-    // ---- fragments: 32x32 MFMA operands, 16 bytes per lane.  Operand row = base +
-    // 32 t + lane % 32, chunk = 2 s + lane / 32 for k sub-step s (32 bytes of K).  swz(row)
-    // only depends on lane % 16 (bases are multiples of 16), so each sub-step reads one
-    // slot per lane.
-    const int wm = w >> 1, wn = w & 1;
-    const int swz = (lane & 7) ^ ((lane >> 3) & 1);
-    const int h = lane >> 5;
-    const int a_rd = (wm * 128 + (lane & 31)) * TN_KB;
-    const int b_rd = TN_SLICE + (wn * 128 + (lane & 31)) * TN_KB;
-
-    AccV acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-    struct Frags {
-        uint4 a[4], b[4];
-    };
-    auto read_frags = [&](Frags& f, const uint8_t* base, int s) {
-        const int slot = ((2 * s + h) ^ swz) * 16;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            f.b[t] = *reinterpret_cast<const uint4*>(base + b_rd + t * 32 * TN_KB + slot);
-            f.a[t] = *reinterpret_cast<const uint4*>(base + a_rd + t * 32 * TN_KB + slot);
-        }
-    };
-    // MFMA A operand = B slice (rows are columns n of C), B operand = A slice (rows m):
-    // the accumulator then holds C^T, 4 consecutive n per lane and register group.
-    auto mma = [&](const Frags& f, int i0, int i1) {
-#pragma unroll
-        for (int i = i0; i < i1; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = Mfma32<T>::run(f.b[j], f.a[i], acc[i][j]);
-    };
-
-    // Per k-tile (128 bytes of K = 4 sub-steps), branch-free so the interleave holds:
-    //   s = 0..2: 16 MFMAs on the current fragments while the next sub-step's 8 LDS
-    //             reads (and, at s = 0 and 1, 8 DMA loads of the next tile each) issue;
-    //   s = 3:    8 MFMAs; wait for this wave's DMA; barrier; then the next tile's
-    //             s = 0 reads under the last 8 MFMAs.
-    // On the last tile the "next" tile re-fetches the current one into the idle stage.
-    {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) dma(q, 0, 0);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    Frags fa, fb;
-    read_frags(fa, smem, 0);
-
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int st = kt & 1;
-        const uint8_t* base = smem + st * 2 * TN_SLICE;
-        const uint8_t* next = smem + (st ^ 1) * 2 * TN_SLICE;
-        const uint32_t kofs_next = (uint32_t)(kt + 1 < ktiles ? kt + 1 : kt) * TN_KB;
-        // s = 0: LDS reads of s = 1, then 16 MFMAs with one DMA load of the next tile after each
-        read_frags(fb, base, 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] = Mfma32<T>::run(fa.b[j], fa.a[i], acc[i][j]);
-                if (j & 1) dma(2 * i + (j >> 1), st ^ 1, kofs_next);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        // s = 1: the other 8 DMA loads (one per two MFMAs) and s = 2's LDS reads under 16 MFMAs
-        read_frags(fa, base, 2);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] = Mfma32<T>::run(fb.b[j], fb.a[i], acc[i][j]);
-                if (j & 1) dma(8 + 2 * i + (j >> 1), st ^ 1, kofs_next);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        read_frags(fb, base, 3);
-        mma(fa, 0, 4);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // s = 3: half the MFMAs, publish the next stage, its first reads under the other half
-        mma(fb, 0, 2);
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's part of the next tile landed
-        __syncthreads();
-        __builtin_amdgcn_sched_barrier(0);
-        read_frags(fa, next, 0);
-        mma(fb, 2, 4);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 3);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 3);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-
-    // ---- epilogue through LDS, so that global stores are whole 512-byte row runs.
-    // acc[i][j] register r of lane l is C[m][n] with m = 128 wm + 32 i + l % 32 and
-    // n = 128 wn + 32 j + 8 (r / 4) + 4 (l / 32) + r % 4 within the tile.  Each wave
-    // stages 32 rows x 128 columns at a time (one i) in its own 16.5 KB of the idle
-    // stage buffers (4 waves: 66 KB of the 128 KB), rows padded to 528 bytes so the
-    // 32 rows of one column group land on distinct banks; then reads whole rows back:
-    // lanes 0..31 and 32..63 each cover one 512-byte row per instruction.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    constexpr int EP_PITCH = 128 * 4 + 16;
-    const int rr = lane & 31;
-    uint8_t* ep = smem + w * (32 * EP_PITCH);
-    typedef Acc Acc4 __attribute__((ext_vector_type(4)));
-    const int64_t row0 = (int64_t)tm * TN_TILE + wm * 128, col0 = (int64_t)tn * TN_TILE + wn * 128;
-    OutT* cbase = C + row0 * ldc + col0;
-    // columns of this lane's 4-column group inside the matrix (RAGGED: 0..4)
-    int cols_in = 4;
-    if constexpr (RAGGED) {
-        const int64_t left = bnd.n - (col0 + 4 * rr);
-        cols_in = left >= 4 ? 4 : (left > 0 ? (int)left : 0);
-    }
-    // one row quarter i at a time; i is a template constant so that acc stays in registers
-    typedef float F4 __attribute__((ext_vector_type(4)));
-    auto quarter = [&](auto itag) {
-        constexpr int i = decltype(itag)::value;
-        // The epilogue's init terms for the 16 rows x 4 columns this lane finishes, all
-        // requested before the staging so that their HBM latency overlaps it (loaded one
-        // row at a time inside the store loop they cost one round trip per row).
-        F4 rin[EPI ? 16 : 1];
-        float bin[EPI ? 16 : 1];
-        F4 bcol = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (EPI) {
-            const int64_t n = col0 + 4 * rr;
-            // 4 floats at p, or those of them inside the matrix (columns < N)
-            auto ld4 = [&](const float* p) {
-                if (epi.vec4 && cols_in == 4) return *reinterpret_cast<const F4*>(p);
-                F4 r = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (k < cols_in) r[k] = p[k];
-                return r;
-            };
-            if (epi.bias && epi.bias_on_cols) bcol = ld4(epi.bias + n);
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int64_t m = row0 + 32 * i + 2 * t + h;
-                rin[t] = F4{0.f, 0.f, 0.f, 0.f};
-                bin[t] = 0.f;
-                if (RAGGED && m >= bnd.m) continue;
-                if (epi.residual) rin[t] = ld4(epi.residual + m * epi.ldr + n);
-                if (epi.bias && !epi.bias_on_cols) bin[t] = epi.bias[m];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const Acc4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                *reinterpret_cast<Acc4*>(ep + rr * EP_PITCH + (32 * j + 8 * g + 4 * h) * 4) = v;
-            }
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's staged rows are in LDS
-        __builtin_amdgcn_wave_barrier();
-        auto store_rows = [&](auto acttag) {
-            constexpr int ACT = decltype(acttag)::value;
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int row = 2 * t + h;                       // 0..31 of this i
-                const Acc4 v = *reinterpret_cast<const Acc4*>(ep + row * EP_PITCH + rr * 16);
-                OutT* dst = cbase + (int64_t)(32 * i + row) * ldc + 4 * rr;
-                if (RAGGED && row0 + 32 * i + row >= bnd.m) continue;
-                if constexpr (!EPI && std::is_same<OutT, Acc>::value) {
-                    if (!RAGGED || (cols_in == 4 && bnd.cvec)) {
-                        *reinterpret_cast<Acc4*>(dst) = v;
-                    } else {
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            if (k < cols_in) dst[k] = v[k];
-                    }
-                } else {
-                    // the fused epilogue on 4 consecutive columns of one row, narrowed (RNE) to D's type
-                    typedef OutT Out4 __attribute__((ext_vector_type(4)));
-                    Out4 o;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        float x = (float)v[k];
-                        // the same fp32 sums as epi_apply: (bias + residual), then acc + that
-                        if constexpr (EPI) x = epi_act_c<ACT>(x + ((bin[t] + bcol[k]) + rin[t][k]));
-                        o[k] = narrow<OutT>(x);
-                    }
-                    if (!RAGGED || (cols_in == 4 && bnd.cvec)) {
-                        *reinterpret_cast<Out4*>(dst) = o;
-                    } else {
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            if (k < cols_in) dst[k] = o[k];
-                    }
-                }
-            }
-        };
-        if constexpr (EPI) {
-            switch (epi.act) {   // uniform: one branch per quarter, none per element
-            case EPI_RELU: store_rows(std::integral_constant<int, EPI_RELU>{}); break;
-            case EPI_GELU_TANH: store_rows(std::integral_constant<int, EPI_GELU_TANH>{}); break;
-            case EPI_GELU_ERF: store_rows(std::integral_constant<int, EPI_GELU_ERF>{}); break;
-            default: store_rows(std::integral_constant<int, EPI_NONE>{}); break;
-            }
-        } else {
-            store_rows(std::integral_constant<int, EPI_NONE>{});
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next i overwrites
-        __builtin_amdgcn_wave_barrier();
-    };
-    quarter(std::integral_constant<int, 0>{});
-    quarter(std::integral_constant<int, 1>{});
-    quarter(std::integral_constant<int, 2>{});
-    quarter(std::integral_constant<int, 3>{});
-}
-
-template <typename T>
-int tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-                     int64_t ldb, int64_t ldc, size_t c_elem) {
-    const int64_t ke = TN_KB / (int64_t)sizeof(T), chunk = 16 / (int64_t)sizeof(T);
-    if (M <= 0 || N <= 0 || K <= 0 || K % chunk) return TN_NO;
-    const int64_t tiles_m = (M + TN_TILE - 1) / TN_TILE, tiles_n = (N + TN_TILE - 1) / TN_TILE;
-    if (tiles_m * tiles_n > 0x7fffffff || (K + ke - 1) / ke > 0x7fffffff || K * (int64_t)sizeof(T) > 0x7fffffff)
-        return TN_NO;
-    if ((lda * (int64_t)sizeof(T)) % 16 || (ldb * (int64_t)sizeof(T)) % 16) return TN_NO;
-    // buffer offsets are 32-bit: a 256-row slab of A or B must span < 2 GiB
-    if ((int64_t)TN_TILE * lda * (int64_t)sizeof(T) >= ((int64_t)1 << 31) ||
-        (int64_t)TN_TILE * ldb * (int64_t)sizeof(T) >= ((int64_t)1 << 31))
-        return TN_NO;
-    if (!aligned(A, 16) || !aligned(B, 16)) return TN_NO;
-    if (M % TN_TILE == 0 && N % TN_TILE == 0 && K % ke == 0 && ldc % 4 == 0 && aligned(C, 4 * c_elem))
-        return TN_FULL;
-    // ragged: worth the 256 x 256 tiles once the product is no longer launch-bound
-    return M * N >= (int64_t)TN_TILE * TN_TILE ? TN_RAGGED : TN_NO;
-}
+LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_INST, true, true)
+LAVA_TN_LAYOUT_INST(int8_t, int32_t, false, true, true)
 
 template <typename T, typename OutT, bool EPI>
 int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                   int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged) {
-    const int tiles_m = (int)((M + TN_TILE - 1) / TN_TILE), tiles_n = (int)((N + TN_TILE - 1) / TN_TILE);
-    const int64_t ke = TN_KB / (int64_t)sizeof(T);
-    const int ktiles = (int)((K + ke - 1) / ke);
-    TnBounds bnd;
-    bnd.m = M;
-    bnd.n = N;
-    bnd.kb = (int)(K * (int64_t)sizeof(T));
-    bnd.cvec = ldc % 4 == 0 && aligned(C, 4 * sizeof(OutT));
-    if (ragged)
-        hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0, s,
-                           A, B, C, tiles_m, tiles_n, ktiles, lda * (int64_t)sizeof(T), ldb * (int64_t)sizeof(T), ldc,
-                           epi, bnd);
-    else
-        hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI, false>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256), 0,
-                           s, A, B, C, tiles_m, tiles_n, ktiles, lda * (int64_t)sizeof(T), ldb * (int64_t)sizeof(T),
-                           ldc, epi, bnd);
-    LAVA_LAUNCH_CHECK("gemm_tn_kernel");
-    return LAVA_HIP_OK;
+                   int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged, bool ak, bool bk) {
+    if (ak && bk) return launch_gemm_tn_layout<T, OutT, EPI, true, true>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
+    if constexpr (sizeof(T) == 2) {
+        if (!ak && bk)
+            return launch_gemm_tn_layout<T, OutT, EPI, false, true>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
+        if (ak && !bk)
+            return launch_gemm_tn_layout<T, OutT, EPI, true, false>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
+        return launch_gemm_tn_layout<T, OutT, EPI, false, false>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
+    }
+    LAVA_REQUIRE(false, LAVA_HIP_ERR_UNSUPPORTED, "gemm_tn: 8-bit operands must both be K-contiguous");
 }
 
 template int tn_gemm_eligible<f16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                   int64_t, size_t);
+                                   int64_t, size_t, bool, bool);
 template int tn_gemm_eligible<bf16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t,
-                                    int64_t, int64_t, size_t);
+                                    int64_t, int64_t, size_t, bool, bool);
 template int tn_gemm_eligible<int8_t>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t,
-                                      int64_t, int64_t, size_t);
+                                      int64_t, int64_t, size_t, bool, bool);
 #define LAVA_TN_INST(T, O, E)                                                                                      \
     template int launch_gemm_tn<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, \
-                                         hipStream_t, const Epilogue&, bool);
+                                         hipStream_t, const Epilogue&, bool, bool, bool);
 LAVA_TN_INST(f16, float, false)
 LAVA_TN_INST(bf16, float, false)
 LAVA_TN_INST(int8_t, int32_t, false)

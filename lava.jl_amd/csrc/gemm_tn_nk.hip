@@ -1,0 +1,8 @@
+// gemm_tn_nk.hip -- gemm_tn_kernel instances for A column-major (M-contiguous), B column-major (K-contiguous).
+#include "gemm_tn_kernel.hpp"
+
+namespace lava {
+
+LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_INST, false, true)
+
+}  // namespace lava

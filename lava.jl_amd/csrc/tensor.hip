@@ -8,13 +8,16 @@
 //    whose padding columns of P * V then hold the row sums of P
 //    (src/device/tensor_intrinsics.jl:139-155);
 //  * lava_hip_gemm_cm2_f16: the coopmat2 GEMM of test/glsl/coopmat2_gemm_regs.comp:
-//    37-84 -- workgroups of 256 invocations own a 128 x 128 block of C, K advances 64
-//    at a time, A and B come straight from memory through zero-clamped layouts sliced
-//    per block (any M, N, K: nothing is padded), the fp32 sum is converted to fp16 and
-//    stored through a clamping layout, or through the transposing view (C^T), as
-//    mul_mm_cm2 stores its result (tensor_intrinsics.jl `lava_tensor_store` with a view).
-//    The shader's one workgroup-scope 128 x 128 matrix is held here as 4 wavefronts x
-//    (2 x 2) 32 x 32 MFMA accumulators.
+//    37-84 (fp16 A, B row-major, zero-clamped so that any M, N, K works unpadded, fp16
+//    C stored plainly or through the transposing view).  By default it runs on the
+//    256 x 256 tile kernel, whose buffer-resource loads are this hardware's clamping
+//    tensor layout (a lane past the extent reads zero); LAVA_HIP_CM2_VOCABULARY runs
+//    the shader's own form written in the tensor vocabulary below: workgroups of 256
+//    invocations own a 128 x 128 block of C, K advances 64 at a time, A and B are
+//    tensor_load-ed straight from memory through layouts sliced per block, the fp32
+//    sum is converted to fp16 and tensor_store-d through a clamping layout or the
+//    (1, 0) view.  The shader's one workgroup-scope 128 x 128 matrix is held as 4
+//    wavefronts x (2 x 2) 32 x 32 MFMA accumulators.
 #include <hip/hip_runtime.h>
 
 #include "lava_hip_internal.hpp"
@@ -232,7 +235,10 @@ int lava_hip_tensor_muladd_16x16x16(const void* A, const lava_hip_tensor_layout*
 }
 
 int lava_hip_gemm_cm2_f16(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-                          int64_t ldb, int64_t ldc, int transpose_c, void* stream) {
+                          int64_t ldb, int64_t ldc, uint32_t flags, void* stream) {
+    LAVA_ARG((flags & ~(LAVA_HIP_CM2_TRANSPOSE_C | LAVA_HIP_CM2_VOCABULARY)) == 0, "gemm_cm2_f16: unknown flags 0x%x",
+             flags);
+    const bool transpose_c = flags & LAVA_HIP_CM2_TRANSPOSE_C;
     LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "gemm_cm2_f16: negative extent");
     if (M == 0 || N == 0) return LAVA_HIP_OK;
     LAVA_ARG(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff && lda <= 0x7fffffff && ldb <= 0x7fffffff &&
@@ -245,6 +251,10 @@ int lava_hip_gemm_cm2_f16(const void* A, const void* B, void* C, int64_t M, int6
     const int64_t gx = (M + CM2_BM - 1) / CM2_BM, gy = (N + CM2_BN - 1) / CM2_BN;
     LAVA_ARG(gx <= 0x7fffffff && gy <= 65535, "gemm_cm2_f16: N = %lld needs more than 65535 workgroup columns",
              (long long)N);
+    if (!(flags & LAVA_HIP_CM2_VOCABULARY))   // the 256 x 256 tile kernel: zero-clamped buffer loads
+        return lava_hip_gemm_ex(LAVA_HIP_F16, LAVA_HIP_F16, A, B, C, M, N, K, lda, ldb, ldc,
+                                LAVA_HIP_A_ROWMAJOR | LAVA_HIP_B_ROWMAJOR | (transpose_c ? 0u : LAVA_HIP_C_ROWMAJOR),
+                                nullptr, nullptr, 0, LAVA_HIP_ACT_NONE, stream);
     int rc = lava_hip_init();
     if (rc != LAVA_HIP_OK) return rc;
     hipStream_t s = as_stream(stream);

@@ -212,10 +212,12 @@ def tensor_muladd_16x16x16(D: HIPDeviceArray, A: HIPDeviceArray, layout_a: Tenso
 
 
 def gemm_cm2(Cm: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray, transpose: bool = False,
-             stream: Optional[int] = None) -> HIPDeviceArray:
+             vocabulary: bool = False, stream: Optional[int] = None) -> HIPDeviceArray:
     """The coopmat2 GEMM (test/glsl/coopmat2_gemm_regs.comp:37-84): fp16 A (M x K) and B
     (K x N) row-major, fp32 accumulate, fp16 C (M x N) row-major -- or, transpose=True,
-    C^T into an N x M row-major array through the transposing view.  Any M, N, K."""
+    C^T into an N x M row-major array through the transposing view.  Any M, N, K.
+    vocabulary=True runs the shader's own form written with tensor_load / tensor_store
+    instead of the 256 x 256 tile kernel."""
     if not (A.dtype == B.dtype == Cm.dtype == "f16"):
         raise ValueError("gemm_cm2 is fp16 in, fp16 out")
     if A.order != "C" or B.order != "C" or Cm.order != "C":
@@ -225,7 +227,7 @@ def gemm_cm2(Cm: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray, transpose
     want = (N, M) if transpose else (M, N)
     if K2 != K or Cm.dims != want:
         raise ValueError(f"shape mismatch: A {A.dims}, B {B.dims}, C {Cm.dims} (want {want})")
+    flags = (1 if transpose else 0) | (2 if vocabulary else 0)
     _lib.call("lava_hip_gemm_cm2_f16", A.ptr, B.ptr, Cm.ptr, M, N, K, max(K, 1), max(N, 1), max(Cm.dims[1], 1),
-              1 if transpose else 0,
-              stream)
+              flags, stream)
     return Cm

@@ -124,3 +124,58 @@ def test_tn_ragged_epilogue(gpu, oracle, d, crow):
     got = oracle.bf16_bits_to_f32(h).astype(np.float64) if d == "bf16" else h.astype(np.float64)
     err = oracle.rel_frobenius(got, ref)
     assert err <= TOL, err
+
+
+LAYOUT_SHAPES = [(512, 768, 256), (1000, 776, 520), (264, 1032, 8), (2048, 256, 1000)]
+
+
+@pytest.mark.parametrize("shape", LAYOUT_SHAPES)
+@pytest.mark.parametrize("layout", range(8))
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_tile_kernel_every_layout(gpu, oracle, dt, layout, shape):
+    """16-bit operands in all 8 layouts at sizes the 256 x 256 tile kernel takes: a
+    K-contiguous operand (A row-major, B column-major) is read directly, an M/N-contiguous
+    one (A column-major, B row-major) through transposing LDS reads; column-major C swaps
+    the operands.  Whole tiles (512 x 768 x 256) and ragged M, N, K."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"tile kernel {dt} layout={layout} M={M} N={N} K={K}")
+    A = lh.HIPDeviceArray(dt, (M, K), order="C" if layout & 1 else "F")
+    B = lh.HIPDeviceArray(dt, (K, N), order="C" if layout & 2 else "F")
+    fill(lh, A, dt, 9000 + 10 * layout + M)
+    fill(lh, B, dt, 9500 + 10 * layout + N)
+    C = lh.HIPDeviceArray("f32", (M, N), order="C" if layout & 4 else "F")
+    C.fill_bytes(0xFF)
+    lh.gemm(C, A, B)
+    rows = sample_rows(M, np.random.default_rng(layout * 131 + M))
+    lda = K if layout & 1 else M
+    ldb = N if layout & 2 else K
+    ref = oracle.gemm_rows(host_flat(A), dt, host_flat(B), dt, M, N, K, lda, ldb, layout & 3, rows)
+    err = oracle.rel_frobenius(C.to_numpy()[rows], ref)
+    assert err <= TOL, err
+
+
+@pytest.mark.parametrize("layout", [0, 2, 3, 6])
+def test_tile_kernel_layouts_epilogue(gpu, oracle, layout):
+    """The fused epilogue on the M/N-contiguous forms (bias + residual + gelu, bf16 out)."""
+    lh = gpu
+    M, N, K = 520, 784, 264
+    announce(f"tile kernel epilogue layout={layout}")
+    A = lh.HIPDeviceArray("bf16", (M, K), order="C" if layout & 1 else "F")
+    B = lh.HIPDeviceArray("bf16", (K, N), order="C" if layout & 2 else "F")
+    lh.fill_uniform(A, 9900 + layout, -1.0, 1.0)
+    lh.fill_uniform(B, 9950 + layout, -1.0, 1.0)
+    order = "C" if layout & 4 else "F"
+    D = lh.HIPDeviceArray("bf16", (M, N), order=order)
+    bias = lh.HIPDeviceArray("f32", (M,))
+    res = lh.HIPDeviceArray("f32", (M, N), order=order)
+    lh.fill_uniform(bias, 9960, -1.0, 1.0)
+    lh.fill_uniform(res, 9961, -2.0, 2.0)
+    lh.gemm_ex(D, A, B, bias=bias, residual=res, act="gelu_tanh")
+    lda = K if layout & 1 else M
+    ldb = N if layout & 2 else K
+    c = oracle.gemm_rows(host_flat(A), "bf16", host_flat(B), "bf16", M, N, K, lda, ldb, layout & 3, np.arange(M))
+    ref = oracle.round_to(oracle.gemm_epilogue(c, bias.to_numpy(), res.to_numpy(), "gelu_tanh"), "bf16")
+    got = oracle.bf16_bits_to_f32(D.to_numpy()).astype(np.float64)
+    err = oracle.rel_frobenius(got, ref)
+    assert err <= TOL, err

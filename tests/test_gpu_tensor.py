@@ -130,20 +130,22 @@ def test_tensor_clamp_value_one_row_sums(gpu, oracle, E, via_view):
     np.testing.assert_allclose(got[:, E:], np.repeat(P64.sum(axis=1, keepdims=True), 16 - E, axis=1), rtol=1e-6)
 
 
+@pytest.mark.parametrize("vocabulary", [False, True])
 @pytest.mark.parametrize("transpose", [False, True])
 @pytest.mark.parametrize("shape", [(128, 128, 64), (200, 300, 100), (1, 1, 1), (513, 257, 1000), (1024, 768, 512),
-                                   (64, 1000, 7)])
-def test_gemm_cm2(gpu, oracle, shape, transpose):
+                                   (64, 1000, 7), (1032, 520, 264)])
+def test_gemm_cm2(gpu, oracle, shape, transpose, vocabulary):
+    """Both forms: the tile kernel (default) and the tensor-vocabulary kernel."""
     lh = gpu
     M, N, K = shape
-    announce(f"gemm_cm2 M={M} N={N} K={K} transpose_c={transpose}")
+    announce(f"gemm_cm2 M={M} N={N} K={K} transpose_c={transpose} vocabulary={vocabulary}")
     A = lh.HIPDeviceArray("f16", (M, K), order="C")
     B = lh.HIPDeviceArray("f16", (K, N), order="C")
     lh.fill_uniform(A, 8000 + M, -1.0, 1.0)
     lh.fill_uniform(B, 8100 + N, -1.0, 1.0)
     Cm = lh.HIPDeviceArray("f16", (N, M) if transpose else (M, N), order="C")
     Cm.fill_bytes(0xFF)
-    lh.gemm_cm2(Cm, A, B, transpose=transpose)
+    lh.gemm_cm2(Cm, A, B, transpose=transpose, vocabulary=vocabulary)
     got = Cm.to_numpy().astype(np.float64)
     if transpose:
         got = got.T
@@ -162,6 +164,11 @@ def test_gemm_cm2_k_zero_and_errors(gpu):
     Cm.fill_bytes(0xFF)
     lh.gemm_cm2(Cm, A, B)
     assert np.all(Cm.to_numpy() == 0)
+    Cm.fill_bytes(0xFF)
+    lh.gemm_cm2(Cm, A, B, vocabulary=True)
+    assert np.all(Cm.to_numpy() == 0)
+    with pytest.raises(lh.InvalidArgument):
+        lh._lib.call("lava_hip_gemm_cm2_f16", Cm.ptr, Cm.ptr, Cm.ptr, 130, 70, 16, 16, 70, 70, 4, None)
     with pytest.raises(lh.InvalidArgument):
         lh._lib.call("lava_hip_gemm_cm2_f16", Cm.ptr, Cm.ptr, Cm.ptr, 130, 70, 16, 8, 70, 70, 0, None)
     l = lh.tensor_setdim(lh.tensor_layout(2, 1), (4, 4))
