@@ -210,8 +210,8 @@ typedef struct lava_hip_tensor_layout {
 /* m = tensor_load(object, src, layout[, view]) on one fragment, then stored row-major to
  * `out` (R x C, dtype LAVA_HIP_F16 or LAVA_HIP_F32).  `object` (R x C, row-major) is the
  * matrix whose values elements outside the slice keep; elements inside the slice but
- * outside the tensor read the clamp constant (CONSTANT, UNDEFINED) or the nearest element
- * (TO_EDGE).  transpose != 0 loads through the (1, 0) TensorView.
+ * outside the tensor read the clamp constant (CONSTANT), the nearest element (TO_EDGE),
+ * or keep the object's value (UNDEFINED).  transpose != 0 loads through the (1, 0) TensorView.
  * Replaces lava_tensor_load (src/device/tensor_intrinsics.jl:258-320) and KernelInterface's
  * tensor_load (tensor.jl:98-105). */
 int lava_hip_tensor_load_tile(int dtype, int shape, const void* src, const lava_hip_tensor_layout* layout,

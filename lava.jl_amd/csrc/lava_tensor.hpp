@@ -16,8 +16,8 @@
 //  * load: an element outside the slice's sizes keeps the object matrix's value; an
 //    element inside the slice but outside the tensor reads the clamp constant
 //    (TENSOR_CLAMP_CONSTANT, default zero), the nearest element inside
-//    (TENSOR_CLAMP_TO_EDGE) or, for TENSOR_CLAMP_UNDEFINED, the clamp constant too
-//    (any value is allowed there; this one never touches memory);
+//    (TENSOR_CLAMP_TO_EDGE), or keeps the object's value (TENSOR_CLAMP_UNDEFINED:
+//    "elements a clamping layout leaves out keep m's values", tensor.jl:98-104);
 //  * store: only elements inside both the slice and the tensor are written;
 //  * the clamp value is given as bits, those of the value in the matrix's component
 //    type zero-extended (tensor_clampbits, tensor.jl:83-85).
@@ -150,7 +150,7 @@ __device__ __forceinline__ Frag<T, R, C, U> tensor_load(Frag<T, R, C, U> m, cons
         if (!tensor_elem(l, outer, outer_in, TRANS ? c : r, TRANS ? r : c, &idx, &in)) continue;
         if (in)
             m.v[j] = base[idx];
-        else
+        else if (l.clamp != ClampUndefined)
             m.v[j] = cval;
     }
     return m;

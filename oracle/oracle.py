@@ -310,9 +310,9 @@ def _tensor_elem(l: dict, outer: int, outer_in: bool, i0: int, i1: int):
 def tensor_load(obj: np.ndarray, src: np.ndarray, l: dict, clamp_value, transpose: bool = False) -> np.ndarray:
     """tensor_load(obj, src, layout[, view]): matrix element (r, c) is slice element
     (r, c), or (c, r) through the transposing view; outside the slice it keeps obj's
-    value; inside the slice but outside the tensor it reads `clamp_value` (CONSTANT,
-    UNDEFINED) or the nearest element (TO_EDGE).  `src` is the flat memory the layout
-    addresses."""
+    value; inside the slice but outside the tensor it reads `clamp_value` (CONSTANT),
+    the nearest element (TO_EDGE) or keeps obj's value (UNDEFINED).  `src` is the flat
+    memory the layout addresses."""
     out = obj.copy()
     outer, outer_in = _tensor_outer(l)
     for r in range(obj.shape[0]):
@@ -320,7 +320,10 @@ def tensor_load(obj: np.ndarray, src: np.ndarray, l: dict, clamp_value, transpos
             e = _tensor_elem(l, outer, outer_in, c if transpose else r, r if transpose else c)
             if e is None:
                 continue
-            out[r, c] = src[e[0]] if e[1] else clamp_value
+            if e[1]:
+                out[r, c] = src[e[0]]
+            elif l["clamp"] != CLAMP_UNDEFINED:
+                out[r, c] = clamp_value
     return out
 
 

@@ -63,7 +63,7 @@ def test_tensor_load_tile(gpu, oracle, shape, dtype):
     for clamp in (lh.TENSOR_CLAMP_UNDEFINED, lh.TENSOR_CLAMP_CONSTANT, lh.TENSOR_CLAMP_TO_EDGE):
         for transpose in (False, True):
             for rank, shrink in ((2, False), (2, True), (3, False), (2, False)):
-                cv = 2.5 if clamp != lh.TENSOR_CLAMP_UNDEFINED else 0.0
+                cv = 2.5   # UNDEFINED keeps the object instead, whatever the clamp value
                 l, nmem = random_layout(lh, rng, R, C, clamp, transpose, rank, dtype, cv, shrink)
                 announce(f"tensor_load {shape} {dtype} clamp={clamp} T={transpose} {l}")
                 mem = (rng.standard_normal(nmem) * 4).astype(NP[dtype])

@@ -367,6 +367,17 @@ def test_tensor_load_transposing_view(oracle):
     assert not np.array_equal(plain, got)
 
 
+def test_tensor_load_undefined_keeps_object_outside_tensor(oracle):
+    """UNDEFINED: elements of the slice past the tensor keep the object's value (the
+    clamp constant is not read); the elements inside are the submatrix."""
+    mem = np.arange(20 * 30, dtype=np.float64)
+    obj = np.full((16, 16), -3.0)
+    l = _layout((20, 30), (30, 1), (10, 20), (16, 16), clamp=0)
+    got = oracle.tensor_load(obj, mem, l, 99.0)
+    np.testing.assert_array_equal(got[:10, :10], mem.reshape(20, 30)[10:20, 20:30])
+    assert np.all(got[10:, :] == -3.0) and np.all(got[:, 10:] == -3.0)
+
+
 def test_tensor_load_keeps_object_outside_slice(oracle):
     mem = np.arange(20 * 30, dtype=np.float64)
     obj = np.full((16, 16), -5.0)
