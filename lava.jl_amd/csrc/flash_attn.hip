@@ -346,7 +346,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool late = w >= F3_WAVES / 2;        // one phase behind its SIMD partner w - 4
-    const int nqb = p.S / F3_BQ;
+    const int nqb = (p.S + F3_BQ - 1) / F3_BQ;   // the last query block may be partial
     const int nbh = p.H * p.B;
     int bid = blockIdx.x;
     const int total = nqb * nbh;
@@ -361,12 +361,17 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     const int r32 = lane & 31, h = lane >> 5;
     const int my_q = q0 + r32;
 
-    // Q^T as B operand: lane (query my_q, half h) holds d = 16 ks + 8 h + [0, 8)
+    // Q^T as B operand: lane (query my_q, half h) holds d = 16 ks + 8 h + [0, 8);
+    // queries past S (a ragged last block) compute on zeros and are not stored
     f16x8 qf[8];
     {
         const f16* qrow = p.Q + head + (int64_t)my_q * p.sl + 8 * h;
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
+        for (int ks = 0; ks < 8; ++ks) qf[ks] = f16x8{};
+        if (my_q < p.S) {
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
+        }
     }
 
     // ---- LDS-DMA: wave w moves rows [8 w, 8 w + 8) of a K or V tile in two
@@ -375,24 +380,35 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     const f3_v4i rk = f3_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
     const f3_v4i rv = f3_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
     uint32_t voff_k[2], voff_v[2];
+    int dma_row[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int row = 8 * w + 4 * i + (lane >> 4);
+        dma_row[i] = row;
         const int pc = lane & 15;
         voff_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ (row & 15));
         voff_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ (4 * (row & 3)));
     }
     const uint32_t lds_k = f3_lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * 256;
     const uint32_t lds_v = f3_lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * 256;
-    const int nkb = CAUSAL ? (qb * F3_BQ + F3_BQ) / F3_BK : p.S / F3_BK;
+    const int nkb_s = (p.S + F3_BK - 1) / F3_BK;   // key blocks holding keys < S
+    const int nkb = CAUSAL ? min((qb * F3_BQ + F3_BQ) / F3_BK, nkb_s) : nkb_s;
     // block j -> stage j % F3_STAGES; blocks past the end re-read the last one so
-    // that every MFMA phase issues the same number of DMAs (the vmcnt accounting)
+    // that every MFMA phase issues the same number of DMAs (the vmcnt accounting).
+    // A row at or past S gets an offset beyond the resource (2^31 > S * row bytes,
+    // no wrap with soffset), so it reads zero whether or not the range check counts
+    // soffset; its scores are masked.
     auto issue = [&](const f3_v4i& rsrc, const uint32_t* voff, uint32_t lds, int j) {
         const int src = j < nkb ? j : nkb - 1;
         const uint32_t soff = (uint32_t)src * F3_BK * row_bytes;
         const uint32_t dst = lds + (uint32_t)(j % F3_STAGES) * F3_TILE;
-        f3_dma16(rsrc, voff[0], soff, dst);
-        f3_dma16(rsrc, voff[1], soff, dst + 1024);
+        uint32_t v0 = voff[0], v1 = voff[1];
+        if ((src + 1) * F3_BK > p.S) {   // uniform: only the ragged last block checks rows
+            v0 = src * F3_BK + dma_row[0] < p.S ? v0 : 0x80000000u;
+            v1 = src * F3_BK + dma_row[1] < p.S ? v1 : 0x80000000u;
+        }
+        f3_dma16(rsrc, v0, soff, dst);
+        f3_dma16(rsrc, v1, soff, dst + 1024);
     };
 
     // K fragment (kt, ks): row 32 kt + r32, logical chunk 2 ks + h, stored at chunk ^ (row % 16)
@@ -485,12 +501,21 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     auto softmax = [&](int kb) {
         const int key0 = kb * F3_BK;
         if (CAUSAL && key0 + F3_BK - 1 > q0) {
+            // (for a query < S every key past S is also past the query)
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * h + (r & 3);
                     st[kt][r] = key > my_q ? -INFINITY : st[kt][r];
+                }
+        } else if (!CAUSAL && key0 + F3_BK > p.S) {   // the ragged last key block
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = key0 + 32 * kt + 8 * (r >> 2) + 4 * h + (r & 3);
+                    st[kt][r] = key >= p.S ? -INFINITY : st[kt][r];
                 }
         }
         float mx = -INFINITY;
@@ -576,6 +601,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // ---- O / L, fp16.  o[dt] register r: d = 32 dt + 8 (r / 4) + 4 h + r % 4 of query my_q.
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
     const float inv = 1.f / l_tot;
+    if (my_q >= p.S) return;
     f16* orow = Ob + (int64_t)my_q * p.osl;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -662,15 +688,19 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     p.causal = causal != 0;
     hipStream_t s = as_stream(stream);
 
-    bool fast = D == FA_D && S % FA_BQ == 0;
-    for (int i = 1; i < 4; ++i) fast = fast && strides[i] % 8 == 0 && os[i] % 4 == 0;
-    fast = fast && aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8);
+    // D = 128 with 16-byte rows: the MFMA kernels.  flash_fwd3_kernel takes any S (a
+    // ragged last block of queries or keys is zero-filled and masked); the older
+    // 128-query kernel remains for scale <= 0 (the base-2 running maximum assumes
+    // a positive scale) with S a multiple of 128.
+    bool lay_ok = D == FA_D;
+    for (int i = 1; i < 4; ++i) lay_ok = lay_ok && strides[i] % 8 == 0 && os[i] % 4 == 0;
+    lay_ok = lay_ok && aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8);
     const int64_t blocks = (S / FA_BQ) * H * B;
-    fast = fast && blocks <= 0x7fffffff;
-    const bool fast3 = fast && S % F3_BQ == 0 && scale > 0.f && S * strides[1] * 2 < ((int64_t)1 << 31) &&
-                       (S / F3_BQ) * H * B <= 0x7fffffff;
+    const bool fast = lay_ok && S % FA_BQ == 0 && blocks <= 0x7fffffff;
+    const int64_t blocks3 = ((S + F3_BQ - 1) / F3_BQ) * H * B;
+    const bool fast3 = lay_ok && scale > 0.f && S * strides[1] * 2 < ((int64_t)1 << 31) && blocks3 <= 0x7fffffff;
     if (fast3) {
-        const dim3 grid((unsigned)((S / F3_BQ) * H * B));
+        const dim3 grid((unsigned)blocks3);
         if (p.causal)
             hipLaunchKernelGGL(flash_fwd3_kernel<true>, grid, dim3(64 * F3_WAVES), 0, s, p);
         else

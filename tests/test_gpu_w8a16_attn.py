@@ -91,7 +91,32 @@ def test_flash_fast_path(gpu, oracle, causal, E, L, H, B):
     check_heads(oracle, Q, K, V, O, 1 / math.sqrt(E), causal, heads, np.arange(L))
 
 
-@pytest.mark.parametrize("E,L,causal", [(64, 200, True), (16, 32, True), (96, 130, False), (128, 100, True)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("L", [1, 7, 100, 255, 257, 1000, 1537])
+def test_flash_fast_ragged_s(gpu, oracle, causal, L):
+    """D = 128 with S not a multiple of the 256-query block: the fast kernel zero-fills the
+    K/V rows past S (offsets beyond the buffer resource), masks their scores, computes the
+    queries past S on zeros and does not store them.  Every row of every head up to S = 257,
+    edge rows plus a sample beyond."""
+    lh = gpu
+    E, H, B = 128, 2, 2
+    announce(f"flash fast ragged D={E} S={L} causal={causal}")
+    Q, K, V = attn_inputs(lh, E, L, H, B)
+    O = lh.HIPDeviceArray("f16", (E, L, H, B))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, causal=causal)
+    if L <= 257:
+        rows = np.arange(L)
+    else:
+        rng = np.random.default_rng(L)
+        edge = [0, 1, 63, 64, 255, 256, L - 65, L - 64, L - 2, L - 1]
+        rows = np.unique(np.concatenate([[r for r in edge if 0 <= r < L], rng.integers(0, L, 24)]))
+    heads = [(b, h) for b in range(B) for h in range(H)]
+    check_heads(oracle, Q, K, V, O, 1 / math.sqrt(E), causal, heads, rows)
+    assert not np.isnan(O.to_numpy()).any()
+
+
+@pytest.mark.parametrize("E,L,causal", [(64, 200, True), (16, 32, True), (96, 130, False), (64, 100, False)])
 def test_flash_generic_path(gpu, oracle, E, L, causal):
     """Head dims and sequence lengths outside the fast kernel's tiling."""
     lh = gpu
