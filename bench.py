@@ -10,7 +10,7 @@ before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|
-                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|copy]
+                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|copy]
 
 A step is one kernel launch over the whole problem.  Kernel time comes from HIP
 events recorded on the launch stream around the K timed launches; wall time
@@ -208,7 +208,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
-                             "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "copy"])
+                             "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -259,6 +259,12 @@ def main():
                                                             "zero-clamped loads, bounds-checked store)"},
                     "kernel_ms": round(kms, 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "attn_d64":
+        flop, kms, wms = bench_attn(lh, K, W, stream, D=64)
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "f16", "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=64"},
+                    "kernel_ms": round(kms, 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_bf16_nn":
         flop, kms, wms = bench_gemm_layout(lh, "bf16", 8192, 1 | 2 | 4, K, W, stream, 1)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),

@@ -277,7 +277,6 @@ constexpr int F3_WAVES = 8;
 constexpr int F3_BQ = 32 * F3_WAVES;        // 256 queries per workgroup
 constexpr int F3_BK = 64;
 constexpr int F3_STAGES = 3;
-constexpr int F3_TILE = F3_BK * FA_D * 2;   // 16 KB: one K or V block
 constexpr float F3_RESCALE = 8.0f;
 constexpr int F3_PREFETCH = 4;        // MFMA-phase operations between an LDS read and its use
 
@@ -332,16 +331,40 @@ __device__ __forceinline__ void f3_pin(const f32x16& v) {
     for (int i = 0; i < 16; i += 4) asm volatile("; pin" ::"v"(v[i]), "v"(v[i + 1]), "v"(v[i + 2]), "v"(v[i + 3]));
 }
 
-// All waits for the DMAs of the phase before last, then the workgroup barrier.
+// All waits for the DMAs of the phase before last (N = the DMA instructions one
+// phase issues), then the workgroup barrier.
+template <int N>
 __device__ __forceinline__ void f3_phase_end() {
-    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    static_assert(N == 4 || N == 2, "K and V tiles of 2 or 1 instructions per wavefront");
+    if constexpr (N == 4)
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     __syncthreads();
 }
 
-template <bool CAUSAL>
+// DH = 128 or 64: the head dimension sets the row size (DH * 2 bytes = CH chunks of
+// 16 bytes), the number of S^T k-steps (DH / 16) and of O^T row tiles (DH / 32), and
+// the swizzles: K chunk ^ (key % 16) for 16-chunk rows, ^ ((key % 8) ^ (key / 8 % 2))
+// for 8-chunk rows (a fragment read, 32 keys x one chunk, spread over the banks);
+// V chunk ^ 4 (key % 4), resp. ^ 2 (key % 4) (a transposing read, 4 keys x 2 chunks per
+// 16-lane group).
+template <bool CAUSAL, int DH>
 __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p) {
-    __shared__ __attribute__((aligned(1024))) uint8_t kbuf[F3_STAGES][F3_TILE];   // [stage][key][256 B]
-    __shared__ __attribute__((aligned(1024))) uint8_t vbuf[F3_STAGES][F3_TILE];
+    static_assert(DH == 128 || DH == 64, "head dimension 128 or 64");
+    constexpr int RB = DH * 2;                             // bytes per K / V row
+    constexpr int CH = RB / 16;                            // 16-byte chunks per row
+    constexpr int TILE = F3_BK * RB;                       // one K or V block
+    constexpr int NKS = DH / 16;                           // S^T MFMAs per key tile
+    constexpr int NDT = DH / 32;                           // O^T row tiles
+    constexpr int NPV = 4 * NDT;                           // O^T MFMAs per block
+    constexpr int NOPS = NPV + 2 * NKS;                    // MFMAs of a full phase
+    constexpr int DPT = TILE / (1024 * F3_WAVES);          // DMA instructions per wavefront per tile
+    constexpr int RPI = 64 / CH;                           // rows per DMA instruction
+    __shared__ __attribute__((aligned(1024))) uint8_t kbuf[F3_STAGES][TILE];   // [stage][key][RB]
+    __shared__ __attribute__((aligned(1024))) uint8_t vbuf[F3_STAGES][TILE];
+    auto kswz = [](int row) { return CH == 16 ? (row & 15) : ((row & 7) ^ ((row >> 3) & 1)); };
+    auto vswz = [](int row) { return CH == 16 ? 4 * (row & 3) : 2 * (row & 3); };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -363,34 +386,34 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
 
     // Q^T as B operand: lane (query my_q, half h) holds d = 16 ks + 8 h + [0, 8);
     // queries past S (a ragged last block) compute on zeros and are not stored
-    f16x8 qf[8];
+    f16x8 qf[NKS];
     {
         const f16* qrow = p.Q + head + (int64_t)my_q * p.sl + 8 * h;
 #pragma unroll
-        for (int ks = 0; ks < 8; ++ks) qf[ks] = f16x8{};
+        for (int ks = 0; ks < NKS; ++ks) qf[ks] = f16x8{};
         if (my_q < p.S) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
+            for (int ks = 0; ks < NKS; ++ks) qf[ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
         }
     }
 
-    // ---- LDS-DMA: wave w moves rows [8 w, 8 w + 8) of a K or V tile in two
-    // instructions: instruction i covers rows 8 w + 4 i + lane / 16, physical chunk lane % 16.
+    // ---- LDS-DMA: wave w moves rows [8 w, 8 w + 8) of a K or V tile in DPT
+    // instructions: instruction i covers rows 8 w + RPI i + lane / CH, physical chunk lane % CH.
     const uint32_t row_bytes = (uint32_t)(p.sl * 2);
     const f3_v4i rk = f3_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
     const f3_v4i rv = f3_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
-    uint32_t voff_k[2], voff_v[2];
-    int dma_row[2];
+    uint32_t voff_k[DPT], voff_v[DPT];
+    int dma_row[DPT];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int row = 8 * w + 4 * i + (lane >> 4);
+    for (int i = 0; i < DPT; ++i) {
+        const int row = 8 * w + RPI * i + lane / CH;
         dma_row[i] = row;
-        const int pc = lane & 15;
-        voff_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ (row & 15));
-        voff_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ (4 * (row & 3)));
+        const int pc = lane % CH;
+        voff_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ kswz(row));
+        voff_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ vswz(row));
     }
-    const uint32_t lds_k = f3_lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * 256;
-    const uint32_t lds_v = f3_lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * 256;
+    const uint32_t lds_k = f3_lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * RB;
+    const uint32_t lds_v = f3_lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * RB;
     const int nkb_s = (p.S + F3_BK - 1) / F3_BK;   // key blocks holding keys < S
     const int nkb = CAUSAL ? min((qb * F3_BQ + F3_BQ) / F3_BK, nkb_s) : nkb_s;
     // block j -> stage j % F3_STAGES; blocks past the end re-read the last one so
@@ -401,34 +424,37 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     auto issue = [&](const f3_v4i& rsrc, const uint32_t* voff, uint32_t lds, int j) {
         const int src = j < nkb ? j : nkb - 1;
         const uint32_t soff = (uint32_t)src * F3_BK * row_bytes;
-        const uint32_t dst = lds + (uint32_t)(j % F3_STAGES) * F3_TILE;
-        uint32_t v0 = voff[0], v1 = voff[1];
+        const uint32_t dst = lds + (uint32_t)(j % F3_STAGES) * TILE;
+        uint32_t v[DPT];
+#pragma unroll
+        for (int i = 0; i < DPT; ++i) v[i] = voff[i];
         if ((src + 1) * F3_BK > p.S) {   // uniform: only the ragged last block checks rows
-            v0 = src * F3_BK + dma_row[0] < p.S ? v0 : 0x80000000u;
-            v1 = src * F3_BK + dma_row[1] < p.S ? v1 : 0x80000000u;
+#pragma unroll
+            for (int i = 0; i < DPT; ++i) v[i] = src * F3_BK + dma_row[i] < p.S ? v[i] : 0x80000000u;
         }
-        f3_dma16(rsrc, v0, soff, dst);
-        f3_dma16(rsrc, v1, soff, dst + 1024);
+#pragma unroll
+        for (int i = 0; i < DPT; ++i) f3_dma16(rsrc, v[i], soff, dst + 1024 * i);
     };
 
-    // K fragment (kt, ks): row 32 kt + r32, logical chunk 2 ks + h, stored at chunk ^ (row % 16)
-    int k_off[8];
+    // K fragment (kt, ks): row 32 kt + r32, logical chunk 2 ks + h, stored at chunk ^ kswz(row)
+    // (kswz depends on row % 16 = r32 % 16 only)
+    int k_off[NKS];
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) k_off[ks] = r32 * 256 + (((2 * ks + h) ^ (lane & 15)) << 4);
+    for (int ks = 0; ks < NKS; ++ks) k_off[ks] = r32 * RB + (((2 * ks + h) ^ kswz(r32)) << 4);
     // V^T fragment (dt, kk = 32 kt + 16 ks, read t = 0/1): source lane jj = (lane % 16) / 4,
     // q = lane % 4, dh = (lane / 16) % 2 addresses V[kk + 8 t + 4 h + jj][32 dt + 16 dh + 4 q],
-    // logical chunk 4 dt + 2 dh + q / 2 stored at chunk ^ 4 jj (jj = key % 4 as kk % 8 == 0).
-    int v_off[4];
+    // logical chunk 4 dt + 2 dh + q / 2 stored at chunk ^ vswz(jj) (jj = key % 4 as kk % 8 == 0).
+    int v_off[NDT];
     {
         const int jj = (lane & 15) >> 2, q = lane & 3, dh = (lane >> 4) & 1;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-            v_off[dt] = (4 * h + jj) * 256 + (((4 * (dt ^ jj)) + 2 * dh + (q >> 1)) << 4) + ((q & 1) << 3);
+        for (int dt = 0; dt < NDT; ++dt)
+            v_off[dt] = (4 * h + jj) * RB + (((4 * dt + 2 * dh + (q >> 1)) ^ vswz(jj)) << 4) + ((q & 1) << 3);
     }
 
-    f32x16 o[4];
+    f32x16 o[NDT];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[dt][r] = 0.f;
     float m_run = -INFINITY;   // running max of the scaled scores (log2 units)
@@ -437,32 +463,33 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     f32x16 st[2];              // S^T of the current block: st[kt] register r = key 32 kt + 8 (r / 4) + 4 h + r % 4
     f16x8 pf[2][2];            // P^T of the previous block, B operand [kt][ks]: keys 32 kt + 16 ks + 8 (i / 4) + 4 h + i % 4
 
-    // The MFMA phase as one list of 32 operations -- ops [0, 16): O^T += V^T P^T for
-    // the previous block (kt = i / 8, ks = i / 4 % 2, dt = i % 4); ops [16, 32):
-    // S^T = K Q^T (ks = (i - 16) / 2, kt = i % 2) -- whose LDS operand reads run
-    // F3_PREFETCH operations ahead of the MFMAs (the partner wavefront is in its
-    // softmax phase, so nothing else hides the LDS latency).
+    // The MFMA phase as one list of NOPS operations -- ops [0, NPV): O^T += V^T P^T
+    // for the previous block (kt = i / (2 NDT), ks = i / NDT % 2, dt = i % NDT); ops
+    // [NPV, NOPS): S^T = K Q^T (ks = (i - NPV) / 2, kt = i % 2) -- whose LDS operand
+    // reads run F3_PREFETCH operations ahead of the MFMAs (the partner wavefront is in
+    // its softmax phase, so nothing else hides the LDS latency).
     auto read_op = [&](int i, const uint8_t* vbase, const uint8_t* kbase) -> f16x8 {
-        if (i < 16) {
-            const int kk = 32 * (i >> 3) + 16 * ((i >> 2) & 1), dt = i & 3;
-            const f3_s16x4 lo = f3_read_tr(vbase + v_off[dt] + kk * 256);
-            const f3_s16x4 hi = f3_read_tr(vbase + v_off[dt] + (kk + 8) * 256);
+        if (i < NPV) {
+            const int kk = 32 * (i / (2 * NDT)) + 16 * ((i / NDT) & 1), dt = i % NDT;
+            const f3_s16x4 lo = f3_read_tr(vbase + v_off[dt] + kk * RB);
+            const f3_s16x4 hi = f3_read_tr(vbase + v_off[dt] + (kk + 8) * RB);
             return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
-        const int j = i - 16;
-        return *reinterpret_cast<const f16x8*>(kbase + k_off[j >> 1] + (j & 1) * 32 * 256);
+        const int j = i - NPV;
+        return *reinterpret_cast<const f16x8*>(kbase + k_off[j >> 1] + (j & 1) * 32 * RB);
     };
     auto mma_op = [&](int i, f16x8 a) {
-        if (i < 16) {
-            o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[i >> 3][(i >> 2) & 1], o[i & 3], 0, 0, 0);
+        if (i < NPV) {
+            o[i % NDT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pf[i / (2 * NDT)][(i / NDT) & 1], o[i % NDT], 0,
+                                                                 0, 0);
         } else {
-            const int j = i - 16;
+            const int j = i - NPV;
             st[j & 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[j >> 1], j < 2 ? f32x16{} : st[j & 1], 0, 0, 0);
         }
     };
     auto mfma_phase = [&](auto pv_tag, auto s_tag, const uint8_t* vbase, const uint8_t* kbase) {
-        constexpr int first = decltype(pv_tag)::value ? 0 : 16;
-        constexpr int last = decltype(s_tag)::value ? 32 : 16;
+        constexpr int first = decltype(pv_tag)::value ? 0 : NPV;
+        constexpr int last = decltype(s_tag)::value ? NOPS : NPV;
         f16x8 buf[F3_PREFETCH];
 #pragma unroll
         for (int t = 0; t < F3_PREFETCH; ++t)
@@ -485,7 +512,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // the loop, instead of as vmcnt waits inside it (which would also cover the
     // DMAs issued in the loop, since it does not count those).
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < NKS; ++ks) {
         const uint4 u = __builtin_bit_cast(uint4, qf[ks]);
         asm volatile("" ::"v"(u.x), "v"(u.y), "v"(u.z), "v"(u.w));
     }
@@ -529,7 +556,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
             l_run *= alpha;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
             m_run = m_new;
@@ -555,7 +582,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) f3_pin(pf[kt][ks]);
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) f3_pin(o[dt]);
+        for (int dt = 0; dt < NDT; ++dt) f3_pin(o[dt]);
         asm volatile("; pin" ::"v"(l_run), "v"(m_run));
     };
     // Every MFMA phase issues the DMAs of K block kb + 2 and V block kb + 1: the
@@ -573,27 +600,27 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // iteration 0: S only
     dma(0);
     mfma_phase(f3_tag<false>{}, f3_tag<true>{}, vb(0), kbuf_of(0));
-    f3_phase_end();
+    f3_phase_end<2 * DPT>();
     softmax(0);
-    f3_phase_end();
+    f3_phase_end<2 * DPT>();
     // iterations 1 .. last: O += V^T P^T for block kb - 1, then S for block kb
     for (int kb = 1; kb <= last; ++kb) {
         dma(kb);
         mfma_phase(f3_tag<true>{}, f3_tag<true>{}, vb(kb), kbuf_of(kb));
-        f3_phase_end();
+        f3_phase_end<2 * DPT>();
         softmax(kb);
-        f3_phase_end();
+        f3_phase_end<2 * DPT>();
     }
     // iteration last + 1: the final O update
     dma(last + 1);
     mfma_phase(f3_tag<true>{}, f3_tag<false>{}, vb(last + 1), kbuf_of(last + 1));
-    f3_phase_end();
-    f3_phase_end();
+    f3_phase_end<2 * DPT>();
+    f3_phase_end<2 * DPT>();
     // remaining iterations (causal: blocks past this wavefront's queries)
     for (int kb = last + 2; kb <= nkb; ++kb) {
         dma(kb);
-        f3_phase_end();
-        f3_phase_end();
+        f3_phase_end<2 * DPT>();
+        f3_phase_end<2 * DPT>();
     }
     if (!late) __builtin_amdgcn_s_barrier();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -604,7 +631,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     if (my_q >= p.S) return;
     f16* orow = Ob + (int64_t)my_q * p.osl;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
             const int d = 32 * dt + 8 * g4 + 4 * h;
@@ -692,19 +719,25 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     // ragged last block of queries or keys is zero-filled and masked); the older
     // 128-query kernel remains for scale <= 0 (the base-2 running maximum assumes
     // a positive scale) with S a multiple of 128.
-    bool lay_ok = D == FA_D;
+    bool lay_ok = D == FA_D || D == 64;
     for (int i = 1; i < 4; ++i) lay_ok = lay_ok && strides[i] % 8 == 0 && os[i] % 4 == 0;
     lay_ok = lay_ok && aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8);
     const int64_t blocks = (S / FA_BQ) * H * B;
-    const bool fast = lay_ok && S % FA_BQ == 0 && blocks <= 0x7fffffff;
+    const bool fast = lay_ok && D == FA_D && S % FA_BQ == 0 && blocks <= 0x7fffffff;
     const int64_t blocks3 = ((S + F3_BQ - 1) / F3_BQ) * H * B;
     const bool fast3 = lay_ok && scale > 0.f && S * strides[1] * 2 < ((int64_t)1 << 31) && blocks3 <= 0x7fffffff;
     if (fast3) {
         const dim3 grid((unsigned)blocks3);
-        if (p.causal)
-            hipLaunchKernelGGL(flash_fwd3_kernel<true>, grid, dim3(64 * F3_WAVES), 0, s, p);
-        else
-            hipLaunchKernelGGL(flash_fwd3_kernel<false>, grid, dim3(64 * F3_WAVES), 0, s, p);
+        if (D == 64) {
+            if (p.causal)
+                hipLaunchKernelGGL((flash_fwd3_kernel<true, 64>), grid, dim3(64 * F3_WAVES), 0, s, p);
+            else
+                hipLaunchKernelGGL((flash_fwd3_kernel<false, 64>), grid, dim3(64 * F3_WAVES), 0, s, p);
+        } else if (p.causal) {
+            hipLaunchKernelGGL((flash_fwd3_kernel<true, 128>), grid, dim3(64 * F3_WAVES), 0, s, p);
+        } else {
+            hipLaunchKernelGGL((flash_fwd3_kernel<false, 128>), grid, dim3(64 * F3_WAVES), 0, s, p);
+        }
         LAVA_LAUNCH_CHECK("flash_fwd3_kernel");
         return LAVA_HIP_OK;
     }

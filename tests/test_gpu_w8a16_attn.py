@@ -116,7 +116,24 @@ def test_flash_fast_ragged_s(gpu, oracle, causal, L):
     assert not np.isnan(O.to_numpy()).any()
 
 
-@pytest.mark.parametrize("E,L,causal", [(64, 200, True), (16, 32, True), (96, 130, False), (64, 100, False)])
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("L", [64, 256, 777, 2048])
+def test_flash_fast_d64(gpu, oracle, causal, L):
+    """Head dimension 64 on the MFMA kernel (128-byte rows, 4 S^T k-steps, 2 O^T tiles)."""
+    lh = gpu
+    E, H, B = 64, 2, 2
+    announce(f"flash fast D=64 S={L} causal={causal}")
+    Q, K, V = attn_inputs(lh, E, L, H, B)
+    O = lh.HIPDeviceArray("f16", (E, L, H, B))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, causal=causal)
+    rng = np.random.default_rng(L + 1)
+    rows = np.arange(L) if L <= 256 else np.unique(np.concatenate([[0, 1, 255, 256, L - 1], rng.integers(0, L, 32)]))
+    check_heads(oracle, Q, K, V, O, 1 / math.sqrt(E), causal, [(b, h) for b in range(B) for h in range(H)], rows)
+    assert not np.isnan(O.to_numpy()).any()
+
+
+@pytest.mark.parametrize("E,L,causal", [(32, 200, True), (16, 32, True), (96, 130, False), (48, 100, False)])
 def test_flash_generic_path(gpu, oracle, E, L, causal):
     """Head dims and sequence lengths outside the fast kernel's tiling."""
     lh = gpu
