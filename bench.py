@@ -325,9 +325,16 @@ def main():
         lh.synchronize()
         kms, wms = timed(lh, lambda: lh._lib.call("lava_hip_memcpy_d2d", dst.ptr, src.ptr, nbytes, stream), K, W,
                          stream)
+        # the device as it reports itself: the dense fp16/bf16 peak re-derived as
+        # CUs x max clock x 4096 FLOP per clock per CU, beside the vendor figure
+        dp = lh.vocabulary.device_properties()
         out.update({"value": round(2 * nbytes / (kms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 4),
                     "dtype": "u8", "config": {"workload": "device copy of 1 GiB (read + write bytes)"},
                     "kernel_ms": round(kms, 4),
+                    "device": {"cus": dp["cores"], "max_clock_mhz": dp["clock_khz"] / 1000.0,
+                               "hbm_gib": round(dp["hbm_bytes"] / 2**30, 1), "l2_mib": round(dp["l2_bytes"] / 2**20, 1),
+                               "derived_peak_bf16_tflops": round(dp["cores"] * dp["clock_khz"] * 1e3 * 4096 / 1e12, 1),
+                               "vendor_peak_bf16_tflops": PEAK_BF16_TFLOPS},
                     "roofline": roofline("hbm", 2 * nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s", 2 * nbytes)})
 
     if args.workload in ("headline", "gemm_bf16") and not args.no_cpu_baseline:

@@ -60,6 +60,16 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
+// Vectors in LDS: the components packed, aligned to 2x (2 components) or 4x
+// (4 components) the component -- the layout Lava's emitter gives `@localmem`
+// vectors (src/compiler/spirv/types.jl:838-900, test_workgroup_vector_layout.jl:24-27).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+static_assert(sizeof(f16x2) == 4 && alignof(f16x2) == 4, "<2 x half> in LDS: 4 bytes, align 4");
+static_assert(sizeof(f16x4) == 8 && alignof(f16x4) == 8, "<4 x half> in LDS: 8 bytes, align 8");
+static_assert(sizeof(f32x2) == 8 && alignof(f32x2) == 8, "<2 x float> in LDS: 8 bytes, align 8");
+static_assert(sizeof(f32x4) == 16 && alignof(f32x4) == 16, "<4 x float> in LDS: 16 bytes, align 16");
+
 enum Use { MatrixA = 0, MatrixB = 1, Accumulator = 2 };
 
 // CoopMatReduce masks (src/vocabulary/coopmat.jl:292-297)

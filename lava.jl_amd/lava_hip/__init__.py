@@ -17,7 +17,7 @@ from .tensor import (TENSOR_CLAMP_CONSTANT, TENSOR_CLAMP_TO_EDGE, TENSOR_CLAMP_U
 from .vocabulary import (Accumulator, CoopMatReduce, DeviceCaps, MatrixA, MatrixB, MatrixShape, SubgroupScope,
                          WorkgroupScope, bestshape, caps, isbetter, library_shapes, matrix_shapes, supports,
                          supports_coopmat_perelement, supports_coopmat_reduce, supports_flexible_coopmat_shapes,
-                         supports_tensor_addressing, wggranularity)
+                         supports_tensor_addressing, wggranularity, workgroup_layout)
 
 # Input seeds: base "LAVA" + 256 * config index + tensor id (A=0, B=1, scale=2; Q=0, K=1, V=2).
 SEED_BASE = 0x4C415641

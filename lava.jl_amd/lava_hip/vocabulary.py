@@ -186,6 +186,26 @@ def supports_tensor_addressing(backend=None) -> bool:
     return True
 
 
+_SCALAR_BYTES = {"f16": 2, "bf16": 2, "f32": 4, "f64": 8, "i8": 1, "u8": 1, "i16": 2, "i32": 4, "u32": 4, "i64": 8}
+
+
+def workgroup_layout(elem: str, n: int = 1) -> tuple:
+    """(size, alignment) in bytes of an n-component vector of `elem` in workgroup memory
+    (LDS), the rule Lava's emitter applies to `@localmem` (src/compiler/spirv/types.jl:
+    838-900, test/test_workgroup_vector_layout.jl:24-27): the components packed, aligned
+    to 2x the component for 2 components and 4x for 3 or 4 (Vulkan's rule); a scalar is
+    its own size.  The 2- and 4-component device types the kernels stage in LDS follow
+    it (static_asserts in lava_coopmat.hpp)."""
+    if elem not in _SCALAR_BYTES:
+        raise ValueError(f"unknown component type {elem!r}")
+    if n not in (1, 2, 3, 4):
+        raise ValueError("vectors have 2, 3 or 4 components")
+    b = _SCALAR_BYTES[elem]
+    if n == 1:
+        return b, b
+    return n * b, (2 if n == 2 else 4) * b
+
+
 _CAPS_FIELDS = ("coopmat", "tile", "subgroup", "coopmatsubgroup", "sharedbudget", "workgrouplimit", "cores",
                 "warps", "clock_khz", "hbm_bytes", "l2_bytes", "gfx_arch")
 

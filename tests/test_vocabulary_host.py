@@ -3,6 +3,8 @@ shape ordering, table queries, and the DeviceCaps copy rules.
 """
 from __future__ import annotations
 
+import pytest
+
 import lava_hip as lh
 from lava_hip import DeviceCaps, MatrixShape, SubgroupScope, WorkgroupScope
 
@@ -58,3 +60,17 @@ def test_gfx950_table_answers():
     assert lh.bestshape(table, "u8", "u32") is None   # CDNA4 has no unsigned MFMA
     assert lh.supports_coopmat_perelement() and lh.supports_coopmat_reduce()
     assert lh.CoopMatReduce.Row == 1 and lh.CoopMatReduce.RowAndColumn == 3
+
+
+def test_workgroup_layout_of_vectors():
+    """test_workgroup_vector_layout.jl:24-27: <2 x half> 4/4, <4 x half> 8/8, <2 x float> 8/8,
+    <4 x float> 16/16 -- and the rule's other cases (3 components packed, aligned as 4)."""
+    assert lh.workgroup_layout("f16", 2) == (4, 4)
+    assert lh.workgroup_layout("f16", 4) == (8, 8)
+    assert lh.workgroup_layout("f32", 2) == (8, 8)
+    assert lh.workgroup_layout("f32", 4) == (16, 16)
+    assert lh.workgroup_layout("f32", 3) == (12, 16)
+    assert lh.workgroup_layout("f16", 1) == (2, 2)
+    assert lh.workgroup_layout("i8", 4) == (4, 4)
+    with pytest.raises(ValueError):
+        lh.workgroup_layout("f32", 5)
