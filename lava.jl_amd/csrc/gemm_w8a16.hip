@@ -46,11 +46,14 @@ __device__ __forceinline__ uint32_t w8_pair(uint32_t lo_row, uint32_t hi_row, in
     return __builtin_amdgcn_perm(hi_row, lo_row, sel) ^ 0x64806480u;
 }
 
+// Wavefront gw = split * W8_WAVES + w takes the 32-row steps [gw ks, min((gw + 1) ks,
+// total_steps)) of K.  KSTEPS > 0: the host guarantees exactly KSTEPS each, fully
+// unrolled; KSTEPS == 0: any count (zero included), in unrolled groups of W8_DEPTH.
 template <int KSTEPS>
 __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
                                                     const f16* __restrict__ scale, float* __restrict__ Y,
                                                     float* __restrict__ partial, int M, int N, int64_t ldx,
-                                                    int64_t ldw, int64_t ldy, int splits) {
+                                                    int64_t ldw, int64_t ldy, int splits, int ks, int total_steps) {
     __shared__ __attribute__((aligned(16))) float red[W8_WAVES][16][W8_COLS];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -60,7 +63,9 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
     const int mb = blockIdx.z;             // 16-row block of X / Y
     const int n0 = cb * W8_COLS;
     const int m0 = mb * 16;
-    const int64_t k_wave = ((int64_t)split * W8_WAVES + w) * (KSTEPS * W8_KSTEP);
+    const int s_begin = (split * W8_WAVES + w) * ks;
+    const int ksteps = KSTEPS > 0 ? KSTEPS : max(0, min(ks, total_steps - s_begin));
+    const int64_t k_wave = (int64_t)s_begin * W8_KSTEP;
 
     // A operand rows: X[m0 + q][k .. k + 8) for this lane's group; rows >= M read as 0
     const bool xrow_ok = (m0 + q) < M;
@@ -75,7 +80,9 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
                         (f16)-1152.f, (f16)-1152.f, (f16)-1152.f, (f16)-1152.f};
     // Weight rows and X for W8_DEPTH steps are in flight ahead of the MFMAs (a ring in
     // registers): the stream is latency-bound otherwise, one HBM round trip per step.
-    constexpr int DEPTH = KSTEPS < W8_DEPTH ? KSTEPS : W8_DEPTH;
+    // With a runtime step count the steps run in groups of DEPTH, the ring slot a
+    // compile-time constant and the count bounding them through wave-uniform branches.
+    constexpr int DEPTH = KSTEPS > 0 && KSTEPS < W8_DEPTH ? KSTEPS : W8_DEPTH;
     u32x2 ring[DEPTH][8];
     uint4 xring[DEPTH];
     auto load_step = [&](int s, u32x2* rows, uint4& xa) {
@@ -85,15 +92,13 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
         xa = make_uint4(0, 0, 0, 0);
         if (xrow_ok) xa = *reinterpret_cast<const uint4*>(xp + s * W8_KSTEP);
     };
-#pragma unroll
-    for (int s = 0; s < DEPTH; ++s) load_step(s, ring[s], xring[s]);
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
+    // step s from ring slot u (a compile-time constant at every call), refilling it with step s + DEPTH
+    auto step = [&](int u, int s) {
         u32x2 rows[8];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) rows[r] = ring[s % DEPTH][r];
-        const f16x8 a = __builtin_bit_cast(f16x8, xring[s % DEPTH]);
-        if (s + DEPTH < KSTEPS) load_step(s + DEPTH, ring[s % DEPTH], xring[s % DEPTH]);
+        for (int r = 0; r < 8; ++r) rows[r] = ring[u][r];
+        const f16x8 a = __builtin_bit_cast(f16x8, xring[u]);
+        if (s + DEPTH < ksteps) load_step(s + DEPTH, ring[u], xring[u]);
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
             const int byte = t & 3;
@@ -112,6 +117,18 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
             const f16x8 b = __builtin_bit_cast(f16x8, bw) + bias;   // exact: w = (1152 + w) - 1152
             acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[t], 0, 0, 0);
         }
+    };
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s)
+        if (s < ksteps) load_step(s, ring[s], xring[s]);
+    if constexpr (KSTEPS > 0) {
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) step(s % DEPTH, s);
+    } else {
+        for (int s0 = 0; s0 < ksteps; s0 += DEPTH)
+#pragma unroll
+            for (int u = 0; u < DEPTH; ++u)
+                if (s0 + u < ksteps) step(u, s0 + u);
     }
     // acc[t] lane holds column 8q + t and rows 4g + j of this wave's partial
 #pragma unroll
@@ -228,20 +245,22 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
     if (rc != LAVA_HIP_OK) return rc;
     hipStream_t s = as_stream(stream);
 
-    // fast path: all row-major, N in 128-column blocks, K in 128-row wavefront slices
-    const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % (W8_WAVES * W8_KSTEP) == 0 &&
+    // fast path: all row-major, N in 128-column blocks, K in 32-row steps
+    const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 && K / W8_KSTEP <= 0x7fffffff &&
                       ldw % 8 == 0 && ldx % 8 == 0 && aligned(W, 8) && aligned(X, 16) && N <= 0x7fffffff &&
                       M <= 0x7fffffff;
     if (fast) {
-        // split K (at most 4 ways: the partial blocks cost 8 * splits bytes per output
-        // element of extra traffic) until the grid covers the 256 CUs
+        // split K (up to 16 ways; the partial blocks cost 8 * splits bytes per output
+        // element of extra traffic) until the grid covers the 256 CUs, keeping >= 4 steps
+        // per wavefront
         const int64_t cblocks = N / W8_COLS, mblocks = (M + 15) / 16;
-        const int64_t kwave_steps = K / (W8_WAVES * W8_KSTEP);   // steps per wave at 1 split
+        const int64_t total_steps = K / W8_KSTEP;
         int splits = 1;
-        while (splits < 4 && cblocks * mblocks * splits < 256 && kwave_steps % (2 * splits) == 0 &&
-               kwave_steps / (2 * splits) >= 2)
+        while (splits < 16 && cblocks * mblocks * splits < 256 && total_steps / (W8_WAVES * splits * 2) >= 4)
             splits *= 2;
-        const int64_t ksteps = kwave_steps / splits;
+        const int64_t ks = (total_steps + W8_WAVES * splits - 1) / (W8_WAVES * splits);
+        const bool even = ks * W8_WAVES * splits == total_steps;
+        const int64_t ksteps = even ? ks : 0;   // the unrolled instances need equal shares
         LAVA_REQUIRE(mblocks <= 65535 && cblocks <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: grid too large");
         float* partial = nullptr;
         if (splits > 1) {
@@ -249,17 +268,18 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
             if (rc != LAVA_HIP_OK) return rc;
         }
         const dim3 grid((unsigned)cblocks, (unsigned)splits, (unsigned)mblocks);
-#define LAVA_W8_LAUNCH(KS)                                                                                           \
-    hipLaunchKernelGGL(w8a16_kernel<KS>, grid, dim3(256), 0, s, (const f16*)X, (const int8_t*)W, (const f16*)scale, \
-                       (float*)Y, partial, (int)M, (int)N, ldx, ldw, ldy, splits)
-        switch (ksteps) {
+#define LAVA_W8_LAUNCH(KS)                                                                                        \
+    hipLaunchKernelGGL(w8a16_kernel<KS>, grid, dim3(256), 0, s, (const f16*)X, (const int8_t*)W,                \
+                       (const f16*)scale, (float*)Y, partial, (int)M, (int)N, ldx, ldw, ldy, splits, (int)ks,     \
+                       (int)total_steps)
+        switch (ksteps) {   // the usual counts fully unrolled, any other in groups of W8_DEPTH
         case 1: LAVA_W8_LAUNCH(1); break;
         case 2: LAVA_W8_LAUNCH(2); break;
         case 4: LAVA_W8_LAUNCH(4); break;
         case 8: LAVA_W8_LAUNCH(8); break;
         case 16: LAVA_W8_LAUNCH(16); break;
         case 32: LAVA_W8_LAUNCH(32); break;
-        default: goto generic;
+        default: LAVA_W8_LAUNCH(0); break;
         }
 #undef LAVA_W8_LAUNCH
         LAVA_LAUNCH_CHECK("w8a16_kernel");
@@ -273,7 +293,7 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
         }
         return LAVA_HIP_OK;
     }
-generic : {
+{   // any layout, any shape
     const int64_t total = M * N;
     LAVA_REQUIRE((total + 255) / 256 <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: problem too large");
     hipLaunchKernelGGL(w8a16_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (const f16*)X,

@@ -26,7 +26,12 @@ def w8_inputs(lh, M, N, K, seed_cfg=3, order="C"):
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 14336, 4096), (16, 1024, 512), (5, 256, 128), (32, 384, 1024),
-                                   (16, 200, 96), (3, 7, 5)])
+                                   (16, 200, 96), (3, 7, 5),
+                                   # step counts that are not powers of two: 86 and 112 steps of 32
+                                   # per wavefront before the split (decode shapes of common models), 3
+                                   (16, 4096, 11008), (16, 4096, 14336), (1, 1024, 384), (48, 256, 1408),
+                                   # K a multiple of 32 only: unequal per-wavefront shares, some empty
+                                   (16, 256, 96), (7, 384, 1120), (16, 128, 32)])
 def test_w8a16(gpu, oracle, M, N, K):
     lh = gpu
     announce(f"w8a16 M={M} N={N} K={K}")
@@ -37,7 +42,7 @@ def test_w8a16(gpu, oracle, M, N, K):
     ref = oracle.w8a16_rows(X.to_numpy(), W.to_numpy(), s.to_numpy(), N, K, K, N, np.arange(M))
     err = oracle.rel_frobenius(Y.to_numpy(), ref)
     assert err <= 1e-3, err
-    # repeat: the split-K tickets return to zero, so a second call is identical
+    # repeat: the split-K partials are summed in a fixed order, so a second call is identical
     Y2 = lh.HIPDeviceArray("f32", (M, N), order="C")
     lh.w8a16(Y2, X, W, s)
     np.testing.assert_array_equal(Y.to_numpy(), Y2.to_numpy())
