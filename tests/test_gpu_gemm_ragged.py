@@ -179,3 +179,32 @@ def test_tile_kernel_layouts_epilogue(gpu, oracle, layout):
     got = oracle.bf16_bits_to_f32(D.to_numpy()).astype(np.float64)
     err = oracle.rel_frobenius(got, ref)
     assert err <= TOL, err
+
+
+@pytest.mark.parametrize("layout", range(8))
+def test_tile_kernel_padded_leading_dims(gpu, oracle, layout):
+    """Leading dimensions larger than the extents (every operand padded by 8 elements,
+    C by 4): the tile kernel's operand forms address through lda / ldb / ldc, and the
+    padding of C is not written."""
+    lh = gpu
+    M, N, K = 520, 776, 264
+    announce(f"tile kernel padded lds layout={layout}")
+    arow, brow, crow = layout & 1, layout & 2, layout & 4
+    lda = (K if arow else M) + 8
+    ldb = (N if brow else K) + 8
+    ldc = (N if crow else M) + 4
+    A = lh.HIPDeviceArray("bf16", ((M if arow else K) * lda,))
+    B = lh.HIPDeviceArray("bf16", ((K if brow else N) * ldb,))
+    Cb = lh.HIPDeviceArray("f32", ((M if crow else N) * ldc,))
+    lh.fill_uniform(A, 9700 + layout, -1.0, 1.0)
+    lh.fill_uniform(B, 9800 + layout, -1.0, 1.0)
+    Cb.fill_bytes(0x5A)
+    lh.gemm_raw("bf16", "f32", A.ptr, B.ptr, Cb.ptr, M, N, K, lda, ldb, ldc, layout)
+    rows = sample_rows(M, np.random.default_rng(layout + 77))
+    ref = oracle.gemm_rows(A.to_numpy(), "bf16", B.to_numpy(), "bf16", M, N, K, lda, ldb, layout & 3, rows)
+    c = Cb.to_numpy()
+    cm = c.reshape(M, ldc) if crow else c.reshape(N, ldc).T
+    err = oracle.rel_frobenius(cm[rows, :N] if crow else cm[:M][rows], ref)
+    assert err <= TOL, err
+    pad = cm[:, N:] if crow else cm[M:, :]
+    assert np.all(pad.view(np.uint32) == 0x5A5A5A5A), "padding of C written"

@@ -180,3 +180,34 @@ def test_flash_full_config(gpu, oracle):
     v = V.to_numpy()
     assert not np.isnan(o).any()
     np.testing.assert_array_equal(o[:, 0, :, :], v[:, 0, :, :])
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("E,L", [(128, 300), (64, 512)])
+def test_flash_strided_layouts(gpu, oracle, causal, E, L):
+    """Q, K, V in (B, L, H, D) memory order (strides 1, D*H, D, D*H*L) and O with padded rows
+    (row stride D + 8): the fast kernel addresses every tensor through its strides."""
+    lh = gpu
+    H, B = 3, 2
+    announce(f"flash strided D={E} S={L} causal={causal}")
+    st = (1, E * H, E, E * H * L)
+    ost = (1, E + 8, (E + 8) * L, (E + 8) * L * H)
+    n = E * H * L * B
+    bufs = []
+    for t in range(3):
+        a = lh.HIPDeviceArray("f16", (n,))
+        lh.fill_normal(a, lh_mod.seed(7, t))
+        bufs.append(a)
+    O = lh.HIPDeviceArray("f16", ((E + 8) * L * H * B,))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd_raw(bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, O.ptr, B, H, L, E, st, ost, None, causal)
+    q, k, v = (a.to_numpy() for a in bufs)
+    o = O.to_numpy()
+    rows = np.arange(L)
+    for (b, h) in [(0, 0), (1, 2), (0, 1)]:
+        ref = oracle.attn_rows(q, k, v, L, E, st, 1 / math.sqrt(E), causal, b, h, rows)
+        idx = (np.arange(E)[None, :] * ost[0] + rows[:, None] * ost[1] + h * ost[2] + b * ost[3])
+        got = o[idx].astype(np.float64)
+        assert oracle.rel_frobenius(got, ref) <= 2e-3, (b, h)
+        pad = o[(np.arange(8)[None, :] + E) + rows[:, None] * ost[1] + h * ost[2] + b * ost[3]]
+        assert np.all(pad.view(np.uint16) == 0xFFFF), "row padding of O written"
