@@ -270,6 +270,11 @@ __global__ void __launch_bounds__(256, 1)
             f.a[t] = sa.read(base, s, t);
         }
     };
+    // the r-th (0..7) of those reads, in the same order: b[0], a[0], b[1], a[1], ...
+    auto read_one = [&](Frags& f, const uint8_t* base, int s, int r) {
+        if (r & 1) f.a[r >> 1] = sa.read(base, s, r >> 1);
+        else f.b[r >> 1] = sb.read(base + TN_SLICE, s, r >> 1);
+    };
     // MFMA A operand = B slice (rows are columns n of C), B operand = A slice (rows m):
     // the accumulator then holds C^T, 4 consecutive n per lane and register group.
     auto mma = [&](const Frags& f, int i0, int i1) {
@@ -280,10 +285,13 @@ __global__ void __launch_bounds__(256, 1)
     };
 
     // Per k-tile (128 bytes of K = 4 sub-steps), branch-free so the interleave holds:
-    //   s = 0..2: 16 MFMAs on the current fragments while the next sub-step's 8 LDS
-    //             reads (and, at s = 0 and 1, 8 DMA loads of the next tile each) issue;
-    //   s = 3:    8 MFMAs; wait for this wave's DMA; barrier; then the next tile's
-    //             s = 0 reads under the last 8 MFMAs.
+    //   s = 0, 1: 16 MFMAs on the current fragments; after each, alternately one of the
+    //             next sub-step's 8 LDS reads and one of 8 DMA loads of the next tile
+    //             (reads issued in one burst fill the LDS command queue and stall the
+    //             wave's MFMA issue behind them);
+    //   s = 2:    16 MFMAs with the next sub-step's reads interleaved;
+    //   s = 3:    12 MFMAs (8 when an operand is M/N-contiguous); wait for this wave's
+    //             DMA; barrier; then the next tile's s = 0 reads under the last 4 (8).
     // On the last tile the "next" tile re-fetches the current one into the idle stage.
     {
 #pragma unroll
@@ -292,32 +300,40 @@ __global__ void __launch_bounds__(256, 1)
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     Frags fa, fb;
-    read_frags(fa, smem, 0);
+    // The same read order as the loop's last sub-step, one at a time: then the loop head
+    // waits only for the reads its first MFMA needs (lgkmcnt counts in issue order; with
+    // another order here the compiler must wait for all of them on every iteration).
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+        read_one(fa, smem, 0, r);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // MFMAs before the barrier in s = 3 (the rest hide the next tile's first reads)
+    constexpr int S3_PRE = NR == 8 ? 3 : 2;
 
     for (int kt = 0; kt < ktiles; ++kt) {
         const int st = kt & 1;
         const uint8_t* base = smem + st * 2 * TN_SLICE;
         const uint8_t* next = smem + (st ^ 1) * 2 * TN_SLICE;
         const uint32_t kofs_next = (uint32_t)(kt + 1 < ktiles ? kt + 1 : kt) * TN_KB;
-        // s = 0: LDS reads of s = 1, then 16 MFMAs with one DMA load of the next tile after each
-        read_frags(fb, base, 1);
+        // s = 0: 16 MFMAs; s = 1's reads and the first 8 DMA loads alternate between them
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 acc[i][j] = Mfma32<T>::run(fa.b[j], fa.a[i], acc[i][j]);
                 if (j & 1) dma(2 * i + (j >> 1), st ^ 1, kofs_next);
+                else read_one(fb, base, 1, 2 * i + (j >> 1));
                 __builtin_amdgcn_sched_barrier(0);
             }
-        // s = 1: the other 8 DMA loads (one per two MFMAs) and s = 2's LDS reads under 16 MFMAs
-        read_frags(fa, base, 2);
-        __builtin_amdgcn_sched_barrier(0);
+        // s = 1: the same with s = 2's reads and the other 8 DMA loads
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 acc[i][j] = Mfma32<T>::run(fb.b[j], fb.a[i], acc[i][j]);
                 if (j & 1) dma(8 + 2 * i + (j >> 1), st ^ 1, kofs_next);
+                else read_one(fa, base, 2, 2 * i + (j >> 1));
                 __builtin_amdgcn_sched_barrier(0);
             }
         read_frags(fb, base, 3);
@@ -343,18 +359,18 @@ __global__ void __launch_bounds__(256, 1)
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        // s = 3: half the MFMAs, publish the next stage, its first reads under the other half
-        mma(fb, 0, 2);
+        // s = 3: most MFMAs, publish the next stage, its first reads under the rest
+        mma(fb, 0, S3_PRE);
         __builtin_amdgcn_sched_barrier(0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's part of the next tile landed
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
         read_frags(fa, next, 0);
-        mma(fb, 2, 4);
+        mma(fb, S3_PRE, 4);
         if constexpr (NR == 8) {
 #pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 3);
+            for (int t = 0; t < 4; ++t) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 3);
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 3);
             }
         } else if constexpr (NR == 12) {
