@@ -251,12 +251,14 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
                       M <= 0x7fffffff;
     if (fast) {
         // split K (up to 16 ways; the partial blocks cost 8 * splits bytes per output
-        // element of extra traffic) until the grid covers the 256 CUs, keeping >= 4 steps
-        // per wavefront
+        // element of extra traffic) while the grid still fits the 256 CUs in one round,
+        // keeping >= 4 steps per wavefront: at 16 x 4096 . 4096 x 14336 the 224-workgroup
+        // grid (2 splits) streams ~6 % faster than the 448-workgroup one (4 splits), and
+        // 1 split (112) or 8 (896) are 20 % slower
         const int64_t cblocks = N / W8_COLS, mblocks = (M + 15) / 16;
         const int64_t total_steps = K / W8_KSTEP;
         int splits = 1;
-        while (splits < 16 && cblocks * mblocks * splits < 256 && total_steps / (W8_WAVES * splits * 2) >= 4)
+        while (splits < 16 && cblocks * mblocks * splits * 2 <= 256 && total_steps / (W8_WAVES * splits * 2) >= 4)
             splits *= 2;
         const int64_t ks = (total_steps + W8_WAVES * splits - 1) / (W8_WAVES * splits);
         const bool even = ks * W8_WAVES * splits == total_steps;
