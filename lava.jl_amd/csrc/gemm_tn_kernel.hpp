@@ -1,4 +1,6 @@
-// gemm_tn_kernel.hpp -- the compute-bound GEMM kernel, C row-major, every operand layout.
+// gemm_tn_kernel.hpp -- the compute-bound GEMM kernels, C row-major, every operand layout:
+// gemm_tn16_kernel (16x16 MFMAs) when both operands are K-contiguous, gemm_tn_kernel
+// (32x32 MFMAs) when one is M/N-contiguous.
 //
 // This is the staged cooperative-matrix GEMM (src/device/coopmat_intrinsics.jl:
 // 104-148 stages A and B through workgroup memory and reads A RowMajor and B
@@ -6,8 +8,8 @@
 // same loop at workgroup scope) laid out for CDNA4:
 //
 //  * one 256 x 256 tile of C per workgroup of 4 wavefronts (one per SIMD), each
-//    wavefront owning a 128 x 128 sub-tile = 4 x 4 MFMA 32x32 accumulators
-//    (256 fp32 registers per lane, all in AGPRs);
+//    wavefront owning a 128 x 128 sub-tile = 4 x 4 MFMA 32x32 accumulators, or 8 x 8
+//    16x16 ones (256 fp32 registers per lane, all in AGPRs);
 //  * K advances 128 bytes at a time (64 bf16/fp16 or 128 int8): A and B slices of
 //    32 KB each, double-buffered in LDS (2 x 64 KB);
 //  * global -> LDS with buffer_load_dwordx4 ... lds: each lane moves 16 bytes
@@ -17,10 +19,12 @@
 //  * each operand is staged in one of two forms, chosen by its layout (AK / BK):
 //    - K-contiguous (A row-major, B column-major): 256 rows x 128 bytes of K; an
 //      instruction covers 8 rows, lane l row l / 8 and slot l % 8.  The slot a
-//      logical 16-byte chunk c of row r lands in is c ^ swz(r), swz(r) =
-//      (r & 7) ^ ((r >> 3) & 1), chosen by which global chunk each lane fetches, so
-//      the fragment reads (16 consecutive rows, one chunk column) spread over all
-//      banks; a fragment is one ds_read_b128 per lane;
+//      logical 16-byte chunk c of row r lands in is c ^ swz(r), chosen by which
+//      global chunk each lane fetches, so that the fragment reads (consecutive rows,
+//      one chunk column) spread over all banks: swz(r) = (r & 7) ^ ((r >> 3) & 1) for
+//      the 32x32 reads (32 rows per 32 lanes), swz(r) = r & 7 for the 16x16 ones (16
+//      rows per 16 lanes; measured with SQ_LDS_BANK_CONFLICT, the row / 8 flip costs
+//      them 4 conflict cycles per read); a fragment is one ds_read_b128 per lane;
 //    - M/N-contiguous (A column-major, B row-major; 16-bit types): 64 rows of K x
 //      512 bytes (256 m or n); an instruction covers 2 rows, lane l row l / 32 and
 //      slot l % 32, which holds logical chunk slot ^ F(row % 4), F = {0, 6, 10, 12};
@@ -30,12 +34,14 @@
 //      receives the 4 k values of column i.  F makes the 4 rows x 2 chunks of one
 //      16-lane group, and the 4 rows x 4 chunks of a 32-lane pair, distinct modulo
 //      the bank period;
-//  * fragments are 16 bytes per lane, one MFMA 32x32x16 (16-bit) or 32x32x32 (int8)
-//    each; 4 sub-steps of 32 bytes of K per stage, each 16 MFMAs, with the next
+//  * 32x32 kernel: fragments are 16 bytes per lane, one MFMA 32x32x16 (16-bit) or
+//    32x32x32 (int8) each; 4 sub-steps of 32 bytes of K per stage, each 16 MFMAs, with the next
 //    sub-step's fragments read underneath (double-buffered fragment registers) and
 //    the next stage's 16 DMA loads issued one per two MFMAs over sub-steps 0 and 1
 //    (a wavefront's vector-memory issue takes ~40-70 cycles per 1 KB instruction;
 //    one per MFMA would stall the MFMA stream);
+//  * 16x16 kernel: two k-steps of 64 bytes per stage, 64 MFMAs each; the barrier in
+//    the middle of the stage (see gemm_tn16_kernel);
 //  * the MFMA's A operand is the B slice and its B operand the A slice, so each
 //    lane's accumulator holds runs of 4 consecutive columns of one row of C; the
 //    epilogue stages them through LDS and stores whole 512-byte row runs;
@@ -119,12 +125,13 @@ struct TnSide<T, true> {
     int rd, swz, h;
 
     // rows_in: rows of this tile inside the matrix; wx: the wavefront's 128-row half.
+    // Row r's 16-byte chunk c is stored at c ^ (r % 8) ^ (flip ? r / 8 % 2 : 0).
     __device__ __forceinline__ void init(const T* X, int64_t ld_b, int tile, int rows_in, int64_t, int, int w, int wx,
-                                         int lane) {
+                                         int lane, int flip = 1) {
         rs = make_rsrc(reinterpret_cast<const char*>(X) + (int64_t)tile * TN_TILE * ld_b,
                        (uint32_t)(rows_in * ld_b));
         const int lr = lane >> 3;
-        const int c_even = (lane & 7) ^ lr, c_odd = c_even ^ 1;
+        const int c_even = (lane & 7) ^ lr, c_odd = c_even ^ flip;
         const uint32_t row = (uint32_t)((64 * w + lr) * ld_b);
         off[0] = row + 16u * c_even;
         off[1] = row + 16u * c_odd;
@@ -507,6 +514,255 @@ __global__ void __launch_bounds__(256, 1)
     quarter(std::integral_constant<int, 3>{});
 }
 
+// Both operands K-contiguous (A row-major, B column-major: the bf16 configuration and
+// every int8 product): the same 256 x 256 tile, LDS stages and epilogue as
+// gemm_tn_kernel, on 16x16 MFMAs (16x16x32 for 16-bit types, 16x16x64 for int8) --
+// 8 x 8 accumulators of 16 x 16 per wavefront.  At the chip's power limit the 16x16 shape
+// sustains ~11 % more than 32x32 (it moves ~20 % fewer register-file bytes per flop),
+// and its fragments (16 rows x 64 bytes of K per k-step) let the whole stage be read by
+// the middle of the k-tile, so that the barrier sits there and each DMA gets a full
+// k-tile to land.
+template <typename T, typename OutT, bool EPI, bool RAGGED>
+__global__ void __launch_bounds__(256, 1)
+    gemm_tn16_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
+                     int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi, TnBounds bnd) {
+    using AccV = typename Mfma16<T>::acc_t;
+    typedef typename Mfma16<T>::acc_elem Acc;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TN_SLICE];  // [stage][A,B][32 KB]
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    int tm, tn;
+    xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
+    const int wm = w >> 1, wn = w & 1;
+    const int h = lane >> 5;
+
+    // Rows (m, n) of this tile inside the matrix: all 256 unless RAGGED and the tile is the last.
+    int a_rows = TN_TILE, b_rows = TN_TILE;
+    if constexpr (RAGGED) {
+        a_rows = (int)(bnd.m - (int64_t)tm * TN_TILE < TN_TILE ? bnd.m - (int64_t)tm * TN_TILE : TN_TILE);
+        b_rows = (int)(bnd.n - (int64_t)tn * TN_TILE < TN_TILE ? bnd.n - (int64_t)tn * TN_TILE : TN_TILE);
+    }
+    const int kelems = bnd.kb / (int)sizeof(T);
+    TnSide<T, true> sa;
+    TnSide<T, true> sb;
+    // the chunk swizzle without the row / 8 flip: the 16x16 fragment read (16 rows x one
+    // chunk per 16 lanes) is bank-conflict-free with it, not with the flip
+    sa.init(A, lda_b, tm, a_rows, bnd.m, kelems, w, wm, lane, 0);
+    sb.init(B, ldb_b, tn, b_rows, bnd.n, kelems, w, wn, lane, 0);
+    // wave w fills 8 KB of each slice: K-contiguous rows [64 w, 64 w + 64), M/N-contiguous
+    // k rows [16 w, 16 w + 16); instruction i 1 KB of it
+    const uint32_t lds0 = lds_addr(smem) + w * 64 * TN_KB;
+
+    // DMA load q (0..15) of a k-tile into `stage`: q < 8 are A, q >= 8 B.
+    auto dma = [&](int q, int stage, uint32_t kofs) {
+        const int i = q & 7;
+        const uint32_t dst = lds0 + stage * 2 * TN_SLICE + (q >> 3) * TN_SLICE + i * 1024;
+        if (q < 8) {
+            uint32_t off = sa.voff(i);
+            if constexpr (RAGGED) off = sa.valid(i, kofs, bnd.kb) ? off : OOB_OFS;
+            dma16(sa.rs, off, sa.soff(i, kofs), dst);
+        } else {
+            uint32_t off = sb.voff(i);
+            if constexpr (RAGGED) off = sb.valid(i, kofs, bnd.kb) ? off : OOB_OFS;
+            dma16(sb.rs, off, sb.soff(i, kofs), dst);
+        }
+    };
+
+    AccV acc[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[i][j][r] = 0;
+
+    // ---- fragments: 16x16 MFMA operands, 16 bytes per lane: row lane % 16 of a 16-row
+    // block, 16-byte chunk 4 u + lane / 16 of k-step u (the 64-byte half u of the stage's
+    // 128 bytes of K).  a[i]: rows 16 i of the wave's 128 m; b[j]: rows 16 j of its 128 n.
+    struct F16 {
+        uint4 a[8], b[8];
+    };
+    const int g16 = lane >> 4;
+    const int swz16 = lane & 7;   // the stage's chunk swizzle of row 8 k + lane % 8 (no flip)
+    const int rda = (wm * 128 + (lane & 15)) * TN_KB, rdb = (wn * 128 + (lane & 15)) * TN_KB;
+    // fragment t (0..15) of k-step u, in the order the MFMAs (i-major) first use them:
+    // a[0], b[0..7], a[1..7]
+    auto rd16 = [&](F16& f, const uint8_t* stage, int u, int t) {
+        const int slot = ((4 * u + g16) ^ swz16) * 16;
+        const bool isa = t == 0 || t > 8;
+        const int blk = t == 0 ? 0 : (t <= 8 ? t - 1 : t - 8);
+        if (isa) f.a[blk] = *reinterpret_cast<const uint4*>(stage + rda + blk * 16 * TN_KB + slot);
+        else f.b[blk] = *reinterpret_cast<const uint4*>(stage + TN_SLICE + rdb + blk * 16 * TN_KB + slot);
+    };
+    // MFMA A operand = B fragment (rows are columns n of C), B operand = A fragment (rows
+    // m): acc[i][j] register r of lane l is C[m][n], m = 128 wm + 16 i + l % 16,
+    // n = 128 wn + 16 j + 4 (l / 16) + r.
+
+    // Per k-tile kt (stage kt % 2), one barrier, at the middle:
+    //   first half:  64 MFMAs of k-step 0 (fragments read during the previous tile); the
+    //                16 fragment reads of k-step 1 from this stage, one per 4 MFMAs;
+    //   middle:      this wave's DMAs of tile kt + 1 (issued during the previous tile's
+    //                second half) landed; barrier: tile kt + 1 published, and every read
+    //                of this stage done;
+    //   second half: 64 MFMAs of k-step 1; tile kt + 1's k-step 0 reads from the other
+    //                stage and the DMAs of tile kt + 2 into this one, each one per 4 MFMAs.
+    // A DMA thus has about a whole k-tile to land.  Past the last tile the DMAs re-fetch
+    // the last one into the idle stage.
+#pragma unroll
+    for (int q = 0; q < 16; ++q) dma(q, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) dma(q, 1, ktiles > 1 ? (uint32_t)TN_KB : 0u);
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");   // tile 0 (the first 16 of this wave's loads)
+    __syncthreads();
+    F16 fa, fb;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+        rd16(fa, smem, 0, t);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    for (int kt = 0; kt < ktiles; ++kt) {
+        const int st = kt & 1;
+        const uint8_t* base = smem + st * 2 * TN_SLICE;
+        const uint8_t* next = smem + (st ^ 1) * 2 * TN_SLICE;
+        const uint32_t kofs2 = (uint32_t)(kt + 2 < ktiles ? kt + 2 : ktiles - 1) * TN_KB;
+#pragma unroll
+        for (int q = 0; q < 64; ++q) {
+            acc[q >> 3][q & 7] = Mfma16<T>::run(fa.b[q & 7], fa.a[q >> 3], acc[q >> 3][q & 7]);
+            if ((q & 3) == 3) rd16(fb, base, 1, q >> 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's part of tile kt + 1 landed
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 64; ++q) {
+            acc[q >> 3][q & 7] = Mfma16<T>::run(fb.b[q & 7], fb.a[q >> 3], acc[q >> 3][q & 7]);
+            if ((q & 3) == 1) rd16(fa, next, 0, q >> 2);
+            if ((q & 3) == 3) dma(q >> 2, st, kofs2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // ---- epilogue through LDS, so that global stores are whole 512-byte row runs.
+    // acc[i][j] register r of lane l is C[m][n] with m = 128 wm + 32 i + l % 32 and
+    // n = 128 wn + 32 j + 8 (r / 4) + 4 (l / 32) + r % 4 within the tile.  Each wave
+    // stages 32 rows x 128 columns at a time (one i) in its own 16.5 KB of the idle
+    // stage buffers (4 waves: 66 KB of the 128 KB), rows padded to 528 bytes so the
+    // 32 rows of one column group land on distinct banks; then reads whole rows back:
+    // lanes 0..31 and 32..63 each cover one 512-byte row per instruction.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    constexpr int EP_PITCH = 128 * 4 + 16;
+    const int rr = lane & 31;
+    uint8_t* ep = smem + w * (32 * EP_PITCH);
+    typedef Acc Acc4 __attribute__((ext_vector_type(4)));
+    const int64_t row0 = (int64_t)tm * TN_TILE + wm * 128, col0 = (int64_t)tn * TN_TILE + wn * 128;
+    OutT* cbase = C + row0 * ldc + col0;
+    // columns of this lane's 4-column group inside the matrix (RAGGED: 0..4)
+    int cols_in = 4;
+    if constexpr (RAGGED) {
+        const int64_t left = bnd.n - (col0 + 4 * rr);
+        cols_in = left >= 4 ? 4 : (left > 0 ? (int)left : 0);
+    }
+    // one row quarter i at a time; i is a template constant so that acc stays in registers
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    auto quarter = [&](auto itag) {
+        constexpr int i = decltype(itag)::value;
+        // The epilogue's init terms for the 16 rows x 4 columns this lane finishes, all
+        // requested before the staging so that their HBM latency overlaps it (loaded one
+        // row at a time inside the store loop they cost one round trip per row).
+        F4 rin[EPI ? 16 : 1];
+        float bin[EPI ? 16 : 1];
+        F4 bcol = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (EPI) {
+            const int64_t n = col0 + 4 * rr;
+            // 4 floats at p, or those of them inside the matrix (columns < N)
+            auto ld4 = [&](const float* p) {
+                if (epi.vec4 && cols_in == 4) return *reinterpret_cast<const F4*>(p);
+                F4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k < cols_in) r[k] = p[k];
+                return r;
+            };
+            if (epi.bias && epi.bias_on_cols) bcol = ld4(epi.bias + n);
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int64_t m = row0 + 32 * i + 2 * t + h;
+                rin[t] = F4{0.f, 0.f, 0.f, 0.f};
+                bin[t] = 0.f;
+                if (RAGGED && m >= bnd.m) continue;
+                if (epi.residual) rin[t] = ld4(epi.residual + m * epi.ldr + n);
+                if (epi.bias && !epi.bias_on_cols) bin[t] = epi.bias[m];
+            }
+        }
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const Acc4 v = {acc[2 * i + ii][j][0], acc[2 * i + ii][j][1], acc[2 * i + ii][j][2], acc[2 * i + ii][j][3]};
+                *reinterpret_cast<Acc4*>(ep + (16 * ii + (lane & 15)) * EP_PITCH + (16 * j + 4 * (lane >> 4)) * 4) = v;
+            }
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's staged rows are in LDS
+        __builtin_amdgcn_wave_barrier();
+        auto store_rows = [&](auto acttag) {
+            constexpr int ACT = decltype(acttag)::value;
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int row = 2 * t + h;                       // 0..31 of this i
+                const Acc4 v = *reinterpret_cast<const Acc4*>(ep + row * EP_PITCH + rr * 16);
+                OutT* dst = cbase + (int64_t)(32 * i + row) * ldc + 4 * rr;
+                if (RAGGED && row0 + 32 * i + row >= bnd.m) continue;
+                if constexpr (!EPI && std::is_same<OutT, Acc>::value) {
+                    if (!RAGGED || (cols_in == 4 && bnd.cvec)) {
+                        *reinterpret_cast<Acc4*>(dst) = v;
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (k < cols_in) dst[k] = v[k];
+                    }
+                } else {
+                    // the fused epilogue on 4 consecutive columns of one row, narrowed (RNE) to D's type
+                    typedef OutT Out4 __attribute__((ext_vector_type(4)));
+                    Out4 o;
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        float x = (float)v[k];
+                        // the same fp32 sums as epi_apply: (bias + residual), then acc + that
+                        if constexpr (EPI) x = epi_act_c<ACT>(x + ((bin[t] + bcol[k]) + rin[t][k]));
+                        o[k] = narrow<OutT>(x);
+                    }
+                    if (!RAGGED || (cols_in == 4 && bnd.cvec)) {
+                        *reinterpret_cast<Out4*>(dst) = o;
+                    } else {
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            if (k < cols_in) dst[k] = o[k];
+                    }
+                }
+            }
+        };
+        if constexpr (EPI) {
+            switch (epi.act) {   // uniform: one branch per quarter, none per element
+            case EPI_RELU: store_rows(std::integral_constant<int, EPI_RELU>{}); break;
+            case EPI_GELU_TANH: store_rows(std::integral_constant<int, EPI_GELU_TANH>{}); break;
+            case EPI_GELU_ERF: store_rows(std::integral_constant<int, EPI_GELU_ERF>{}); break;
+            default: store_rows(std::integral_constant<int, EPI_NONE>{}); break;
+            }
+        } else {
+            store_rows(std::integral_constant<int, EPI_NONE>{});
+        }
+        __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next i overwrites
+        __builtin_amdgcn_wave_barrier();
+    };
+    quarter(std::integral_constant<int, 0>{});
+    quarter(std::integral_constant<int, 1>{});
+    quarter(std::integral_constant<int, 2>{});
+    quarter(std::integral_constant<int, 3>{});
+}
+
 
 // Which kernel applies (see TnFit): the operand forms AK (A K-contiguous, i.e. row-major)
 // and BK (B K-contiguous, i.e. column-major).
@@ -544,7 +800,14 @@ int launch_gemm_tn_layout(const T* A, const T* B, OutT* C, int64_t M, int64_t N,
     bnd.kb = (int)(K * (int64_t)sizeof(T));
     bnd.cvec = ldc % 4 == 0 && aligned(C, 4 * sizeof(OutT));
     const int64_t lda_b = lda * (int64_t)sizeof(T), ldb_b = ldb * (int64_t)sizeof(T);
-    if (ragged)
+    if constexpr (AK && BK) {
+        if (ragged)
+            hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
+                               0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
+        else
+            hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, false>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
+                               0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
+    } else if (ragged)
         hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI, true, AK, BK>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
                            0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
     else
