@@ -45,40 +45,6 @@ struct Mfma16<int8_t> {
     }
 };
 
-// One 32x32 MFMA step with 16-byte-per-lane operands: 8 x fp16 / 8 x bf16
-// (32x32x16) or 16 x int8 (32x32x32).  Operand lane l holds row (or column) l % 32
-// and k-slots 8 (l / 32) + [0, 8) (16-bit) or 16 (l / 32) + [0, 16) (int8); the
-// accumulator lane holds column l % 32, rows 8 (j / 4) + 4 (l / 32) + j % 4.
-template <typename T>
-struct Mfma32;
-
-template <>
-struct Mfma32<f16> {
-    typedef f32x16 acc_t;
-    __device__ static acc_t run(uint4 a, uint4 b, acc_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
-                                                      0, 0);
-    }
-};
-
-template <>
-struct Mfma32<bf16> {
-    typedef f32x16 acc_t;
-    __device__ static acc_t run(uint4 a, uint4 b, acc_t c) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
-                                                       0, 0, 0);
-    }
-};
-
-template <>
-struct Mfma32<int8_t> {
-    typedef i32x16 acc_t;
-    __device__ static acc_t run(uint4 a, uint4 b, acc_t c) {
-        return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), __builtin_bit_cast(i32x4, b), c, 0,
-                                                     0, 0);
-    }
-};
-
 // MI355X places workgroup b on XCD b % 8 and each XCD has its own L2.  Renumber
 // so that the tiles one XCD runs at the same time form a compact block of C
 // (rows of A and columns of B that the XCD's L2 then shares):

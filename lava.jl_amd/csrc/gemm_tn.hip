@@ -1,8 +1,7 @@
 // gemm_tn.hip -- the compute-bound GEMM: eligibility, the layout dispatcher and the
 // instances with both operands K-contiguous (A row-major, B column-major: the bf16
-// configuration, and every int8 product), which run gemm_tn16_kernel.  The kernels are
-// in gemm_tn_kernel.hpp; the other operand forms (gemm_tn_kernel) are instantiated in
-// gemm_tn_{nk,kn,nn}.hip.
+// configuration, and every int8 product).  The kernel (gemm_tn16_kernel) is
+// gemm_tn_kernel.hpp; the other operand forms are instantiated in gemm_tn_{nk,kn,nn}.hip.
 #include "gemm_tn_kernel.hpp"
 
 namespace lava {

@@ -1,6 +1,5 @@
-// gemm_tn_kernel.hpp -- the compute-bound GEMM kernels, C row-major, every operand layout:
-// gemm_tn16_kernel (16x16 MFMAs) when both operands are K-contiguous, gemm_tn_kernel
-// (32x32 MFMAs) when one is M/N-contiguous.
+// gemm_tn_kernel.hpp -- the compute-bound GEMM kernel (gemm_tn16_kernel), C row-major,
+// every operand layout.
 //
 // This is the staged cooperative-matrix GEMM (src/device/coopmat_intrinsics.jl:
 // 104-148 stages A and B through workgroup memory and reads A RowMajor and B
@@ -8,40 +7,22 @@
 // same loop at workgroup scope) laid out for CDNA4:
 //
 //  * one 256 x 256 tile of C per workgroup of 4 wavefronts (one per SIMD), each
-//    wavefront owning a 128 x 128 sub-tile = 4 x 4 MFMA 32x32 accumulators, or 8 x 8
-//    16x16 ones (256 fp32 registers per lane, all in AGPRs);
+//    wavefront owning a 128 x 128 sub-tile = 8 x 8 MFMA 16x16 accumulators (256 fp32
+//    registers per lane, all in AGPRs);
 //  * K advances 128 bytes at a time (64 bf16/fp16 or 128 int8): A and B slices of
 //    32 KB each, double-buffered in LDS (2 x 64 KB);
 //  * global -> LDS with buffer_load_dwordx4 ... lds: each lane moves 16 bytes
 //    straight into LDS, no register staging, addressed by a buffer resource plus a
 //    32-bit lane offset (the wave-uniform parts in soffset); one wavefront
 //    instruction fills 1 KB of LDS, lane l the 16-byte slot l;
-//  * each operand is staged in one of two forms, chosen by its layout (AK / BK):
-//    - K-contiguous (A row-major, B column-major): 256 rows x 128 bytes of K; an
-//      instruction covers 8 rows, lane l row l / 8 and slot l % 8.  The slot a
-//      logical 16-byte chunk c of row r lands in is c ^ swz(r), chosen by which
-//      global chunk each lane fetches, so that the fragment reads (consecutive rows,
-//      one chunk column) spread over all banks: swz(r) = (r & 7) ^ ((r >> 3) & 1) for
-//      the 32x32 reads (32 rows per 32 lanes), swz(r) = r & 7 for the 16x16 ones (16
-//      rows per 16 lanes; measured with SQ_LDS_BANK_CONFLICT, the row / 8 flip costs
-//      them 4 conflict cycles per read); a fragment is one ds_read_b128 per lane;
-//    - M/N-contiguous (A column-major, B row-major; 16-bit types): 64 rows of K x
-//      512 bytes (256 m or n); an instruction covers 2 rows, lane l row l / 32 and
-//      slot l % 32, which holds logical chunk slot ^ F(row % 4), F = {0, 6, 10, 12};
-//      a fragment is two transposing reads (ds_read_b64_tr_b16: in a 16-lane group,
-//      output lane i value j is the 16-bit word at source lane 4 j + i / 4's address
-//      + 2 (i % 4)), source lanes pointing at 4 k rows x 4 columns, so output lane i
-//      receives the 4 k values of column i.  F makes the 4 rows x 2 chunks of one
-//      16-lane group, and the 4 rows x 4 chunks of a 32-lane pair, distinct modulo
-//      the bank period;
-//  * 32x32 kernel: fragments are 16 bytes per lane, one MFMA 32x32x16 (16-bit) or
-//    32x32x32 (int8) each; 4 sub-steps of 32 bytes of K per stage, each 16 MFMAs, with the next
-//    sub-step's fragments read underneath (double-buffered fragment registers) and
-//    the next stage's 16 DMA loads issued one per two MFMAs over sub-steps 0 and 1
-//    (a wavefront's vector-memory issue takes ~40-70 cycles per 1 KB instruction;
-//    one per MFMA would stall the MFMA stream);
-//  * 16x16 kernel: two k-steps of 64 bytes per stage, 64 MFMAs each; the barrier in
-//    the middle of the stage (see gemm_tn16_kernel);
+//  * each operand is staged in one of two forms, chosen by its layout (TnSide):
+//    K-contiguous (A row-major, B column-major), 256 rows x 128 bytes of K, or
+//    M/N-contiguous (A column-major, B row-major; 16-bit types), 64 rows of K x 512
+//    bytes; 16-byte chunks XOR-swizzled per row, chosen by which global chunk each lane
+//    fetches, so that the fragment reads are bank-conflict-free;
+//  * a fragment is 16 bytes per lane (one ds_read_b128, or two transposing
+//    ds_read_b64_tr_b16 for an M/N-contiguous operand); per stage two k-steps of 64
+//    bytes, 64 MFMAs each, one barrier in the middle of the stage (gemm_tn16_kernel);
 //  * the MFMA's A operand is the B slice and its B operand the A slice, so each
 //    lane's accumulator holds runs of 4 consecutive columns of one row of C; the
 //    epilogue stages them through LDS and stores whole 512-byte row runs;
@@ -114,110 +95,126 @@ __device__ __forceinline__ int tn_mn_swz(int r4) { return (0xCA60 >> (4 * r4)) &
 template <typename T, bool KC>
 struct TnSide;
 
-// K-contiguous: the slice is 256 rows (m or n) x 128 bytes of K.
+// K-contiguous: the slice is 256 rows (m or n) x 128 bytes of K.  Row r's logical
+// 16-byte chunk c is stored at slot c ^ (r % 8): a 16x16 fragment read (16 consecutive
+// rows, one chunk per 16 lanes) then hits every bank once.  (With an extra ^ (r / 8 % 2),
+// the swizzle a 32-row read needs, the 16-row read costs ~4 conflict cycles; measured with
+// SQ_LDS_BANK_CONFLICT.)
 template <typename T>
 struct TnSide<T, true> {
     v4i rs;
-    uint32_t off[2];   // per chunk parity (instruction i & 1)
+    uint32_t off;      // the lane's row and chunk within an instruction's 8 rows
     uint32_t step;     // soffset per instruction: 8 rows
     int lim;           // instruction i's rows are inside iff 8 i < lim
-    int kend[2];       // last byte (+1) of the lane's chunk per parity
-    int rd, swz, h;
+    int kend;          // last byte (+1) of the lane's chunk
+    int rd16, sl16[2];   // fragment reads: row offset, chunk slot per k-step
 
-    // rows_in: rows of this tile inside the matrix; wx: the wavefront's 128-row half.
-    // Row r's 16-byte chunk c is stored at c ^ (r % 8) ^ (flip ? r / 8 % 2 : 0).
+    // rows_in: rows of this tile inside the matrix; w: the wavefront; wx: its 128-row half.
     __device__ __forceinline__ void init(const T* X, int64_t ld_b, int tile, int rows_in, int64_t, int, int w, int wx,
-                                         int lane, int flip = 1) {
+                                         int lane) {
         rs = make_rsrc(reinterpret_cast<const char*>(X) + (int64_t)tile * TN_TILE * ld_b,
                        (uint32_t)(rows_in * ld_b));
+        // DMA: an instruction covers 8 rows; lane l row l / 8, slot l % 8, which holds chunk slot ^ row % 8
         const int lr = lane >> 3;
-        const int c_even = (lane & 7) ^ lr, c_odd = c_even ^ flip;
-        const uint32_t row = (uint32_t)((64 * w + lr) * ld_b);
-        off[0] = row + 16u * c_even;
-        off[1] = row + 16u * c_odd;
+        const int c = (lane & 7) ^ lr;
+        off = (uint32_t)((64 * w + lr) * ld_b + 16 * c);
         step = (uint32_t)(8 * ld_b);
         lim = rows_in - 64 * w - lr;
-        kend[0] = 16 * c_even + 16;
-        kend[1] = 16 * c_odd + 16;
-        rd = (wx * 128 + (lane & 31)) * TN_KB;
-        swz = (lane & 7) ^ ((lane >> 3) & 1);
-        h = lane >> 5;
+        kend = 16 * c + 16;
+        // fragments: row 16 t + lane % 16 of the half, chunk 4 u + lane / 16
+        rd16 = (wx * 128 + (lane & 15)) * TN_KB;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) sl16[u] = ((4 * u + (lane >> 4)) ^ (lane & 7)) * 16;
     }
     __device__ __forceinline__ bool valid(int i, uint32_t kofs, int kb) const {
-        return 8 * i < lim && (int)kofs + kend[i & 1] <= kb;
+        return 8 * i < lim && (int)kofs + kend <= kb;
     }
-    __device__ __forceinline__ uint32_t voff(int i) const { return off[i & 1]; }
+    __device__ __forceinline__ uint32_t voff(int) const { return off; }
     __device__ __forceinline__ uint32_t soff(int i, uint32_t kofs) const { return i * step + kofs; }
-    // operand row 32 t + lane % 32 of the wavefront's half, chunk 2 s + lane / 32
-    __device__ __forceinline__ uint4 read(const uint8_t* slice, int s, int t) const {
-        const int slot = ((2 * s + h) ^ swz) * 16;
-        return *reinterpret_cast<const uint4*>(slice + rd + t * 32 * TN_KB + slot);
+    // fragment t (rows 16 t of the half) of k-step u (64 bytes of K)
+    __device__ __forceinline__ uint4 read16(const uint8_t* slice, int u, int t) const {
+        return *reinterpret_cast<const uint4*>(slice + rd16 + t * 16 * TN_KB + sl16[u]);
     }
 };
 
-// M/N-contiguous (16-bit): the slice is 64 rows of K x 512 bytes (256 m or n).
+// M/N-contiguous (16-bit): the slice is 64 rows of K x 512 bytes (256 m or n).  Row r's
+// logical 16-byte chunk c is stored at slot c ^ F(r % 4) ^ 8 (r / 8 % 4), F = {0, 6, 10, 12}:
+// a 16x16 fragment is two transposing reads (ds_read_b64_tr_b16: in a 16-lane group,
+// output lane i value j is the 16-bit word at source lane 4 j + i / 4's address
+// + 2 (i % 4)), whose 16 k rows (4 groups of 4, 8 apart) x 32 bytes that swizzle spreads
+// over all banks (without the r / 8 term, ~2 conflict cycles per read; SQ_LDS_BANK_CONFLICT).
 template <typename T>
 struct TnSide<T, false> {
     static_assert(sizeof(T) == 2, "M/N-contiguous staging reads 16-bit elements transposed");
     v4i rs;
-    uint32_t off[2];   // per instruction parity (the row's swizzle depends on (2 i + h) % 4)
+    uint32_t off[4];   // per instruction variant (i % 2, i / 4): the row's swizzle depends on them
     uint32_t step;     // soffset per instruction: 2 rows of K
     uint32_t ld;       // bytes per row of K
     int klim;          // instruction i's row is inside iff k0 + 2 i < klim
-    bool cin[2];       // the lane's chunk lies inside M (N), per parity
-    int mnr[2];        // read offsets of the two transposing reads, t = 0
-    int fh;            // the swizzle's bits 2-3: chunk group t lands at t ^ fh
+    bool cin[4];       // the lane's chunk lies inside M (N), per variant
+    int mr16;          // fragment reads: the lane's row and byte offset
+    int c16[8];        // fragment reads: the stored chunk of column block t, times 16
 
-    // mn_total: M (N); K: the depth in elements; wx: the wavefront's 128-column half.
+    // mn_total: M (N); K: the depth in elements; w: the wavefront; wx: its 128-column half.
     __device__ __forceinline__ void init(const T* X, int64_t ld_b, int tile, int, int64_t mn_total, int K, int w,
                                          int wx, int lane) {
         const int64_t col0 = (int64_t)tile * TN_TILE;
         rs = make_rsrc(reinterpret_cast<const char*>(X) + col0 * (int64_t)sizeof(T),
                        (uint32_t)((int64_t)K * ld_b - col0 * (int64_t)sizeof(T)));
+        // DMA: instruction i covers rows 16 w + 2 i + h (h = lane / 32), slot lane % 32; that
+        // row's r % 4 is 2 (i % 2) + h and r / 8 % 4 is (2 w + i / 4) % 4
         const int h = lane >> 5, p = lane & 31;
 #pragma unroll
-        for (int par = 0; par < 2; ++par) {
-            const int c = p ^ tn_mn_swz((2 * par + h) & 3);
-            off[par] = (uint32_t)((16 * w + h) * ld_b + 16 * c);
-            cin[par] = col0 + 8 * c < mn_total;
+        for (int v = 0; v < 4; ++v) {
+            const int c = p ^ tn_mn_swz((2 * (v & 1) + h) & 3) ^ (((2 * w + (v >> 1)) & 3) << 3);
+            off[v] = (uint32_t)((16 * w + h) * ld_b + 16 * c);
+            cin[v] = col0 + 8 * c < mn_total;
         }
         step = (uint32_t)(2 * ld_b);
         ld = (uint32_t)ld_b;
         klim = K - 16 * w - h;
-        // transposing reads: source lane ss of 16-lane group g points at k row
-        // 8 (g / 2) + 4 r + ss / 4, columns 16 (g % 2) + 4 (ss % 4) of the 32-column block
+        // fragments: source lane ss of 16-lane group g points at k row 8 g + 4 r + ss / 4
+        // (+ 32 u), columns 16 t + 4 (ss % 4) of the half; that row's swizzle is
+        // F(ss / 4) ^ 8 g for every u, t and r
         const int ss = lane & 15, g = lane >> 4;
-        const int f = tn_mn_swz(ss >> 2);
-        fh = (f >> 2) & 3;
-        const int cl2 = (2 * (g & 1) + ((ss & 3) >> 1)) ^ (f & 3);
+        const int f = tn_mn_swz(ss >> 2) ^ (g << 3);
+        mr16 = (8 * g + (ss >> 2)) * 512 + 8 * (ss & 1);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) mnr[r] = (8 * (g >> 1) + 4 * r + (ss >> 2)) * 512 + 16 * (16 * wx + cl2) + 8 * (ss & 1);
+        for (int t = 0; t < 8; ++t) c16[t] = ((16 * wx + 2 * t + ((ss & 3) >> 1)) ^ f) * 16;
     }
+    __device__ __forceinline__ static int variant(int i) { return (i & 1) | ((i >> 2) << 1); }
     __device__ __forceinline__ bool valid(int i, uint32_t kofs, int) const {
-        return (int)(kofs / sizeof(T)) + 2 * i < klim && cin[i & 1];
+        return (int)(kofs / sizeof(T)) + 2 * i < klim && cin[variant(i)];
     }
-    __device__ __forceinline__ uint32_t voff(int i) const { return off[i & 1]; }
+    __device__ __forceinline__ uint32_t voff(int i) const { return off[variant(i)]; }
     __device__ __forceinline__ uint32_t soff(int i, uint32_t kofs) const {
         return (kofs / (uint32_t)sizeof(T)) * ld + i * step;
     }
-    __device__ __forceinline__ uint4 read(const uint8_t* slice, int s, int t) const {
-        const uint8_t* b = slice + s * 16 * 512 + 64 * (t ^ fh);
+    // fragment t (columns 16 t of the half) of k-step u (32 rows of K): two transposing
+    // reads, k rows 8 g + [0, 4) and 8 g + [4, 8) of the k-step
+    __device__ __forceinline__ uint4 read16(const uint8_t* slice, int u, int t) const {
+        const uint8_t* b = slice + u * 32 * 512 + mr16 + c16[t];
         const tn_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) tn_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(b + mnr[0]));
+            (__attribute__((address_space(3))) tn_s16x4*)(const __attribute__((address_space(3))) uint8_t*)b);
         const tn_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) tn_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(b + mnr[1]));
+            (__attribute__((address_space(3))) tn_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(b + 4 * 512));
         return __builtin_bit_cast(uint4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     }
 };
 
+// The tile kernel.  AK / BK: A / B K-contiguous (row-major A, column-major B) or
+// M/N-contiguous; int8 needs both K-contiguous.  16x16 MFMAs (16x16x32 for 16-bit
+// types, 16x16x64 for int8), 8 x 8 accumulators of 16 x 16 per wavefront: at the chip's
+// power limit the 16x16 shape sustains ~11 % more than 32x32 (it moves ~20 % fewer
+// register-file bytes per flop), and its fragments (16 rows x 64 bytes of K per k-step)
+// let the whole stage be read by the middle of the k-tile, so that the barrier sits there
+// and each DMA gets a full k-tile to land.
 template <typename T, typename OutT, bool EPI, bool RAGGED, bool AK, bool BK>
 __global__ void __launch_bounds__(256, 1)
-    gemm_tn_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
-                   int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi, TnBounds bnd) {
-    using AccV = typename Mfma32<T>::acc_t;
+    gemm_tn16_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
+                     int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi, TnBounds bnd) {
+    using AccV = typename Mfma16<T>::acc_t;
     typedef typename Mfma16<T>::acc_elem Acc;
-    // LDS reads per sub-step: 4 per K-contiguous operand, 8 per M/N-contiguous one
-    constexpr int NR = (AK ? 4 : 8) + (BK ? 4 : 8);
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TN_SLICE];  // [stage][A,B][32 KB]
 
     const int lane = threadIdx.x & 63;
@@ -257,318 +254,6 @@ __global__ void __launch_bounds__(256, 1)
         }
     };
 
-    AccV acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
-
-    // ---- fragments: 32x32 MFMA operands, 16 bytes (8 k values of one row m / column n)
-    // per lane: lanes 0-31 k 0..7, lanes 32-63 k 8..15 of the sub-step.
-    struct Frags {
-        uint4 a[4], b[4];
-    };
-    auto read_frags = [&](Frags& f, const uint8_t* base, int s) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            f.b[t] = sb.read(base + TN_SLICE, s, t);
-            f.a[t] = sa.read(base, s, t);
-        }
-    };
-    // the r-th (0..7) of those reads, in the same order: b[0], a[0], b[1], a[1], ...
-    auto read_one = [&](Frags& f, const uint8_t* base, int s, int r) {
-        if (r & 1) f.a[r >> 1] = sa.read(base, s, r >> 1);
-        else f.b[r >> 1] = sb.read(base + TN_SLICE, s, r >> 1);
-    };
-    // MFMA A operand = B slice (rows are columns n of C), B operand = A slice (rows m):
-    // the accumulator then holds C^T, 4 consecutive n per lane and register group.
-    auto mma = [&](const Frags& f, int i0, int i1) {
-#pragma unroll
-        for (int i = i0; i < i1; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = Mfma32<T>::run(f.b[j], f.a[i], acc[i][j]);
-    };
-
-    // Per k-tile (128 bytes of K = 4 sub-steps), branch-free so the interleave holds:
-    //   s = 0, 1: 16 MFMAs on the current fragments; after each, alternately one of the
-    //             next sub-step's 8 LDS reads and one of 8 DMA loads of the next tile
-    //             (reads issued in one burst fill the LDS command queue and stall the
-    //             wave's MFMA issue behind them);
-    //   s = 2:    16 MFMAs with the next sub-step's reads interleaved;
-    //   s = 3:    12 MFMAs (8 when an operand is M/N-contiguous); wait for this wave's
-    //             DMA; barrier; then the next tile's s = 0 reads under the last 4 (8).
-    // On the last tile the "next" tile re-fetches the current one into the idle stage.
-    {
-#pragma unroll
-        for (int q = 0; q < 16; ++q) dma(q, 0, 0);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    Frags fa, fb;
-    // The same read order as the loop's last sub-step, one at a time: then the loop head
-    // waits only for the reads its first MFMA needs (lgkmcnt counts in issue order; with
-    // another order here the compiler must wait for all of them on every iteration).
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-        read_one(fa, smem, 0, r);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    // MFMAs before the barrier in s = 3 (the rest hide the next tile's first reads)
-    constexpr int S3_PRE = NR == 8 ? 3 : 2;
-
-    for (int kt = 0; kt < ktiles; ++kt) {
-        const int st = kt & 1;
-        const uint8_t* base = smem + st * 2 * TN_SLICE;
-        const uint8_t* next = smem + (st ^ 1) * 2 * TN_SLICE;
-        const uint32_t kofs_next = (uint32_t)(kt + 1 < ktiles ? kt + 1 : kt) * TN_KB;
-        // s = 0: 16 MFMAs; s = 1's reads and the first 8 DMA loads alternate between them
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] = Mfma32<T>::run(fa.b[j], fa.a[i], acc[i][j]);
-                if (j & 1) dma(2 * i + (j >> 1), st ^ 1, kofs_next);
-                else read_one(fb, base, 1, 2 * i + (j >> 1));
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        // s = 1: the same with s = 2's reads and the other 8 DMA loads
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[i][j] = Mfma32<T>::run(fb.b[j], fb.a[i], acc[i][j]);
-                if (j & 1) dma(8 + 2 * i + (j >> 1), st ^ 1, kofs_next);
-                else read_one(fa, base, 2, 2 * i + (j >> 1));
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        read_frags(fb, base, 3);
-        mma(fa, 0, 4);
-        // interleave this sub-step's NR LDS reads (0x100) with its 16 MFMAs (0x008)
-        if constexpr (NR == 8) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 2);
-            }
-        } else if constexpr (NR == 12) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 3, 2);
-                __builtin_amdgcn_sched_group_barrier(0x008, 4, 2);
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        // s = 3: most MFMAs, publish the next stage, its first reads under the rest
-        mma(fb, 0, S3_PRE);
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's part of the next tile landed
-        __syncthreads();
-        __builtin_amdgcn_sched_barrier(0);
-        read_frags(fa, next, 0);
-        mma(fb, S3_PRE, 4);
-        if constexpr (NR == 8) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 3);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 3);
-            }
-        } else if constexpr (NR == 12) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 3, 3);
-                __builtin_amdgcn_sched_group_barrier(0x008, 2, 3);
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 3);
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 3);
-            }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-    }
-
-    // ---- epilogue through LDS, so that global stores are whole 512-byte row runs.
-    // acc[i][j] register r of lane l is C[m][n] with m = 128 wm + 32 i + l % 32 and
-    // n = 128 wn + 32 j + 8 (r / 4) + 4 (l / 32) + r % 4 within the tile.  Each wave
-    // stages 32 rows x 128 columns at a time (one i) in its own 16.5 KB of the idle
-    // stage buffers (4 waves: 66 KB of the 128 KB), rows padded to 528 bytes so the
-    // 32 rows of one column group land on distinct banks; then reads whole rows back:
-    // lanes 0..31 and 32..63 each cover one 512-byte row per instruction.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    constexpr int EP_PITCH = 128 * 4 + 16;
-    const int rr = lane & 31;
-    uint8_t* ep = smem + w * (32 * EP_PITCH);
-    typedef Acc Acc4 __attribute__((ext_vector_type(4)));
-    const int64_t row0 = (int64_t)tm * TN_TILE + wm * 128, col0 = (int64_t)tn * TN_TILE + wn * 128;
-    OutT* cbase = C + row0 * ldc + col0;
-    // columns of this lane's 4-column group inside the matrix (RAGGED: 0..4)
-    int cols_in = 4;
-    if constexpr (RAGGED) {
-        const int64_t left = bnd.n - (col0 + 4 * rr);
-        cols_in = left >= 4 ? 4 : (left > 0 ? (int)left : 0);
-    }
-    // one row quarter i at a time; i is a template constant so that acc stays in registers
-    typedef float F4 __attribute__((ext_vector_type(4)));
-    auto quarter = [&](auto itag) {
-        constexpr int i = decltype(itag)::value;
-        // The epilogue's init terms for the 16 rows x 4 columns this lane finishes, all
-        // requested before the staging so that their HBM latency overlaps it (loaded one
-        // row at a time inside the store loop they cost one round trip per row).
-        F4 rin[EPI ? 16 : 1];
-        float bin[EPI ? 16 : 1];
-        F4 bcol = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (EPI) {
-            const int64_t n = col0 + 4 * rr;
-            // 4 floats at p, or those of them inside the matrix (columns < N)
-            auto ld4 = [&](const float* p) {
-                if (epi.vec4 && cols_in == 4) return *reinterpret_cast<const F4*>(p);
-                F4 r = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    if (k < cols_in) r[k] = p[k];
-                return r;
-            };
-            if (epi.bias && epi.bias_on_cols) bcol = ld4(epi.bias + n);
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int64_t m = row0 + 32 * i + 2 * t + h;
-                rin[t] = F4{0.f, 0.f, 0.f, 0.f};
-                bin[t] = 0.f;
-                if (RAGGED && m >= bnd.m) continue;
-                if (epi.residual) rin[t] = ld4(epi.residual + m * epi.ldr + n);
-                if (epi.bias && !epi.bias_on_cols) bin[t] = epi.bias[m];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const Acc4 v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
-                *reinterpret_cast<Acc4*>(ep + rr * EP_PITCH + (32 * j + 8 * g + 4 * h) * 4) = v;
-            }
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): the wave's staged rows are in LDS
-        __builtin_amdgcn_wave_barrier();
-        auto store_rows = [&](auto acttag) {
-            constexpr int ACT = decltype(acttag)::value;
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int row = 2 * t + h;                       // 0..31 of this i
-                const Acc4 v = *reinterpret_cast<const Acc4*>(ep + row * EP_PITCH + rr * 16);
-                OutT* dst = cbase + (int64_t)(32 * i + row) * ldc + 4 * rr;
-                if (RAGGED && row0 + 32 * i + row >= bnd.m) continue;
-                if constexpr (!EPI && std::is_same<OutT, Acc>::value) {
-                    if (!RAGGED || (cols_in == 4 && bnd.cvec)) {
-                        *reinterpret_cast<Acc4*>(dst) = v;
-                    } else {
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            if (k < cols_in) dst[k] = v[k];
-                    }
-                } else {
-                    // the fused epilogue on 4 consecutive columns of one row, narrowed (RNE) to D's type
-                    typedef OutT Out4 __attribute__((ext_vector_type(4)));
-                    Out4 o;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        float x = (float)v[k];
-                        // the same fp32 sums as epi_apply: (bias + residual), then acc + that
-                        if constexpr (EPI) x = epi_act_c<ACT>(x + ((bin[t] + bcol[k]) + rin[t][k]));
-                        o[k] = narrow<OutT>(x);
-                    }
-                    if (!RAGGED || (cols_in == 4 && bnd.cvec)) {
-                        *reinterpret_cast<Out4*>(dst) = o;
-                    } else {
-#pragma unroll
-                        for (int k = 0; k < 4; ++k)
-                            if (k < cols_in) dst[k] = o[k];
-                    }
-                }
-            }
-        };
-        if constexpr (EPI) {
-            switch (epi.act) {   // uniform: one branch per quarter, none per element
-            case EPI_RELU: store_rows(std::integral_constant<int, EPI_RELU>{}); break;
-            case EPI_GELU_TANH: store_rows(std::integral_constant<int, EPI_GELU_TANH>{}); break;
-            case EPI_GELU_ERF: store_rows(std::integral_constant<int, EPI_GELU_ERF>{}); break;
-            default: store_rows(std::integral_constant<int, EPI_NONE>{}); break;
-            }
-        } else {
-            store_rows(std::integral_constant<int, EPI_NONE>{});
-        }
-        __builtin_amdgcn_s_waitcnt(0xc07f);   // reads done before the next i overwrites
-        __builtin_amdgcn_wave_barrier();
-    };
-    quarter(std::integral_constant<int, 0>{});
-    quarter(std::integral_constant<int, 1>{});
-    quarter(std::integral_constant<int, 2>{});
-    quarter(std::integral_constant<int, 3>{});
-}
-
-// Both operands K-contiguous (A row-major, B column-major: the bf16 configuration and
-// every int8 product): the same 256 x 256 tile, LDS stages and epilogue as
-// gemm_tn_kernel, on 16x16 MFMAs (16x16x32 for 16-bit types, 16x16x64 for int8) --
-// 8 x 8 accumulators of 16 x 16 per wavefront.  At the chip's power limit the 16x16 shape
-// sustains ~11 % more than 32x32 (it moves ~20 % fewer register-file bytes per flop),
-// and its fragments (16 rows x 64 bytes of K per k-step) let the whole stage be read by
-// the middle of the k-tile, so that the barrier sits there and each DMA gets a full
-// k-tile to land.
-template <typename T, typename OutT, bool EPI, bool RAGGED>
-__global__ void __launch_bounds__(256, 1)
-    gemm_tn16_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
-                     int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi, TnBounds bnd) {
-    using AccV = typename Mfma16<T>::acc_t;
-    typedef typename Mfma16<T>::acc_elem Acc;
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TN_SLICE];  // [stage][A,B][32 KB]
-
-    const int lane = threadIdx.x & 63;
-    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    int tm, tn;
-    xcd_tile(blockIdx.x, tiles_m, tiles_n, 4, tm, tn);
-    const int wm = w >> 1, wn = w & 1;
-    const int h = lane >> 5;
-
-    // Rows (m, n) of this tile inside the matrix: all 256 unless RAGGED and the tile is the last.
-    int a_rows = TN_TILE, b_rows = TN_TILE;
-    if constexpr (RAGGED) {
-        a_rows = (int)(bnd.m - (int64_t)tm * TN_TILE < TN_TILE ? bnd.m - (int64_t)tm * TN_TILE : TN_TILE);
-        b_rows = (int)(bnd.n - (int64_t)tn * TN_TILE < TN_TILE ? bnd.n - (int64_t)tn * TN_TILE : TN_TILE);
-    }
-    const int kelems = bnd.kb / (int)sizeof(T);
-    TnSide<T, true> sa;
-    TnSide<T, true> sb;
-    // the chunk swizzle without the row / 8 flip: the 16x16 fragment read (16 rows x one
-    // chunk per 16 lanes) is bank-conflict-free with it, not with the flip
-    sa.init(A, lda_b, tm, a_rows, bnd.m, kelems, w, wm, lane, 0);
-    sb.init(B, ldb_b, tn, b_rows, bnd.n, kelems, w, wn, lane, 0);
-    // wave w fills 8 KB of each slice: K-contiguous rows [64 w, 64 w + 64), M/N-contiguous
-    // k rows [16 w, 16 w + 16); instruction i 1 KB of it
-    const uint32_t lds0 = lds_addr(smem) + w * 64 * TN_KB;
-
-    // DMA load q (0..15) of a k-tile into `stage`: q < 8 are A, q >= 8 B.
-    auto dma = [&](int q, int stage, uint32_t kofs) {
-        const int i = q & 7;
-        const uint32_t dst = lds0 + stage * 2 * TN_SLICE + (q >> 3) * TN_SLICE + i * 1024;
-        if (q < 8) {
-            uint32_t off = sa.voff(i);
-            if constexpr (RAGGED) off = sa.valid(i, kofs, bnd.kb) ? off : OOB_OFS;
-            dma16(sa.rs, off, sa.soff(i, kofs), dst);
-        } else {
-            uint32_t off = sb.voff(i);
-            if constexpr (RAGGED) off = sb.valid(i, kofs, bnd.kb) ? off : OOB_OFS;
-            dma16(sb.rs, off, sb.soff(i, kofs), dst);
-        }
-    };
-
     AccV acc[8][8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -577,23 +262,20 @@ __global__ void __launch_bounds__(256, 1)
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc[i][j][r] = 0;
 
-    // ---- fragments: 16x16 MFMA operands, 16 bytes per lane: row lane % 16 of a 16-row
-    // block, 16-byte chunk 4 u + lane / 16 of k-step u (the 64-byte half u of the stage's
-    // 128 bytes of K).  a[i]: rows 16 i of the wave's 128 m; b[j]: rows 16 j of its 128 n.
+    // ---- fragments: 16x16 MFMA operands, 16 bytes per lane: row (m or n) lane % 16 of a
+    // 16-row block, 8 k values (16-bit) or 16 (int8) at 8 (lane / 16) of k-step u (the
+    // 64-byte half u of the stage's 128 bytes of K).  a[i]: rows 16 i of the wave's 128 m;
+    // b[j]: rows 16 j of its 128 n.
     struct F16 {
         uint4 a[8], b[8];
     };
-    const int g16 = lane >> 4;
-    const int swz16 = lane & 7;   // the stage's chunk swizzle of row 8 k + lane % 8 (no flip)
-    const int rda = (wm * 128 + (lane & 15)) * TN_KB, rdb = (wn * 128 + (lane & 15)) * TN_KB;
     // fragment t (0..15) of k-step u, in the order the MFMAs (i-major) first use them:
     // a[0], b[0..7], a[1..7]
     auto rd16 = [&](F16& f, const uint8_t* stage, int u, int t) {
-        const int slot = ((4 * u + g16) ^ swz16) * 16;
         const bool isa = t == 0 || t > 8;
         const int blk = t == 0 ? 0 : (t <= 8 ? t - 1 : t - 8);
-        if (isa) f.a[blk] = *reinterpret_cast<const uint4*>(stage + rda + blk * 16 * TN_KB + slot);
-        else f.b[blk] = *reinterpret_cast<const uint4*>(stage + TN_SLICE + rdb + blk * 16 * TN_KB + slot);
+        if (isa) f.a[blk] = sa.read16(stage, u, blk);
+        else f.b[blk] = sb.read16(stage + TN_SLICE, u, blk);
     };
     // MFMA A operand = B fragment (rows are columns n of C), B operand = A fragment (rows
     // m): acc[i][j] register r of lane l is C[m][n], m = 128 wm + 16 i + l % 16,
@@ -800,18 +482,11 @@ int launch_gemm_tn_layout(const T* A, const T* B, OutT* C, int64_t M, int64_t N,
     bnd.kb = (int)(K * (int64_t)sizeof(T));
     bnd.cvec = ldc % 4 == 0 && aligned(C, 4 * sizeof(OutT));
     const int64_t lda_b = lda * (int64_t)sizeof(T), ldb_b = ldb * (int64_t)sizeof(T);
-    if constexpr (AK && BK) {
-        if (ragged)
-            hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, true>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
-                               0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
-        else
-            hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, false>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
-                               0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
-    } else if (ragged)
-        hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI, true, AK, BK>), dim3((unsigned)(tiles_m * tiles_n)), dim3(256),
-                           0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
+    if (ragged)
+        hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, true, AK, BK>), dim3((unsigned)(tiles_m * tiles_n)),
+                           dim3(256), 0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
     else
-        hipLaunchKernelGGL((gemm_tn_kernel<T, OutT, EPI, false, AK, BK>), dim3((unsigned)(tiles_m * tiles_n)),
+        hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, false, AK, BK>), dim3((unsigned)(tiles_m * tiles_n)),
                            dim3(256), 0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
     LAVA_LAUNCH_CHECK("gemm_tn_kernel");
     return LAVA_HIP_OK;

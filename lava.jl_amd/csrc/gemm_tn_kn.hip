@@ -1,4 +1,4 @@
-// gemm_tn_kn.hip -- gemm_tn_kernel instances for A row-major (K-contiguous), B row-major (N-contiguous): the coopmat2 and fp16-256 layout.
+// gemm_tn_kn.hip -- tile-kernel instances for A row-major (K-contiguous), B row-major (N-contiguous): the coopmat2 and fp16-256 layout.
 #include "gemm_tn_kernel.hpp"
 
 namespace lava {

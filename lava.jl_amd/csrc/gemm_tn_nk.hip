@@ -1,4 +1,4 @@
-// gemm_tn_nk.hip -- gemm_tn_kernel instances for A column-major (M-contiguous), B column-major (K-contiguous).
+// gemm_tn_nk.hip -- tile-kernel instances for A column-major (M-contiguous), B column-major (K-contiguous).
 #include "gemm_tn_kernel.hpp"
 
 namespace lava {

@@ -1,4 +1,4 @@
-// gemm_tn_nn.hip -- gemm_tn_kernel instances for A column-major (M-contiguous), B row-major (N-contiguous).
+// gemm_tn_nn.hip -- tile-kernel instances for A column-major (M-contiguous), B row-major (N-contiguous).
 #include "gemm_tn_kernel.hpp"
 
 namespace lava {
