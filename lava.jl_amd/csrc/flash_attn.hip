@@ -25,8 +25,8 @@
 //    blocks are masked per element, and a wavefront skips the products of a block
 //    that lies entirely above its 32 queries;
 //  * workgroups are ordered XCD by XCD so that all query blocks of one (batch,
-//    head) run on one XCD and share its K and V through that XCD's L2, longest
-//    query blocks first.
+//    head) run on one XCD and share its K and V through that XCD's L2; causal:
+//    longest query blocks first across the XCD's heads (fa_order).
 #include <hip/hip_runtime.h>
 
 #include "lava_coopmat.hpp"
@@ -53,6 +53,33 @@ struct FaParams {
     int causal;
 };
 
+// Workgroup -> (batch * head, query block).  Workgroups are dispatched round-robin
+// over the 8 XCDs (blockIdx % 8).  Non-causal: every block costs the same, and each
+// XCD takes a contiguous range of (head, block) pairs, so one head's K and V stay in
+// one XCD's L2.  Causal: query block qb costs qb + 1 key blocks, so each XCD takes
+// whole heads (when 8 divides B * H) and runs their heaviest blocks first, then the
+// next lighter ones -- longest first across heads, so that the dispatcher hands each
+// freed CU the heaviest block left and the light ones fill the tail; without the
+// split by XCD, heavy first over all heads.
+__device__ __forceinline__ void fa_order(int nqb, int nbh, bool causal, int& bh, int& qb) {
+    const int bid = blockIdx.x;
+    if (causal) {
+        if ((nbh & 7) == 0) {
+            const int h8 = nbh >> 3, local = bid >> 3;
+            qb = nqb - 1 - local / h8;
+            bh = (bid & 7) * h8 + local % h8;
+        } else {
+            qb = nqb - 1 - bid / nbh;
+            bh = bid % nbh;
+        }
+    } else {
+        const int total = nqb * nbh;
+        const int b2 = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+        bh = b2 / nqb;
+        qb = b2 % nqb;
+    }
+}
+
 __device__ __forceinline__ float wave_xor32_max(float x) { return fmaxf(x, __shfl_xor(x, 32, 64)); }
 
 template <bool CAUSAL>
@@ -63,12 +90,8 @@ __global__ void __launch_bounds__(256, 2) flash_fwd_kernel(FaParams p) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int nqb = p.S / FA_BQ;
     const int nbh = p.H * p.B;
-    // workgroup -> (batch*head, query block): consecutive ids on one XCD, heavy first
-    int bid = blockIdx.x, bh, qb;
-    const int total = nqb * nbh;
-    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-    bh = bid / nqb;
-    qb = CAUSAL ? (nqb - 1 - bid % nqb) : bid % nqb;
+    int bh, qb;
+    fa_order(nqb, nbh, CAUSAL, bh, qb);
     const int h = bh % p.H, b = bh / p.H;
 
     const f16* Qb = p.Q + h * p.sh + b * p.sb;
@@ -371,11 +394,8 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     const bool late = w >= F3_WAVES / 2;        // one phase behind its SIMD partner w - 4
     const int nqb = (p.S + F3_BQ - 1) / F3_BQ;   // the last query block may be partial
     const int nbh = p.H * p.B;
-    int bid = blockIdx.x;
-    const int total = nqb * nbh;
-    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-    const int bh = bid / nqb;
-    const int qb = CAUSAL ? (nqb - 1 - bid % nqb) : bid % nqb;
+    int bh, qb;
+    fa_order(nqb, nbh, CAUSAL, bh, qb);
     const int hh = bh % p.H, bb = bh / p.H;
     const int64_t head = (int64_t)hh * p.sh + (int64_t)bb * p.sb;
     f16* Ob = p.O + (int64_t)hh * p.osh + (int64_t)bb * p.osb;
