@@ -29,6 +29,10 @@
 //    longest query blocks first across the XCD's heads (fa_order).
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
+#include <type_traits>
+#include <utility>
+
 #include "lava_coopmat.hpp"
 #include "lava_hip_internal.hpp"
 
@@ -661,6 +665,352 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
         }
 }
 
+// ---- flash_fwd5_kernel: score and output wavefronts ----
+//
+// Same transposed formulation (S^T = K Q^T, O^T = V^T P^T on 32x32x16 f16 MFMAs, a
+// lane owns one query per 32-query half), with the work of 64 queries split between
+// the two wavefronts that share a SIMD (w and w + 4):
+//  * score wavefront w (0-3): Q^T of its 64 queries in registers; per key block it
+//    computes S^T = K Q^T (32 MFMAs), the online softmax (lazy rescale), and writes
+//    P^T as MFMA B-operand fragments (8 KB) and the rescale factors to workgroup
+//    memory;
+//  * output wavefront w + 4: O^T of the same 64 queries in registers; per key block
+//    it rescales O when told to and adds V^T P^T (32 MFMAs).
+// Every K or V fragment read from LDS feeds two MFMAs (two 32-query halves), and the
+// score wavefront's softmax VALU runs beside the output wavefront's MFMAs on the same
+// SIMD -- no phase barrier between them, one workgroup barrier per key block.
+// Score wavefronts compute S for block j + 1 while output wavefronts add P V of block
+// j; P is double-buffered.  One workgroup = 8 wavefronts = 256 queries; K in a
+// three-stage LDS ring, V in two stages.  The output wavefronts, which wait for the
+// score wavefronts, also issue every K and V load and sum the rows of P (from the
+// fp16 fragments they read, in fp32) -- the score wavefront does only the scores and
+// the softmax.
+constexpr int F5_PAIRS = 4;
+constexpr int F5_BQ = 64 * F5_PAIRS;   // 256 queries per workgroup
+constexpr int F5_BK = 64;
+constexpr int F5_KST = 3, F5_VST = 2;
+constexpr int F5_PF = 3;               // fragments read ahead of the MFMA that uses them
+
+typedef _Float16 f5_h2 __attribute__((ext_vector_type(2)));
+typedef uint32_t f5_u32x4 __attribute__((ext_vector_type(4)));
+
+// x in lanes 0-31 and 32-63 as two registers: one v_permlane32_swap between two
+// distinct copies of x (the builtin with one value twice may be given one register,
+// and a register swapped with itself does not produce both halves)
+__device__ __forceinline__ void f5_xor32_pair(float x, float& a, float& b) {
+    a = x;
+    b = x;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+
+template <bool CAUSAL>
+__global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams p) {
+    constexpr int DH = 128;
+    constexpr int RB = DH * 2;                 // 256 bytes per K / V row
+    constexpr int CH = RB / 16;                // 16 chunks
+    constexpr int TILE = F5_BK * RB;           // 16 KB
+    constexpr int NKS = DH / 16;               // 8 k-steps of S^T
+    constexpr int NDT = DH / 32;               // 4 O^T row tiles
+    constexpr int DPT = TILE / (1024 * F5_PAIRS);   // 4 DMA instructions per wavefront per tile
+    constexpr int PBUF = 8 * 1024;             // one pair's P^T fragments for one block
+    static_assert(DPT == 4, "4 DMA instructions per tile and wavefront");
+    __shared__ __attribute__((aligned(1024))) uint8_t kbuf[F5_KST][TILE];   // [key][RB], chunk ^ key % 16
+    __shared__ __attribute__((aligned(1024))) uint8_t vbuf[F5_VST][TILE];   // [key][RB], chunk ^ 4 (key % 4)
+    __shared__ __attribute__((aligned(1024))) uint8_t pbuf[2][F5_PAIRS][PBUF];
+    __shared__ float abuf[2][F5_PAIRS][64];    // rescale factor per query of the next block
+    __shared__ int fbuf[2][F5_PAIRS];          // whether that block rescales
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool is_s = w < F5_PAIRS;
+    const int pr = w & (F5_PAIRS - 1);         // the pair: queries q0 .. q0 + 63
+    const int nqb = (p.S + F5_BQ - 1) / F5_BQ;
+    const int nbh = p.H * p.B;
+    int bh, qb;
+    fa_order(nqb, nbh, CAUSAL, bh, qb);
+    const int hh = bh % p.H, bb = bh / p.H;
+    const int64_t head = (int64_t)hh * p.sh + (int64_t)bb * p.sb;
+    f16* Ob = p.O + (int64_t)hh * p.osh + (int64_t)bb * p.osb;
+    const int q0 = qb * F5_BQ + pr * 64;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int nkb_s = (p.S + F5_BK - 1) / F5_BK;
+    const int nkb = CAUSAL ? min((qb + 1) * (F5_BQ / F5_BK), nkb_s) : nkb_s;
+    const int last = CAUSAL ? min(nkb - 1, (q0 + 63) / F5_BK) : nkb - 1;   // this pair's last key block
+
+    // LDS-DMA of K (score wavefronts) or V (output wavefronts): wavefront pr moves rows
+    // 16 pr + 4 i + lane / 16 of a tile, physical chunk lane % 16; blocks past the end
+    // re-read the last one (every iteration issues the same DMAs); rows at or past S
+    // read zero.
+    const uint32_t row_bytes = (uint32_t)(p.sl * 2);
+    const f3_v4i rsrc_k = f3_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
+    const f3_v4i rsrc_v = f3_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
+    auto dma1 = [&](bool is_k, int j, int i) __attribute__((always_inline)) {
+        const int src = j < nkb ? j : nkb - 1;
+        const uint32_t soff = (uint32_t)src * F5_BK * row_bytes;
+        const int row = 16 * pr + 4 * i + lane / CH;
+        const uint32_t swz = is_k ? (uint32_t)((lane % CH) ^ (row & 15)) : (uint32_t)((lane % CH) ^ (4 * (row & 3)));
+        uint32_t v = (uint32_t)row * row_bytes + 16u * swz;
+        if ((src + 1) * F5_BK > p.S) v = src * F5_BK + row < p.S ? v : 0x80000000u;
+        const uint32_t dst = f3_lds_addr(is_k ? &kbuf[0][0] : &vbuf[0][0]) + (uint32_t)pr * 16 * RB +
+                             (uint32_t)(j % (is_k ? F5_KST : F5_VST)) * TILE + 1024u * i;
+        const f3_v4i& rs = is_k ? rsrc_k : rsrc_v;
+        f3_v4i r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = __builtin_amdgcn_readfirstlane(rs[e]);
+        f3_dma16(r, v, __builtin_amdgcn_readfirstlane(soff), __builtin_amdgcn_readfirstlane(dst));
+    };
+    typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
+    typedef __attribute__((address_space(3))) f3_s16x4 lds_s16x4;
+    // P^T fragment (kt, ks, qh) of pair pr in buffer b: 1 KB, lane l at 16 l
+    const uint32_t p_lane = f3_lds_addr(&pbuf[0][0][0]) + (uint32_t)pr * PBUF + 16u * lane;
+    auto paddr = [&](int b, int kt, int ks, int qh) __attribute__((always_inline)) -> uint32_t {
+        return p_lane + (uint32_t)(b * F5_PAIRS * PBUF + ((kt * 2 + ks) * 2 + qh) * 1024);
+    };
+
+    // prologue DMAs (output wavefronts): K_0, K_1, K_2, V_0
+    if (!is_s) {
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+#pragma unroll
+            for (int i = 0; i < DPT; ++i) dma1(true, t, i);
+#pragma unroll
+        for (int i = 0; i < DPT; ++i) dma1(false, 0, i);
+    }
+
+    if (is_s) {
+        // ================= score wavefront =================
+        f16x8 qf[2][NKS];   // Q^T B operands: query q0 + 32 qh + r32, d = 16 ks + 8 h + [0, 8)
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+            const int q = q0 + 32 * qh + r32;
+            const f16* qrow = p.Q + head + (int64_t)q * p.sl + 8 * h;
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) qf[qh][ks] = f16x8{};
+            if (q < p.S) {
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks) qf[qh][ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
+            }
+        }
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const uint4 u = __builtin_bit_cast(uint4, qf[qh][ks]);
+                asm volatile("" ::"v"(u.x), "v"(u.y), "v"(u.z), "v"(u.w));
+            }
+        // K fragment (kt, ks): row 32 kt + r32, chunk (2 ks + h) ^ (r32 % 16)
+        uint32_t kb0[NKS];
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks)
+            kb0[ks] = f3_lds_addr(&kbuf[0][0]) + (uint32_t)(r32 * RB + (((2 * ks + h) ^ (r32 & 15)) << 4));
+        f32x16 st[2][2];           // st[kt][qh] register r: key 32 kt + 8 (r / 4) + 4 h + r % 4
+        float m_run[2] = {-INFINITY, -INFINITY};
+        const float c = p.scale_log2;
+
+        // S_kb = K_kb Q^T, the softmax, P^T and the rescale factors into buffer b
+        auto block = [&](int kb, int b) __attribute__((always_inline)) {
+            uint32_t ka[NKS];
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                ka[ks] = kb0[ks] + (uint32_t)((kb % F5_KST) * TILE);
+                asm("; lds address" : "+v"(ka[ks]));
+            }
+            auto kread = [&](int f) __attribute__((always_inline)) -> f16x8 {   // f = 2 ks + kt
+                return *(const lds_f16x8*)(uintptr_t)(ka[f >> 1] + (uint32_t)((f & 1) * 32 * RB));
+            };
+            f16x8 fr[F5_PF];
+#pragma unroll
+            for (int f = 0; f < F5_PF; ++f) fr[f] = kread(f);
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {   // MFMA i: fragment f = i / 2 (ks = f / 2, kt = f % 2), qh = i % 2
+                const int f = i >> 1, qh = i & 1, ks = f >> 1, kt = f & 1;
+                st[kt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[f % F5_PF], qf[qh][ks],
+                                                                    ks == 0 ? f32x16{} : st[kt][qh], 0, 0, 0);
+                if (qh == 1 && f + F5_PF < 16) fr[f % F5_PF] = kread(f + F5_PF);
+            }
+            // mask: causal key > query (the diagonal block and any past it); else keys >= S
+            if (CAUSAL ? kb >= last : (kb + 1) * F5_BK > p.S) {
+                int dv = CAUSAL ? kb * F5_BK - q0 + 4 * h - r32 : kb * F5_BK + 4 * h - p.S;
+                asm volatile("; mask" : "+v"(dv));
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            const int kr = 32 * kt + 8 * (r >> 2) + (r & 3);
+                            const bool off = CAUSAL ? dv > 32 * qh - kr : dv >= -kr;
+                            st[kt][qh][r] = off ? -INFINITY : st[kt][qh][r];
+                        }
+            }
+            float mx[2];
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh) {
+                float v = -INFINITY;
+#pragma unroll
+                for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) v = fmaxf(v, st[kt][qh][r]);
+                float a, bb2;
+                f5_xor32_pair(v, a, bb2);
+                mx[qh] = fmaxf(a, bb2) * c;
+            }
+            const bool rescale =
+                __builtin_amdgcn_ballot_w64(mx[0] > m_run[0] + F3_RESCALE || mx[1] > m_run[1] + F3_RESCALE) != 0;
+            float alpha[2];
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh) {
+                const float m_new = rescale ? fmaxf(m_run[qh], mx[qh]) : m_run[qh];
+                alpha[qh] = __builtin_amdgcn_exp2f(m_run[qh] - m_new);
+                m_run[qh] = m_new;
+            }
+            if (rescale) {
+                if (h == 0) {
+                    abuf[b][pr][r32] = alpha[0];
+                    abuf[b][pr][32 + r32] = alpha[1];
+                }
+            }
+            if (lane == 0) fbuf[b][pr] = rescale ? 1 : 0;
+            // P = exp2(s c - m) in fp16 (RNE), stored as the output wavefront's B operands
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int qh = 0; qh < 2; ++qh) {
+                        f5_u32x4 u;
+                        const float mneg = -m_run[qh];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const int r0 = 8 * ks + 2 * k;
+                            const float e0 = __builtin_amdgcn_exp2f(fmaf(st[kt][qh][r0], c, mneg));
+                            const float e1 = __builtin_amdgcn_exp2f(fmaf(st[kt][qh][r0 + 1], c, mneg));
+                            const f5_h2 hv = {(_Float16)e0, (_Float16)e1};
+                            u[k] = __builtin_bit_cast(uint32_t, hv);
+                        }
+                        *(__attribute__((address_space(3))) f5_u32x4*)(uintptr_t)paddr(b, kt, ks, qh) = u;
+                    }
+        };
+
+        __syncthreads();                         // K_0 .. K_2, V_0 in LDS
+        block(0, 0);
+        __syncthreads();                         // P_0 published
+        for (int j = 0; j < nkb; ++j) {
+            if (j + 1 <= last) block(j + 1, (j + 1) & 1);
+            __syncthreads();
+        }
+    } else {
+        // ================= output wavefront =================
+        // V^T fragment (dt, kk): two transposing reads at keys kk + 4 h + jj and + 8
+        uint32_t vb0[NDT];
+        {
+            const int jj = (lane & 15) >> 2, q = lane & 3, dh = (lane >> 4) & 1;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                vb0[dt] = f3_lds_addr(&vbuf[0][0]) +
+                          (uint32_t)((4 * h + jj) * RB + (((4 * dt + 2 * dh + (q >> 1)) ^ (4 * jj)) << 4) + ((q & 1) << 3));
+        }
+        f32x16 o[NDT][2];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[dt][qh][r] = 0.f;
+        float l_run[2] = {0.f, 0.f};             // this lane's partial row sums of P
+        const f5_h2 ones = {(_Float16)1.f, (_Float16)1.f};
+
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();                         // K_0 .. K_2, V_0 in LDS
+        __syncthreads();                         // P_0 published
+        for (int j = 0; j < nkb; ++j) {
+            const int b = j & 1;
+            // K_{j+3} into K_j's stage and V_{j+1} into V_{j-1}'s (both read in iteration j - 1)
+#pragma unroll
+            for (int i = 0; i < DPT; ++i) dma1(true, j + 3, i);
+#pragma unroll
+            for (int i = 0; i < DPT; ++i) dma1(false, j + 1, i);
+            if (j <= last) {
+                if (j > 0 && fbuf[b][pr] != 0) {   // the maximum moved at block j: O *= alpha
+                    const float a0 = abuf[b][pr][r32], a1 = abuf[b][pr][32 + r32];
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            o[dt][0][r] *= a0;
+                            o[dt][1][r] *= a1;
+                        }
+                    l_run[0] *= a0;
+                    l_run[1] *= a1;
+                }
+                uint32_t va[NDT];
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    va[dt] = vb0[dt] + (uint32_t)((j % F5_VST) * TILE);
+                    asm("; lds address" : "+v"(va[dt]));
+                }
+                auto vread = [&](int f) __attribute__((always_inline)) -> f16x8 {   // f = 4 kk + dt
+                    const int kk = 16 * (f >> 2), dt = f & 3;
+                    const f3_s16x4 lo =
+                        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(va[dt] + (uint32_t)(kk * RB)));
+                    const f3_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(uintptr_t)(va[dt] + (uint32_t)((kk + 8) * RB)));
+                    return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                };
+                auto pread = [&](int kk, int qh) __attribute__((always_inline)) -> f16x8 {
+                    return *(const lds_f16x8*)(uintptr_t)paddr(b, kk >> 1, kk & 1, qh);
+                };
+                f16x8 fr[F5_PF];
+                f16x8 pp[2][2];   // [kk % 2][qh]
+#pragma unroll
+                for (int f = 0; f < F5_PF; ++f) fr[f] = vread(f);
+                pp[0][0] = pread(0, 0);
+                pp[0][1] = pread(0, 1);
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {   // MFMA i: V fragment f = i / 2 (kk = f / 4, dt = f % 4), qh = i % 2
+                    const int f = i >> 1, qh = i & 1, kk = f >> 2, dt = f & 3;
+                    if (i % 8 == 0 && kk < 3) {   // the next key step's P fragments
+                        pp[(kk + 1) & 1][0] = pread(kk + 1, 0);
+                        pp[(kk + 1) & 1][1] = pread(kk + 1, 1);
+                    }
+                    if (i % 8 == 4) {   // row sums of this key step's P (fp16 values, fp32 sum)
+#pragma unroll
+                        for (int qq = 0; qq < 2; ++qq)
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                l_run[qq] = __builtin_amdgcn_fdot2(f5_h2{pp[kk & 1][qq][2 * e], pp[kk & 1][qq][2 * e + 1]},
+                                                                   ones, l_run[qq], false);
+                    }
+                    o[dt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[f % F5_PF], pp[kk & 1][qh], o[dt][qh], 0, 0,
+                                                                       0);
+                    if (qh == 1 && f + F5_PF < 16) fr[f % F5_PF] = vread(f + F5_PF);
+                }
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K_{j+3}, V_{j+1} landed
+            __syncthreads();
+        }
+        // ---- O / L, fp16.  o[dt][qh] register r: d = 32 dt + 8 (r / 4) + 4 h + r % 4 of query q0 + 32 qh + r32.
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+            const int q = q0 + 32 * qh + r32;
+            float la, lb;
+            f5_xor32_pair(l_run[qh], la, lb);
+            const float inv = 1.f / (la + lb);
+            if (q >= p.S) continue;
+            f16* orow = Ob + (int64_t)q * p.osl;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int g4 = 0; g4 < 4; ++g4) {
+                    const int d = 32 * dt + 8 * g4 + 4 * h;
+                    f16x4 v = {(f16)(o[dt][qh][4 * g4 + 0] * inv), (f16)(o[dt][qh][4 * g4 + 1] * inv),
+                               (f16)(o[dt][qh][4 * g4 + 2] * inv), (f16)(o[dt][qh][4 * g4 + 3] * inv)};
+                    *reinterpret_cast<f16x4*>(orow + d) = v;
+                }
+        }
+    }
+}
+
 // Any D <= 256, any S: one thread per query row, online softmax in fp32 over every
 // key (the clamped/ragged path; not the fast one).
 __global__ void flash_generic_kernel(FaParams p, int D) {
@@ -746,6 +1096,17 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     const bool fast = lay_ok && D == FA_D && S % FA_BQ == 0 && blocks <= 0x7fffffff;
     const int64_t blocks3 = ((S + F3_BQ - 1) / F3_BQ) * H * B;
     const bool fast3 = lay_ok && scale > 0.f && S * strides[1] * 2 < ((int64_t)1 << 31) && blocks3 <= 0x7fffffff;
+    const int64_t blocks5 = ((S + F5_BQ - 1) / F5_BQ) * H * B;
+    const char* sel = getenv("LAVA_HIP_ATTN_KERNEL");
+    const bool fast5 = fast3 && D == FA_D && blocks5 <= 0x7fffffff && !(sel && sel[0] == '3');
+    if (fast5) {
+        if (p.causal)
+            hipLaunchKernelGGL((flash_fwd5_kernel<true>), dim3((unsigned)blocks5), dim3(128 * F5_PAIRS), 0, s, p);
+        else
+            hipLaunchKernelGGL((flash_fwd5_kernel<false>), dim3((unsigned)blocks5), dim3(128 * F5_PAIRS), 0, s, p);
+        LAVA_LAUNCH_CHECK("flash_fwd5_kernel");
+        return LAVA_HIP_OK;
+    }
     if (fast3) {
         const dim3 grid((unsigned)blocks3);
         if (D == 64) {
