@@ -7,7 +7,16 @@
 //   P = exp(S - M); O = O * exp(Mold - M) + P V; L = L * exp(Mold - M) + rowsum(P)
 // and finally O / L, converted to fp16 (RNE).
 //
-// CDNA4 formulation (one wavefront = 32 queries, 4 wavefronts = 128 queries):
+// Kernels (the dispatcher at the end of the file picks one):
+//  * flash_fwd5_kernel -- D = 128, the headline shape: on each SIMD a score
+//    wavefront and an output wavefront share 64 queries (described at the kernel);
+//  * flash_fwd3_kernel -- D = 64 (and D = 128 on request): ping-pong pairs of
+//    32-query wavefronts;
+//  * flash_fwd_kernel -- the first form, described next (kept for scale <= 0);
+//  * flash_generic_kernel -- any D <= 256, one thread per query.
+//
+// CDNA4 formulation of the first form (one wavefront = 32 queries, 4 wavefronts =
+// 128 queries):
 //  * everything is computed transposed, S^T = K Q^T and O^T = V^T P^T, with the
 //    32x32x16 fp16 MFMA.  In that form the accumulator lane owns ONE query
 //    (lane % 32; lanes l and l ^ 32 share it) and holds that query's scores for
@@ -26,7 +35,7 @@
 //    that lies entirely above its 32 queries;
 //  * workgroups are ordered XCD by XCD so that all query blocks of one (batch,
 //    head) run on one XCD and share its K and V through that XCD's L2; causal:
-//    longest query blocks first across the XCD's heads (fa_order).
+//    longest query blocks first across groups of the XCD's heads (fa_order).
 #include <hip/hip_runtime.h>
 
 #include <cstdlib>
@@ -61,17 +70,22 @@ struct FaParams {
 // over the 8 XCDs (blockIdx % 8).  Non-causal: every block costs the same, and each
 // XCD takes a contiguous range of (head, block) pairs, so one head's K and V stay in
 // one XCD's L2.  Causal: query block qb costs qb + 1 key blocks, so each XCD takes
-// whole heads (when 8 divides B * H) and runs their heaviest blocks first, then the
-// next lighter ones -- longest first across heads, so that the dispatcher hands each
-// freed CU the heaviest block left and the light ones fill the tail; without the
-// split by XCD, heavy first over all heads.
+// whole heads (when 8 divides B * H), in groups of 4 heads (when 4 divides the
+// XCD's count), and runs a group's heaviest blocks first, then the next lighter
+// ones: longest first across the group keeps the dispatch tail short, and one
+// group's K and V (8 MiB at D = 128, S = 4096) is what the XCD streams at a time.
+// Measured at B = 4, H = 32, S = 4096: groups of 4 heads 934-937 TFLOP/s, of all 16
+// of the XCD's heads 886-893, one head at a time 835.  Without the split by XCD,
+// heavy first over all heads.
 __device__ __forceinline__ void fa_order(int nqb, int nbh, bool causal, int& bh, int& qb) {
     const int bid = blockIdx.x;
     if (causal) {
         if ((nbh & 7) == 0) {
             const int h8 = nbh >> 3, local = bid >> 3;
-            qb = nqb - 1 - local / h8;
-            bh = (bid & 7) * h8 + local % h8;
+            const int G = (h8 & 3) == 0 ? 4 : h8;   // heads per group
+            const int grp = local / (G * nqb), r = local % (G * nqb);
+            qb = nqb - 1 - r / G;
+            bh = (bid & 7) * h8 + grp * G + r % G;
         } else {
             qb = nqb - 1 - bid / nbh;
             bh = bid % nbh;
@@ -1085,10 +1099,13 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     p.causal = causal != 0;
     hipStream_t s = as_stream(stream);
 
-    // D = 128 with 16-byte rows: the MFMA kernels.  flash_fwd3_kernel takes any S (a
-    // ragged last block of queries or keys is zero-filled and masked); the older
-    // 128-query kernel remains for scale <= 0 (the base-2 running maximum assumes
-    // a positive scale) with S a multiple of 128.
+    // D = 128 or 64 with 16-byte rows: the MFMA kernels.  D = 128 runs on
+    // flash_fwd5_kernel (score/output wavefront pairs), D = 64 on flash_fwd3_kernel
+    // (ping-pong wavefront pairs); both take any S (a ragged last block of queries or
+    // keys is zero-filled and masked) and a positive scale (the base-2 running maximum
+    // assumes one).  LAVA_HIP_ATTN_KERNEL=3 in the environment runs D = 128 on
+    // flash_fwd3_kernel as well (a comparison switch; both are parity-tested).  The
+    // older 128-query kernel remains for scale <= 0 with S a multiple of 128.
     bool lay_ok = D == FA_D || D == 64;
     for (int i = 1; i < 4; ++i) lay_ok = lay_ok && strides[i] % 8 == 0 && os[i] % 4 == 0;
     lay_ok = lay_ok && aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8);

@@ -97,6 +97,21 @@ def test_flash_fast_path(gpu, oracle, causal, E, L, H, B):
 
 
 @pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("L", [128, 777, 1024])
+def test_flash_pingpong_kernel_d128(gpu, oracle, causal, L, monkeypatch):
+    """D = 128 on the ping-pong kernel (LAVA_HIP_ATTN_KERNEL=3; the default D = 128 path
+    is the score/output split kernel), including a ragged S."""
+    lh = gpu
+    monkeypatch.setenv("LAVA_HIP_ATTN_KERNEL", "3")
+    announce(f"flash fwd ping-pong kernel D=128 S={L} causal={causal}")
+    Q, K, V = attn_inputs(lh, 128, L, 2, 1)
+    O = lh.HIPDeviceArray("f16", (128, L, 2, 1))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, causal=causal)
+    check_heads(oracle, Q, K, V, O, 1 / math.sqrt(128), causal, [(0, 0), (0, 1)], np.arange(L))
+
+
+@pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("L", [1, 7, 100, 255, 257, 1000, 1537])
 def test_flash_fast_ragged_s(gpu, oracle, causal, L):
     """D = 128 with S not a multiple of the 256-query block: the fast kernel zero-fills the
