@@ -96,6 +96,21 @@ def test_flash_fast_path(gpu, oracle, causal, E, L, H, B):
     check_heads(oracle, Q, K, V, O, 1 / math.sqrt(E), causal, heads, np.arange(L))
 
 
+@pytest.mark.parametrize("H,B", [(4, 2), (8, 3), (8, 4), (5, 1)])
+def test_flash_causal_block_orders(gpu, oracle, H, B):
+    """Causal workgroup orders: B * H = 8 (one head per XCD), 24 (three per XCD, no
+    4-head groups), 32 (groups of 4 heads), 5 (no split by XCD); every head's rows."""
+    lh = gpu
+    E, L = 128, 1024
+    announce(f"flash fwd causal order D={E} S={L} H={H} B={B}")
+    Q, K, V = attn_inputs(lh, E, L, H, B)
+    O = lh.HIPDeviceArray("f16", (E, L, H, B))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, causal=True)
+    heads = [(b, h) for b in range(B) for h in range(H)]
+    check_heads(oracle, Q, K, V, O, 1 / math.sqrt(E), True, heads, np.arange(0, L, 7))
+
+
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("L", [128, 777, 1024])
 def test_flash_pingpong_kernel_d128(gpu, oracle, causal, L, monkeypatch):
