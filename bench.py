@@ -12,9 +12,10 @@ before timing starts.
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|
                               gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|copy]
 
-A step is one kernel launch over the whole problem.  Kernel time comes from HIP
-events recorded on the launch stream around the K timed launches; wall time
-from a synchronised host clock around the same region.
+A step is one kernel launch over the whole problem.  Kernel time is the median
+of the K per-launch times that HIP events recorded on the launch stream give
+(`kernel_ms`; the mean is `kernel_ms_mean`); wall time comes from a synchronised
+host clock around the same region.
 """
 from __future__ import annotations
 
@@ -22,6 +23,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -39,20 +41,28 @@ PEAK_HBM_GBS = 8000.0
 
 
 def timed(lh, launch, steps: int, warmup: int, stream):
-    """Warm up, then time exactly `steps` launches: HIP events on `stream` give the
-    kernel time; a synchronised host clock gives the wall time."""
+    """Warm up, then time exactly `steps` launches.  An event recorded on `stream`
+    after every launch splits the region into per-launch kernel times; the median of
+    them is the kernel time (the mean is returned beside it).  A synchronised host
+    clock around the same region gives the wall time per step."""
     for _ in range(warmup):
         launch()
     lh.synchronize()
-    e0, e1 = lh.Event(), lh.Event()
+    ev = [lh.Event() for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    e0.record(stream)
-    for _ in range(steps):
+    ev[0].record(stream)
+    for i in range(steps):
         launch()
-    e1.record(stream)
+        ev[i + 1].record(stream)
     lh.synchronize()
     wall = time.perf_counter() - t0
-    return e0.elapsed_ms(e1) / steps, wall * 1e3 / steps
+    per = [ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)]
+    TIMED_MEAN_MS[0] = sum(per) / steps
+    return statistics.median(per), wall * 1e3 / steps
+
+
+# mean of the per-launch kernel times of the last timed() call (reported beside the median)
+TIMED_MEAN_MS = [0.0]
 
 
 def load_traffic(name: str):
@@ -229,18 +239,20 @@ def main():
 
     if args.workload in ("headline", "gemm_bf16"):
         flop, kms, wms = bench_gemm(lh, "bf16", 8192, K, W, stream, 1)
+        gemm_mean = TIMED_MEAN_MS[0]
         achieved = flop / (kms * 1e-3) / 1e12
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16",
                     "config": {"workload": "bf16 GEMM M=N=K=8192, A row-major, B column-major, fp32 accumulate "
                                            "and output (BASELINE configs[1])", "M": 8192, "N": 8192, "K": 8192},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(gemm_mean, 4),
                     "roofline": roofline("mfma", achieved, PEAK_BF16_TFLOPS, "TFLOP/s", load_traffic("gemm_bf16_8192"))})
         if args.workload == "headline":
             aflop, akms, awms = bench_attn(lh, K, W, stream)
             a_ach = aflop / (akms * 1e-3) / 1e12
             out["attn_fwd"] = {"value": round(aflop / (awms * 1e-3) / 1e12, 2), "unit": "TFLOP/s",
-                               "ms_per_step": round(awms, 4), "kernel_ms": round(akms, 4), "dtype": "f16",
+                               "ms_per_step": round(awms, 4), "kernel_ms": round(akms, 4),
+                               "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4), "dtype": "f16",
                                "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=128 fp16, "
                                                       "fp32 softmax state (BASELINE configs[4]); FLOP = "
                                                       "0.5*4*B*H*S^2*D"},
@@ -250,34 +262,36 @@ def main():
         flop, kms, wms = bench_gemm(lh, "bf16", 4096, K, W, stream, 1)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16", "config": {"workload": "bf16 GEMM 4096^3 A row-major B column-major"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_bf16_ragged":
         flop, kms, wms = bench_gemm(lh, "bf16", 0, K, W, stream, 1, shape=(8000, 8000, 8000))
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16", "config": {"workload": "bf16 GEMM M=N=K=8000 (not a tile multiple: "
                                                             "zero-clamped loads, bounds-checked store)"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "attn_d64":
         flop, kms, wms = bench_attn(lh, K, W, stream, D=64)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "f16", "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=64"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_bf16_nn":
         flop, kms, wms = bench_gemm_layout(lh, "bf16", 8192, 1 | 2 | 4, K, W, stream, 1)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16", "config": {"workload": "bf16 GEMM 8192^3, A and B row-major (B read through "
                                                             "transposing LDS reads)"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_cm2_f16":
         flop, kms, wms = bench_gemm_cm2(lh, 4096, K, W, stream, 1)
+        tile_mean = TIMED_MEAN_MS[0]
         _, vkms, _ = bench_gemm_cm2(lh, 4096, K, W, stream, 1, vocabulary=True)
+        TIMED_MEAN_MS[0] = tile_mean
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "f16", "config": {"workload": "coopmat2 GEMM 4096^3 fp16 -> fp16, A and B row-major"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "vocabulary_form_tflops": round(flop / (vkms * 1e-3) / 1e12, 2),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_ex_bf16":
@@ -285,20 +299,20 @@ def main():
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16", "config": {"workload": "bf16 GEMM 8192^3 with the fused epilogue: D bf16 = "
                                                             "gelu_tanh(A*B + bias[row] + residual), bias and residual fp32"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "attn":
         flop, kms, wms = bench_attn(lh, K, W, stream)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "f16", "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=128"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s",
                                          load_traffic("flash_fwd_causal"))})
     elif args.workload == "gemm_i8":
         flop, kms, wms = bench_gemm(lh, "i8", 4096, K, W, stream, 2)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "int8", "config": {"workload": "int8 GEMM 4096^3 -> int32 (BASELINE configs[2])"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_INT8_TOPS, "TOP/s",
                                          load_traffic("gemm_i8_4096"))})
     elif args.workload == "w8a16":
@@ -306,14 +320,14 @@ def main():
         out.update({"value": round(nbytes / (wms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 5),
                     "dtype": "f16", "config": {"workload": "W8A16 16x4096 . 4096x14336, per-column fp16 scale, "
                                                            "6 rotating weight copies (BASELINE configs[3])"},
-                    "kernel_ms": round(kms, 5),
+                    "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
                     "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s",
                                          load_traffic("w8a16"))})
     elif args.workload == "gemm_f16_256":
         flop, kms, wms = bench_gemm_layout(lh, "f16", 256, 3 | 4, K, W, stream, 0)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "f16", "config": {"workload": "fp16 GEMM 256^3, A and B row-major (BASELINE configs[0])"},
-                    "kernel_ms": round(kms, 5),
+                    "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
 
     elif args.workload == "copy":
@@ -330,7 +344,7 @@ def main():
         dp = lh.vocabulary.device_properties()
         out.update({"value": round(2 * nbytes / (kms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 4),
                     "dtype": "u8", "config": {"workload": "device copy of 1 GiB (read + write bytes)"},
-                    "kernel_ms": round(kms, 4),
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "device": {"cus": dp["cores"], "max_clock_mhz": dp["clock_khz"] / 1000.0,
                                "hbm_gib": round(dp["hbm_bytes"] / 2**30, 1), "l2_mib": round(dp["l2_bytes"] / 2**20, 1),
                                "derived_peak_bf16_tflops": round(dp["cores"] * dp["clock_khz"] * 1e3 * 4096 / 1e12, 1),

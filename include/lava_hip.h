@@ -171,6 +171,78 @@ int lava_hip_coopmat_reduce(const float* in, float* out, int tile, uint32_t mask
  * n must be a multiple of 256 (whole 16x16 tiles). */
 int lava_hip_coopmat_convert(const float* in, void* out, int out_dtype, int64_t n, void* stream);
 
+/* Matrix uses (src/vocabulary/matrix.jl:37-46) */
+#define LAVA_HIP_USE_MATRIX_A 0
+#define LAVA_HIP_USE_MATRIX_B 1
+#define LAVA_HIP_USE_ACCUMULATOR 2
+
+/* convert(CoopMatrix{To,T,T,Use}, m) of fp32 tile x tile Accumulators (tile 16 or 32,
+ * column-major with stride `tile`, ntiles consecutive tiles) to F16 or BF16 (RNE) *and*
+ * to another use: the result is stored column-major through the destination use's lane
+ * map, so `out` equals the narrowed input exactly when each element reached the lane
+ * that use assigns to it.  Replaces coopmat_convert with a use change (OpFConvert, then
+ * OpCooperativeMatrixConvertNV: src/device/coopmat_intrinsics.jl:222-247;
+ * src/compiler/spirv/coopmat.jl:783-824). */
+int lava_hip_coopmat_convert_use(const float* in, void* out, int out_dtype, int tile, int use, int64_t ntiles,
+                                 void* stream);
+
+/* Attention's second product on 16x16x16 tiles: D = convert(MatrixA f16, P) * V + 0, with P
+ * an fp32 Accumulator and V an fp16 MatrixB, all column-major with stride 16, ntiles
+ * consecutive tiles (the P_A step of flash_attn_cm2, coopmat_intrinsics.jl:222-231). */
+int lava_hip_coopmat_convert_use_muladd_16x16x16(const float* P, const void* V, float* D, int64_t ntiles,
+                                                 void* stream);
+
+/* D = mul(a, b) or add(a, b) (OpFMul / OpFAdd component-wise, src/compiler/spirv/coopmat.jl:
+ * 870-885; src/device/coopmat_intrinsics.jl:402-464) on fp32 tile x tile Accumulators loaded
+ * like coopmat_load: strides are element strides between columns (column-major) or rows
+ * (row-major); a stride of 0 loads the broadcast factor matrix (every column, or row,
+ * reading the same vector).  layout bits 0..2: A, B, D row-major; tile t at + t*tile_step. */
+#define LAVA_HIP_ELEMENTWISE_MUL 0
+#define LAVA_HIP_ELEMENTWISE_ADD 1
+int lava_hip_coopmat_elementwise(int op, int tile, const float* A, int64_t strideA, const float* B, int64_t strideB,
+                                 float* D, int64_t strideD, uint32_t layout, int64_t ntiles, int64_t tile_step,
+                                 void* stream);
+
+/* `accinit` then muladd on 16x16x16 tiles: c = add(bias at stride 0, residual at ldr);
+ * D = muladd(a, b, c).  A, B fp16 16x16 column-major (stride 16) at t*256; bias: 16 fp32
+ * per tile (one per row) at t*16; residual and D fp32 column-major, tile t at t*16*ld
+ * (src/device/coopmat_intrinsics.jl:435-464). */
+int lava_hip_coopmat_accinit_muladd_16x16x16(const void* A, const void* B, const float* bias, const float* residual,
+                                             int64_t ldr, float* D, int64_t ldd, int64_t ntiles, void* stream);
+
+/* The portable elementwise epilogue: for i in 0:coopmat_length(m)-1,
+ * m = coopmat_setcomp(m, i, act(coopmat_getcomp(m, i))) on fp32 tile x tile Accumulators
+ * (column-major, stride tile); *length_out (device memory) receives coopmat_length as the
+ * kernel saw it (src/device/coopmat_intrinsics.jl:322-400; coopmat.jl:826-868).
+ * act: LAVA_HIP_ACT_* below. */
+int lava_hip_coopmat_foreach_act(const float* in, float* out, int tile, int act, int64_t ntiles, int32_t* length_out,
+                                 void* stream);
+
+/* coopmat_length(CoopMatrix{dtype,rows,cols,use}) of the fragment types the kernels use:
+ * rows * cols / 64 components per lane (host query, no device needed). */
+int lava_hip_coopmat_length(int dtype, int rows, int cols, int use, int32_t* length_out);
+
+/* coopmat_perelement(f, m, ptr, base) with a pointer and an offset in `extras`
+ * (src/device/coopmat_intrinsics.jl:569-572, 595-628) on fp32 tile x tile Accumulators:
+ *   by_row == 0: f(r, c, e, s, b) = e * float(s[b + c]), s fp16 -- the W8A16 dequant scale;
+ *   by_row != 0: f(r, c, e, cs, b) = e * cs[b + r], cs fp32 -- attention's row rescale.
+ * Tile t passes b = base + t * tile. */
+int lava_hip_coopmat_perelement_scale(const float* in, float* out, int tile, int by_row, const void* factors,
+                                      int64_t base, int64_t ntiles, void* stream);
+
+/* The workgroup-scope table `wggran` (src/vocabulary/caps.jl:122-145): row i is
+ * out[4*i .. 4*i+4) = {invocations, M, N, K}, the multiples a workgroup-scope fp16 x fp16
+ * -> fp32 matrix must be at a workgroup of that many invocations. */
+int lava_hip_workgroup_shapes(int32_t* out, int max_rows, int* count);
+
+/* C (M x N, fp32) = A (M x K, fp16) * B (K x N, fp16) as ONE workgroup-scope matrix held by
+ * a single workgroup of `invocations` lanes (a row of lava_hip_workgroup_shapes); M, N, K
+ * must be positive multiples of that row's (M, N, K), at most 4096 each.  layout bits as
+ * for the GEMMs below (WorkgroupMatrix, src/vocabulary/coopmat.jl:36-92). */
+int lava_hip_coopmat_workgroup_gemm_f16(int invocations, const void* A, const void* B, float* C, int64_t M, int64_t N,
+                                        int64_t K, int64_t lda, int64_t ldb, int64_t ldc, uint32_t layout,
+                                        void* stream);
+
 /* y[i] = dot4x8(a[i], b[i]) (src/vocabulary/vocabulary.jl:31-35). */
 int lava_hip_dot4x8(const uint32_t* a, const uint32_t* b, int32_t* y, int64_t n, void* stream);
 

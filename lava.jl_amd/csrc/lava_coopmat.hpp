@@ -89,8 +89,8 @@ struct Layout<R, K, MatrixA> {
     static constexpr int groups = 64 / R;
     static constexpr int len = K / groups;
     static_assert(len * groups == K && len >= 1, "K must split over the lane groups");
-    __device__ static int row(int lane, int) { return lane % R; }
-    __device__ static int col(int lane, int j) { return (lane / R) * len + j; }
+    __host__ __device__ static constexpr int row(int lane, int) { return lane % R; }
+    __host__ __device__ static constexpr int col(int lane, int j) { return (lane / R) * len + j; }
 };
 
 template <int K, int C>
@@ -99,22 +99,22 @@ struct Layout<K, C, MatrixB> {
     static constexpr int groups = 64 / C;
     static constexpr int len = K / groups;
     static_assert(len * groups == K && len >= 1, "K must split over the lane groups");
-    __device__ static int row(int lane, int j) { return (lane / C) * len + j; }
-    __device__ static int col(int lane, int) { return lane % C; }
+    __host__ __device__ static constexpr int row(int lane, int j) { return (lane / C) * len + j; }
+    __host__ __device__ static constexpr int col(int lane, int) { return lane % C; }
 };
 
 template <>
 struct Layout<16, 16, Accumulator> {
     static constexpr int len = 4;
-    __device__ static int row(int lane, int j) { return 4 * (lane / 16) + j; }
-    __device__ static int col(int lane, int) { return lane % 16; }
+    __host__ __device__ static constexpr int row(int lane, int j) { return 4 * (lane / 16) + j; }
+    __host__ __device__ static constexpr int col(int lane, int) { return lane % 16; }
 };
 
 template <>
 struct Layout<32, 32, Accumulator> {
     static constexpr int len = 16;
-    __device__ static int row(int lane, int j) { return 8 * (j / 4) + 4 * (lane / 32) + (j % 4); }
-    __device__ static int col(int lane, int) { return lane % 32; }
+    __host__ __device__ static constexpr int row(int lane, int j) { return 8 * (j / 4) + 4 * (lane / 32) + (j % 4); }
+    __host__ __device__ static constexpr int col(int lane, int) { return lane % 32; }
 };
 
 // ---------------------------------------------------------------------------
@@ -127,7 +127,11 @@ struct Frag {
     T v[L::len];
 };
 
-// coopmat_length / getcomp / setcomp
+// coopmat_length / getcomp / setcomp.  length is a property of the type (how the
+// MFMA layout splits R x C over 64 lanes: R * C / 64 components per lane); the
+// component index is 0-based and names this lane's slot j of the layout above.
+template <typename FragT>
+__host__ __device__ __forceinline__ constexpr int length() { return FragT::len; }
 template <typename T, int R, int C, Use U>
 __device__ __forceinline__ constexpr int length(const Frag<T, R, C, U>&) { return Frag<T, R, C, U>::len; }
 template <typename T, int R, int C, Use U>
@@ -140,14 +144,6 @@ __device__ __forceinline__ FragT zero() {
     FragT m;
 #pragma unroll
     for (int j = 0; j < FragT::len; ++j) m.v[j] = 0;
-    return m;
-}
-
-template <typename FragT, typename T>
-__device__ __forceinline__ FragT fill(T x) {
-    FragT m;
-#pragma unroll
-    for (int j = 0; j < FragT::len; ++j) m.v[j] = x;
     return m;
 }
 
@@ -196,7 +192,60 @@ __device__ __forceinline__ Frag<To, R, C, U> convert(const Frag<T, R, C, U>& m) 
     return o;
 }
 
-// coopmat_mul / coopmat_add
+// Whether two uses of an R x C tile put every element in the same lane and slot.
+// True for a 16 x 16 Accumulator and a 16 x 16 MatrixB (K = 16): both hold column
+// lane % 16, rows 4 (lane / 16) + j.
+template <int R, int C, Use U1, Use U2>
+__host__ __device__ constexpr bool same_lane_map() {
+    using L1 = Layout<R, C, U1>;
+    using L2 = Layout<R, C, U2>;
+    if (L1::len != L2::len) return false;
+    for (int lane = 0; lane < 64; ++lane)
+        for (int j = 0; j < L1::len; ++j)
+            if (L1::row(lane, j) != L2::row(lane, j) || L1::col(lane, j) != L2::col(lane, j)) return false;
+    return true;
+}
+
+// LDS traffic of one wavefront is performed in issue order; the fence (lgkmcnt(0)
+// and a compiler barrier) orders this lane's LDS stores before the other lanes'
+// loads that follow.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// coopmat_convert with a change of use, e.g. an fp32 Accumulator to an fp16 MatrixA
+// (the P operand of attention's second product; OpFConvert then
+// OpCooperativeMatrixConvertNV, src/compiler/spirv/coopmat.jl:783-824;
+// src/device/coopmat_intrinsics.jl:222-247).  The component type is narrowed first
+// (RNE), at the source use, as the emitter does.  Where both uses map elements to
+// the same lanes the relayout is free; otherwise the tile goes through `scratch`, R x C
+// elements of LDS private to this wavefront: each lane stores its components at
+// (row, col) and loads the destination use's (row, col).
+template <typename To, Use UTo, typename T, int R, int C, Use U>
+__device__ __forceinline__ Frag<To, R, C, UTo> convert(const Frag<T, R, C, U>& m, To* scratch) {
+    Frag<To, R, C, UTo> o;
+    if constexpr (same_lane_map<R, C, U, UTo>()) {
+#pragma unroll
+        for (int j = 0; j < Frag<T, R, C, U>::len; ++j) o.v[j] = narrow<To>((float)m.v[j]);
+    } else {
+        using LS = Layout<R, C, U>;
+        using LD = Layout<R, C, UTo>;
+        const int lane = lane_id();
+        wave_lds_sync();   // earlier reads of scratch by other lanes are done
+#pragma unroll
+        for (int j = 0; j < LS::len; ++j) scratch[LS::row(lane, j) * C + LS::col(lane, j)] = narrow<To>((float)m.v[j]);
+        wave_lds_sync();
+#pragma unroll
+        for (int j = 0; j < LD::len; ++j) o.v[j] = scratch[LD::row(lane, j) * C + LD::col(lane, j)];
+    }
+    return o;
+}
+
+// coopmat_mul / coopmat_add: OpFMul / OpFAdd, component-wise
+// (src/compiler/spirv/coopmat.jl:870-885).  With one operand loaded at stride 0 (every
+// column reads the same vector) mul is the per-row rescale and add the bias of
+// `accinit` (src/device/coopmat_intrinsics.jl:402-464).
 template <typename T, int R, int C, Use U>
 __device__ __forceinline__ Frag<T, R, C, U> mul(const Frag<T, R, C, U>& a, const Frag<T, R, C, U>& b) {
     Frag<T, R, C, U> o;
@@ -373,36 +422,6 @@ __device__ __forceinline__ Frag<int32_t, 16, 16, Accumulator> mma(const Frag<int
     i32x4 cv = {c.v[0], c.v[1], c.v[2], c.v[3]};
     cv = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv, cv, 0, 0, 0);
     for (int j = 0; j < 4; ++j) c.v[j] = cv[j];
-    return c;
-}
-
-// uint8 x uint8 -> uint32 (the unsigned product, no signedness operands:
-// test/spirv/test_coopmat_int8.jl:71-98).  CDNA4's integer MFMA is signed, so the
-// unsigned tile product runs on the packed VALU dot instruction v_dot4_u32_u8:
-// each lane produces its accumulator elements from a row of A and a column of B
-// exchanged through the lane's register copies.
-template <int K>
-__device__ __forceinline__ Frag<uint32_t, 16, 16, Accumulator> mma_u8(const uint8_t* a_rows, int64_t lda_elems_row,
-                                                                      const uint8_t* b_cols, int64_t ldb_elems_col,
-                                                                      Frag<uint32_t, 16, 16, Accumulator> c) {
-    // a_rows: row r of A at a_rows + r*lda (k contiguous); b_cols: column n of B at
-    // b_cols + n*ldb (k contiguous).  Used by the tile-level vocabulary kernels only.
-    const int lane = lane_id();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = Layout<16, 16, Accumulator>::row(lane, j), n = Layout<16, 16, Accumulator>::col(lane, j);
-        uint32_t s = c.v[j];
-        for (int k = 0; k < K; k += 4) {
-            uint32_t x = 0, y = 0;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                x |= (uint32_t)a_rows[r * lda_elems_row + k + t] << (8 * t);
-                y |= (uint32_t)b_cols[n * ldb_elems_col + k + t] << (8 * t);
-            }
-            s = __builtin_amdgcn_udot4(x, y, s, false);
-        }
-        c.v[j] = s;
-    }
     return c;
 }
 

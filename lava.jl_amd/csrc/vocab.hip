@@ -7,6 +7,7 @@
 // checked element by element against the CPU oracle.
 #include <hip/hip_runtime.h>
 
+#include "gemm_common.hpp"
 #include "lava_coopmat.hpp"
 #include "lava_hip_internal.hpp"
 
@@ -139,6 +140,120 @@ __global__ void dot4x8_kernel(const uint32_t* a, const uint32_t* b, int32_t* y, 
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = dot4x8(a[i], b[i]);
 }
 
+
+// ---- convert with a change of use (src/device/coopmat_intrinsics.jl:222-247) ----------
+// The fp32 Accumulator tile becomes a To tile of use UTo and is stored through UTo's
+// lane map, so the stored matrix equals the narrowed input exactly when every element
+// reached the lane and slot UTo assigns to it.
+template <int T, typename To, Use UTo>
+__global__ void __launch_bounds__(64) convert_use_kernel(const float* in, To* out) {
+    __shared__ To scratch[T * T];
+    const int64_t base = (int64_t)blockIdx.x * T * T;
+    auto m = load<Frag<float, T, T, Accumulator>>(in + base, T, false);
+    store(out + base, T, false, convert<To, UTo>(m, scratch));
+}
+
+// Attention's second product: P (fp32 Accumulator) -> fp16 MatrixA, times V (MatrixB).
+__global__ void __launch_bounds__(64) convert_use_muladd_kernel(const float* P, const f16* V, float* D) {
+    __shared__ f16 scratch[256];
+    const int64_t base = (int64_t)blockIdx.x * 256;
+    auto p = load<Frag<float, 16, 16, Accumulator>>(P + base, 16, false);
+    auto pa = convert<f16, MatrixA>(p, scratch);
+    auto v = load<Frag<f16, 16, 16, MatrixB>>(V + base, 16, false);
+    store(D + base, 16, false, mma(pa, v, zero<Frag<float, 16, 16, Accumulator>>()));
+}
+
+// ---- coopmat_mul / coopmat_add (src/device/coopmat_intrinsics.jl:402-464) ------------
+// Operands are Accumulator loads; a stride of 0 makes every column (column-major) or
+// every row (row-major) read the same vector.
+template <int T, int OP>
+__global__ void __launch_bounds__(64) elementwise_kernel(const float* A, int64_t sa, const float* B, int64_t sb,
+                                                         float* D, int64_t sd, uint32_t layout, int64_t step) {
+    const int64_t t = blockIdx.x;
+    auto a = load<Frag<float, T, T, Accumulator>>(A + t * step, sa, (layout & 1u) != 0);
+    auto b = load<Frag<float, T, T, Accumulator>>(B + t * step, sb, (layout & 2u) != 0);
+    store(D + t * step, sd, (layout & 4u) != 0, OP == LAVA_HIP_ELEMENTWISE_MUL ? mul(a, b) : add(a, b));
+}
+
+// `accinit`: the accumulator starts from bias (stride-0 load, one value per row) plus the
+// residual (its own leading dimension), summed with coopmat_add, then muladd.
+__global__ void __launch_bounds__(64) accinit_muladd_kernel(const f16* A, const f16* B, const float* bias,
+                                                            const float* R, int64_t ldr, float* D, int64_t ldd) {
+    const int64_t t = blockIdx.x;
+    auto a = load<Frag<f16, 16, 16, MatrixA>>(A + t * 256, 16, false);
+    auto b = load<Frag<f16, 16, 16, MatrixB>>(B + t * 256, 16, false);
+    auto bias0 = load<Frag<float, 16, 16, Accumulator>>(bias + t * 16, 0, false);
+    auto res = load<Frag<float, 16, 16, Accumulator>>(R + t * 16 * ldr, ldr, false);
+    store(D + t * 16 * ldd, ldd, false, mma(a, b, add(bias0, res)));
+}
+
+// ---- the portable elementwise epilogue: for i in 0:length-1, setcomp(m, i, f(getcomp(m, i)))
+// (src/device/coopmat_intrinsics.jl:322-400) -----------------------------------------------
+template <int T, int ACT>
+__global__ void __launch_bounds__(64) foreach_act_kernel(const float* in, float* out, int32_t* len_out) {
+    const int64_t base = (int64_t)blockIdx.x * T * T;
+    auto m = load<Frag<float, T, T, Accumulator>>(in + base, T, false);
+    const int n = length(m);
+    for (int i = 0; i < n; ++i) m = setcomp(m, i, epi_act_c<ACT>(getcomp(m, i)));
+    store(out + base, T, false, m);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *len_out = n;
+}
+
+// ---- coopmat_perelement(f, m, extras...) with a pointer and an offset in extras
+// (src/device/coopmat_intrinsics.jl:569-572): the W8A16 dequant e * s[base + col] and
+// attention's rescale e * cs[base + row] ------------------------------------------------------
+struct ScaleByColumn {
+    __device__ float operator()(uint32_t, uint32_t col, float e, const f16* s, uint32_t base) const {
+        return e * (float)s[base + col];
+    }
+};
+struct ScaleByRow {
+    __device__ float operator()(uint32_t row, uint32_t, float e, const float* cs, uint32_t base) const {
+        return e * cs[base + row];
+    }
+};
+
+template <int T, bool BY_ROW>
+__global__ void __launch_bounds__(64) perelement_scale_kernel(const float* in, float* out, const void* factors,
+                                                              uint32_t base) {
+    const int64_t off = (int64_t)blockIdx.x * T * T;
+    auto m = load<Frag<float, T, T, Accumulator>>(in + off, T, false);
+    const uint32_t tb = base + (uint32_t)blockIdx.x * T;
+    if constexpr (BY_ROW)
+        m = perelement(ScaleByRow{}, m, static_cast<const float*>(factors), tb);
+    else
+        m = perelement(ScaleByColumn{}, m, static_cast<const f16*>(factors), tb);
+    store(out + off, T, false, m);
+}
+
+// ---- workgroup-scope matrices -----------------------------------------------------------
+// A workgroup-scope matrix at NT invocations is held by its NT / 64 wavefronts, arranged
+// WM x WN, wavefront (wm, wn) holding the 16 x 16 tiles (i, j) with i % WM == wm and
+// j % WN == wn; K advances in steps of the 16x16x16 instruction.  Its (M, N, K) must be
+// multiples of (16 WM, 16 WN, 16): the rows of the `wggran` table (caps.jl:122-145).
+struct WgShape {
+    int nt, wm, wn;
+};
+constexpr WgShape kWgShapes[] = {{64, 1, 1}, {128, 2, 1}, {256, 2, 2}, {512, 4, 2}, {1024, 4, 4}};
+
+template <int WM, int WN>
+__global__ void __launch_bounds__(WM * WN * 64) workgroup_gemm_kernel(const f16* A, const f16* B, float* C, int M,
+                                                                      int N, int K, int64_t lda, int64_t ldb,
+                                                                      int64_t ldc, uint32_t layout) {
+    const int w = threadIdx.x >> 6, wm = w / WN, wn = w % WN;
+    const bool arow = layout & 1u, brow = layout & 2u, crow = layout & 4u;
+    for (int i = wm; i < M / 16; i += WM)
+        for (int j = wn; j < N / 16; j += WN) {
+            auto acc = zero<Frag<float, 16, 16, Accumulator>>();
+            for (int k = 0; k < K / 16; ++k) {
+                auto a = load<Frag<f16, 16, 16, MatrixA>>(A + tile_index(16 * i, 16 * k, lda, arow), lda, arow);
+                auto b = load<Frag<f16, 16, 16, MatrixB>>(B + tile_index(16 * k, 16 * j, ldb, brow), ldb, brow);
+                acc = mma(a, b, acc);
+            }
+            store(C + tile_index(16 * i, 16 * j, ldc, crow), ldc, crow, acc);
+        }
+}
+
 static size_t dtype_size(int dt) {
     switch (dt) {
     case LAVA_HIP_F16:
@@ -267,6 +382,223 @@ int lava_hip_coopmat_convert(const float* in, void* out, int out_dtype, int64_t 
     else
         hipLaunchKernelGGL(convert_kernel<bf16>, dim3(g), dim3(64), 0, as_stream(stream), in, (bf16*)out);
     LAVA_LAUNCH_CHECK("convert_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_convert_use(const float* in, void* out, int out_dtype, int tile, int use, int64_t ntiles,
+                                 void* stream) {
+    LAVA_ARG(out_dtype == LAVA_HIP_F16 || out_dtype == LAVA_HIP_BF16, "coopmat_convert_use: dtype %d is not F16 or BF16",
+             out_dtype);
+    LAVA_ARG(tile == 16 || tile == 32, "coopmat_convert_use: tile = %d is not 16 or 32", tile);
+    LAVA_ARG(use == LAVA_HIP_USE_MATRIX_A || use == LAVA_HIP_USE_MATRIX_B || use == LAVA_HIP_USE_ACCUMULATOR,
+             "coopmat_convert_use: use %d is not MatrixA, MatrixB or Accumulator", use);
+    LAVA_ARG(ntiles >= 0 && ntiles <= 0x7fffffff, "coopmat_convert_use: ntiles out of range");
+    if (ntiles == 0) return LAVA_HIP_OK;
+    LAVA_ARG(in && out, "coopmat_convert_use: null pointer");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    const dim3 g((unsigned)ntiles);
+    hipStream_t s = as_stream(stream);
+#define LAVA_CONVERT_USE(T, TO)                                                                                     \
+    do {                                                                                                            \
+        if (use == LAVA_HIP_USE_MATRIX_A)                                                                           \
+            hipLaunchKernelGGL((convert_use_kernel<T, TO, MatrixA>), g, dim3(64), 0, s, in, (TO*)out);             \
+        else if (use == LAVA_HIP_USE_MATRIX_B)                                                                      \
+            hipLaunchKernelGGL((convert_use_kernel<T, TO, MatrixB>), g, dim3(64), 0, s, in, (TO*)out);             \
+        else                                                                                                        \
+            hipLaunchKernelGGL((convert_use_kernel<T, TO, Accumulator>), g, dim3(64), 0, s, in, (TO*)out);         \
+    } while (0)
+    if (tile == 16 && out_dtype == LAVA_HIP_F16) LAVA_CONVERT_USE(16, lava::f16);
+    else if (tile == 16) LAVA_CONVERT_USE(16, bf16);
+    else if (out_dtype == LAVA_HIP_F16) LAVA_CONVERT_USE(32, lava::f16);
+    else LAVA_CONVERT_USE(32, bf16);
+#undef LAVA_CONVERT_USE
+    LAVA_LAUNCH_CHECK("convert_use_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_convert_use_muladd_16x16x16(const float* P, const void* V, float* D, int64_t ntiles,
+                                                 void* stream) {
+    LAVA_ARG(ntiles >= 0 && ntiles <= 0x7fffffff, "coopmat_convert_use_muladd: ntiles out of range");
+    if (ntiles == 0) return LAVA_HIP_OK;
+    LAVA_ARG(P && V && D, "coopmat_convert_use_muladd: null pointer");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    hipLaunchKernelGGL(convert_use_muladd_kernel, dim3((unsigned)ntiles), dim3(64), 0, as_stream(stream), P,
+                       (const lava::f16*)V, D);
+    LAVA_LAUNCH_CHECK("convert_use_muladd_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_elementwise(int op, int tile, const float* A, int64_t strideA, const float* B, int64_t strideB,
+                                 float* D, int64_t strideD, uint32_t layout, int64_t ntiles, int64_t tile_step,
+                                 void* stream) {
+    LAVA_ARG(op == LAVA_HIP_ELEMENTWISE_MUL || op == LAVA_HIP_ELEMENTWISE_ADD, "coopmat_elementwise: op %d unknown", op);
+    LAVA_ARG(tile == 16 || tile == 32, "coopmat_elementwise: tile = %d is not 16 or 32", tile);
+    LAVA_ARG(layout <= 7u, "coopmat_elementwise: layout %u has bits beyond A, B, D row-major", layout);
+    LAVA_ARG(ntiles >= 0 && ntiles <= 0x7fffffff, "coopmat_elementwise: ntiles out of range");
+    if (ntiles == 0) return LAVA_HIP_OK;
+    LAVA_ARG(A && B && D, "coopmat_elementwise: null pointer");
+    LAVA_ARG(strideA >= 0 && strideB >= 0 && strideD >= tile && tile_step >= 0,
+             "coopmat_elementwise: operand strides must be >= 0 (0 broadcasts), D's >= tile, tile_step >= 0");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    const dim3 g((unsigned)ntiles);
+    hipStream_t s = as_stream(stream);
+    if (tile == 16 && op == LAVA_HIP_ELEMENTWISE_MUL)
+        hipLaunchKernelGGL((elementwise_kernel<16, LAVA_HIP_ELEMENTWISE_MUL>), g, dim3(64), 0, s, A, strideA, B,
+                           strideB, D, strideD, layout, tile_step);
+    else if (tile == 16)
+        hipLaunchKernelGGL((elementwise_kernel<16, LAVA_HIP_ELEMENTWISE_ADD>), g, dim3(64), 0, s, A, strideA, B,
+                           strideB, D, strideD, layout, tile_step);
+    else if (op == LAVA_HIP_ELEMENTWISE_MUL)
+        hipLaunchKernelGGL((elementwise_kernel<32, LAVA_HIP_ELEMENTWISE_MUL>), g, dim3(64), 0, s, A, strideA, B,
+                           strideB, D, strideD, layout, tile_step);
+    else
+        hipLaunchKernelGGL((elementwise_kernel<32, LAVA_HIP_ELEMENTWISE_ADD>), g, dim3(64), 0, s, A, strideA, B,
+                           strideB, D, strideD, layout, tile_step);
+    LAVA_LAUNCH_CHECK("elementwise_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_accinit_muladd_16x16x16(const void* A, const void* B, const float* bias, const float* residual,
+                                             int64_t ldr, float* D, int64_t ldd, int64_t ntiles, void* stream) {
+    LAVA_ARG(ntiles >= 0 && ntiles <= 0x7fffffff, "coopmat_accinit_muladd: ntiles out of range");
+    if (ntiles == 0) return LAVA_HIP_OK;
+    LAVA_ARG(A && B && bias && residual && D, "coopmat_accinit_muladd: null pointer");
+    LAVA_ARG(ldr >= 16 && ldd >= 16, "coopmat_accinit_muladd: ldr and ldd must be >= 16");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    hipLaunchKernelGGL(accinit_muladd_kernel, dim3((unsigned)ntiles), dim3(64), 0, as_stream(stream),
+                       (const lava::f16*)A, (const lava::f16*)B, bias, residual, ldr, D, ldd);
+    LAVA_LAUNCH_CHECK("accinit_muladd_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_foreach_act(const float* in, float* out, int tile, int act, int64_t ntiles, int32_t* length_out,
+                                 void* stream) {
+    LAVA_ARG(tile == 16 || tile == 32, "coopmat_foreach_act: tile = %d is not 16 or 32", tile);
+    LAVA_ARG(act >= LAVA_HIP_ACT_NONE && act <= LAVA_HIP_ACT_GELU_ERF, "coopmat_foreach_act: act %d unknown", act);
+    LAVA_ARG(ntiles >= 1 && ntiles <= 0x7fffffff, "coopmat_foreach_act: ntiles out of range (>= 1)");
+    LAVA_ARG(in && out && length_out, "coopmat_foreach_act: null pointer");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    const dim3 g((unsigned)ntiles);
+    hipStream_t s = as_stream(stream);
+#define LAVA_FOREACH(T)                                                                                          \
+    do {                                                                                                         \
+        switch (act) {                                                                                           \
+        case LAVA_HIP_ACT_RELU:                                                                                  \
+            hipLaunchKernelGGL((foreach_act_kernel<T, EPI_RELU>), g, dim3(64), 0, s, in, out, length_out);       \
+            break;                                                                                               \
+        case LAVA_HIP_ACT_GELU_TANH:                                                                             \
+            hipLaunchKernelGGL((foreach_act_kernel<T, EPI_GELU_TANH>), g, dim3(64), 0, s, in, out, length_out);  \
+            break;                                                                                               \
+        case LAVA_HIP_ACT_GELU_ERF:                                                                              \
+            hipLaunchKernelGGL((foreach_act_kernel<T, EPI_GELU_ERF>), g, dim3(64), 0, s, in, out, length_out);   \
+            break;                                                                                               \
+        default: hipLaunchKernelGGL((foreach_act_kernel<T, EPI_NONE>), g, dim3(64), 0, s, in, out, length_out); \
+        }                                                                                                        \
+    } while (0)
+    if (tile == 16) LAVA_FOREACH(16);
+    else LAVA_FOREACH(32);
+#undef LAVA_FOREACH
+    LAVA_LAUNCH_CHECK("foreach_act_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_length(int dtype, int rows, int cols, int use, int32_t* length_out) {
+    LAVA_ARG(length_out != nullptr, "coopmat_length: null output pointer");
+    (void)dtype;   // the component count depends on the shape and use only
+    int n = -1;
+    if (use == LAVA_HIP_USE_ACCUMULATOR) {
+        if (rows == 16 && cols == 16) n = length<Frag<float, 16, 16, Accumulator>>();
+        else if (rows == 32 && cols == 32) n = length<Frag<float, 32, 32, Accumulator>>();
+    } else if (use == LAVA_HIP_USE_MATRIX_A) {
+        if (rows == 16 && cols == 16) n = length<Frag<lava::f16, 16, 16, MatrixA>>();
+        else if (rows == 16 && cols == 32) n = length<Frag<lava::f16, 16, 32, MatrixA>>();
+        else if (rows == 32 && cols == 16) n = length<Frag<lava::f16, 32, 16, MatrixA>>();
+        else if (rows == 32 && cols == 32) n = length<Frag<lava::f16, 32, 32, MatrixA>>();
+        else if (rows == 16 && cols == 64) n = length<Frag<int8_t, 16, 64, MatrixA>>();
+    } else if (use == LAVA_HIP_USE_MATRIX_B) {
+        if (rows == 16 && cols == 16) n = length<Frag<lava::f16, 16, 16, MatrixB>>();
+        else if (rows == 32 && cols == 16) n = length<Frag<lava::f16, 32, 16, MatrixB>>();
+        else if (rows == 16 && cols == 32) n = length<Frag<lava::f16, 16, 32, MatrixB>>();
+        else if (rows == 32 && cols == 32) n = length<Frag<lava::f16, 32, 32, MatrixB>>();
+        else if (rows == 64 && cols == 16) n = length<Frag<int8_t, 64, 16, MatrixB>>();
+    }
+    LAVA_REQUIRE(n > 0, LAVA_HIP_ERR_UNSUPPORTED, "coopmat_length: no %d x %d fragment of use %d", rows, cols, use);
+    *length_out = n;
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_perelement_scale(const float* in, float* out, int tile, int by_row, const void* factors,
+                                      int64_t base, int64_t ntiles, void* stream) {
+    LAVA_ARG(tile == 16 || tile == 32, "coopmat_perelement_scale: tile = %d is not 16 or 32", tile);
+    LAVA_ARG(ntiles >= 0 && ntiles <= 0x7fffffff, "coopmat_perelement_scale: ntiles out of range");
+    if (ntiles == 0) return LAVA_HIP_OK;
+    LAVA_ARG(in && out && factors, "coopmat_perelement_scale: null pointer");
+    LAVA_ARG(base >= 0 && base + ntiles * tile <= 0xffffffffll, "coopmat_perelement_scale: base out of range");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    const dim3 g((unsigned)ntiles);
+    hipStream_t s = as_stream(stream);
+    const uint32_t b = (uint32_t)base;
+    if (tile == 16 && by_row) hipLaunchKernelGGL((perelement_scale_kernel<16, true>), g, dim3(64), 0, s, in, out, factors, b);
+    else if (tile == 16) hipLaunchKernelGGL((perelement_scale_kernel<16, false>), g, dim3(64), 0, s, in, out, factors, b);
+    else if (by_row) hipLaunchKernelGGL((perelement_scale_kernel<32, true>), g, dim3(64), 0, s, in, out, factors, b);
+    else hipLaunchKernelGGL((perelement_scale_kernel<32, false>), g, dim3(64), 0, s, in, out, factors, b);
+    LAVA_LAUNCH_CHECK("perelement_scale_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_workgroup_shapes(int32_t* out, int max_rows, int* count) {
+    LAVA_ARG(count != nullptr, "workgroup_shapes: null count pointer");
+    const int n = (int)(sizeof(kWgShapes) / sizeof(kWgShapes[0]));
+    *count = n;
+    if (out == nullptr) return LAVA_HIP_OK;
+    for (int i = 0; i < n && i < max_rows; ++i) {
+        out[4 * i + 0] = kWgShapes[i].nt;
+        out[4 * i + 1] = 16 * kWgShapes[i].wm;
+        out[4 * i + 2] = 16 * kWgShapes[i].wn;
+        out[4 * i + 3] = 16;
+    }
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_workgroup_gemm_f16(int invocations, const void* A, const void* B, float* C, int64_t M, int64_t N,
+                                        int64_t K, int64_t lda, int64_t ldb, int64_t ldc, uint32_t layout,
+                                        void* stream) {
+    int wm = 0, wn = 0;
+    for (const WgShape& w : kWgShapes)
+        if (w.nt == invocations) { wm = w.wm; wn = w.wn; }
+    LAVA_REQUIRE(wm > 0, LAVA_HIP_ERR_UNSUPPORTED, "workgroup_gemm: no workgroup-scope matrix at %d invocations",
+                 invocations);
+    LAVA_ARG(layout <= 7u, "workgroup_gemm: layout %u has bits beyond A, B, C row-major", layout);
+    LAVA_ARG(M > 0 && N > 0 && K > 0 && M % (16 * wm) == 0 && N % (16 * wn) == 0 && K % 16 == 0,
+             "workgroup_gemm: (M, N, K) = (%lld, %lld, %lld) are not positive multiples of (%d, %d, 16) at %d invocations",
+             (long long)M, (long long)N, (long long)K, 16 * wm, 16 * wn, invocations);
+    LAVA_ARG(M <= 4096 && N <= 4096 && K <= 4096, "workgroup_gemm: one workgroup holds at most 4096 x 4096 x 4096");
+    const bool arow = layout & 1u, brow = layout & 2u, crow = layout & 4u;
+    LAVA_ARG(lda >= (arow ? K : M) && ldb >= (brow ? N : K) && ldc >= (crow ? N : M),
+             "workgroup_gemm: leading dimension too small");
+    LAVA_ARG(A && B && C, "workgroup_gemm: null pointer");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    const dim3 blk((unsigned)(64 * wm * wn));
+#define LAVA_WG(WM_, WN_)                                                                                        \
+    hipLaunchKernelGGL((workgroup_gemm_kernel<WM_, WN_>), dim3(1), blk, 0, s, (const lava::f16*)A,              \
+                       (const lava::f16*)B, C, (int)M, (int)N, (int)K, lda, ldb, ldc, layout)
+    switch (invocations) {
+    case 64: LAVA_WG(1, 1); break;
+    case 128: LAVA_WG(2, 1); break;
+    case 256: LAVA_WG(2, 2); break;
+    case 512: LAVA_WG(4, 2); break;
+    default: LAVA_WG(4, 4); break;
+    }
+#undef LAVA_WG
+    LAVA_LAUNCH_CHECK("workgroup_gemm_kernel");
     return LAVA_HIP_OK;
 }
 

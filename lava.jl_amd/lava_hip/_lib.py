@@ -25,6 +25,9 @@ A_ROWMAJOR, B_ROWMAJOR, C_ROWMAJOR = 1, 2, 4
 
 COMBINE_ADD, COMBINE_MAX, COMBINE_MIN = 0, 1, 2
 
+USE_MATRIX_A, USE_MATRIX_B, USE_ACCUMULATOR = 0, 1, 2
+ELEMENTWISE_MUL, ELEMENTWISE_ADD = 0, 1
+
 
 class LavaHIPError(RuntimeError):
     """A nonzero status from liblava_hip.so, with its thread-local message."""
@@ -85,6 +88,15 @@ PROTOTYPES: dict[str, tuple] = {
     "lava_hip_coopmat_reduce": (ci, [vp, vp, ci, u32, ci, i64, vp]),
     "lava_hip_coopmat_convert": (ci, [vp, vp, ci, i64, vp]),
     "lava_hip_dot4x8": (ci, [vp, vp, vp, i64, vp]),
+    "lava_hip_coopmat_convert_use": (ci, [vp, vp, ci, ci, ci, i64, vp]),
+    "lava_hip_coopmat_convert_use_muladd_16x16x16": (ci, [vp, vp, vp, i64, vp]),
+    "lava_hip_coopmat_elementwise": (ci, [ci, ci, vp, i64, vp, i64, vp, i64, u32, i64, i64, vp]),
+    "lava_hip_coopmat_accinit_muladd_16x16x16": (ci, [vp, vp, vp, vp, i64, vp, i64, i64, vp]),
+    "lava_hip_coopmat_foreach_act": (ci, [vp, vp, ci, ci, i64, vp, vp]),
+    "lava_hip_coopmat_length": (ci, [ci, ci, ci, ci, C.POINTER(C.c_int32)]),
+    "lava_hip_coopmat_perelement_scale": (ci, [vp, vp, ci, ci, vp, i64, i64, vp]),
+    "lava_hip_workgroup_shapes": (ci, [C.POINTER(C.c_int32), ci, C.POINTER(ci)]),
+    "lava_hip_coopmat_workgroup_gemm_f16": (ci, [ci, vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_gemm_f16_f32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_gemm_bf16_f32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_gemm_i8_i32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),

@@ -93,8 +93,12 @@ def gemm_ex(D: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray, bias: Optio
 def coopmat_gemm_tiles(C_: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray,
                        stream: Optional[int] = None) -> HIPDeviceArray:
     """The 16x16x16 vocabulary-tile GEMM of docs/src/device.md:81-88 (fp16 -> fp32)."""
+    if A.dtype != "f16" or B.dtype != "f16" or C_.dtype != "f32":
+        raise ValueError(f"the tile GEMM is f16 x f16 -> f32 (got {A.dtype}, {B.dtype}, {C_.dtype})")
     M, K = A.dims
-    _, N = B.dims
+    K2, N = B.dims
+    if K2 != K or C_.dims != (M, N):
+        raise ValueError(f"shape mismatch: A {A.dims}, B {B.dims}, C {C_.dims}")
     layout = (1 if A.order == "C" else 0) | (2 if B.order == "C" else 0) | (4 if C_.order == "C" else 0)
     _lib.call("lava_hip_coopmat_gemm_f16_tiles", A.ptr, B.ptr, C_.ptr, M, N, K, _ld(A), _ld(B), _ld(C_), layout,
               stream)
@@ -173,6 +177,77 @@ def coopmat_reduce(inp: int, out: int, tile: int, mask: int, combine: str, ntile
 def coopmat_convert(inp: int, out: int, out_dtype: str, n: int, stream: Optional[int] = None) -> None:
     code = {"f16": _lib.F16, "bf16": _lib.BF16}[out_dtype]
     _lib.call("lava_hip_coopmat_convert", inp, out, code, n, stream)
+
+
+_USES = {"MatrixA": _lib.USE_MATRIX_A, "MatrixB": _lib.USE_MATRIX_B, "Accumulator": _lib.USE_ACCUMULATOR}
+
+
+def coopmat_convert_use(inp: int, out: int, out_dtype: str, tile: int, use: str, ntiles: int,
+                        stream: Optional[int] = None) -> None:
+    """convert(CoopMatrix{out_dtype,tile,tile,use}, m) of fp32 Accumulator tiles: narrowing
+    (RNE) and a change of use (coopmat_intrinsics.jl:222-247), stored through the new use's
+    lane map."""
+    code = {"f16": _lib.F16, "bf16": _lib.BF16}[out_dtype]
+    _lib.call("lava_hip_coopmat_convert_use", inp, out, code, tile, _USES[use], ntiles, stream)
+
+
+def coopmat_convert_use_muladd(P: int, V: int, D: int, ntiles: int, stream: Optional[int] = None) -> None:
+    """D = convert(MatrixA f16, P) * V on 16x16x16 tiles (attention's P_A step)."""
+    _lib.call("lava_hip_coopmat_convert_use_muladd_16x16x16", P, V, D, ntiles, stream)
+
+
+def coopmat_elementwise(op: str, tile: int, A: int, strideA: int, B: int, strideB: int, D: int, strideD: int,
+                        layout: int = 0, ntiles: int = 1, tile_step: int = 0, stream: Optional[int] = None) -> None:
+    """D = coopmat_mul(a, b) or coopmat_add(a, b); a stride of 0 loads a broadcast factor
+    matrix (coopmat_intrinsics.jl:402-464).  layout bits 0..2: A, B, D row-major."""
+    code = {"mul": _lib.ELEMENTWISE_MUL, "add": _lib.ELEMENTWISE_ADD}[op]
+    _lib.call("lava_hip_coopmat_elementwise", code, tile, A, strideA, B, strideB, D, strideD, layout, ntiles,
+              tile_step, stream)
+
+
+def coopmat_accinit_muladd(A: int, B: int, bias: int, residual: int, ldr: int, D: int, ldd: int, ntiles: int = 1,
+                           stream: Optional[int] = None) -> None:
+    """D = muladd(a, b, add(bias at stride 0, residual)) on 16x16x16 tiles (`accinit`)."""
+    _lib.call("lava_hip_coopmat_accinit_muladd_16x16x16", A, B, bias, residual, ldr, D, ldd, ntiles, stream)
+
+
+def coopmat_foreach_act(inp: int, out: int, tile: int, act: str, ntiles: int, length_out: int,
+                        stream: Optional[int] = None) -> None:
+    """for i in 0:length-1: setcomp(m, i, act(getcomp(m, i))) (coopmat_intrinsics.jl:322-400)."""
+    if act not in _ACTS:
+        raise ValueError(f"act must be one of {sorted(_ACTS)}")
+    _lib.call("lava_hip_coopmat_foreach_act", inp, out, tile, _ACTS[act], ntiles, length_out, stream)
+
+
+def coopmat_length(dtype: str, rows: int, cols: int, use: str) -> int:
+    """coopmat_length(CoopMatrix{dtype,rows,cols,use}): components per lane."""
+    codes = {"f16": _lib.F16, "bf16": _lib.BF16, "f32": _lib.F32, "i8": _lib.I8, "i32": _lib.I32}
+    n = C.c_int32()
+    _lib.call("lava_hip_coopmat_length", codes[dtype], rows, cols, _USES[use], C.byref(n))
+    return int(n.value)
+
+
+def coopmat_perelement_scale(inp: int, out: int, tile: int, by_row: bool, factors: int, base: int, ntiles: int,
+                             stream: Optional[int] = None) -> None:
+    """coopmat_perelement(f, m, ptr, base): e * s[base + col] (fp16 s, the W8A16 dequant) or
+    e * cs[base + row] (fp32 cs, the attention rescale) (coopmat_intrinsics.jl:569-628)."""
+    _lib.call("lava_hip_coopmat_perelement_scale", inp, out, tile, int(bool(by_row)), factors, base, ntiles, stream)
+
+
+def coopmat_workgroup_gemm(C_: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray, invocations: int,
+                           stream: Optional[int] = None) -> HIPDeviceArray:
+    """C = A * B as one workgroup-scope matrix held by a workgroup of `invocations` lanes;
+    (M, N, K) must be multiples of wggranularity(caps(), invocations)."""
+    if A.dtype != "f16" or B.dtype != "f16" or C_.dtype != "f32":
+        raise ValueError("workgroup GEMM is fp16 x fp16 -> fp32")
+    M, K = A.dims
+    K2, N = B.dims
+    if K2 != K or C_.dims != (M, N):
+        raise ValueError(f"shape mismatch: A {A.dims}, B {B.dims}, C {C_.dims}")
+    layout = (1 if A.order == "C" else 0) | (2 if B.order == "C" else 0) | (4 if C_.order == "C" else 0)
+    _lib.call("lava_hip_coopmat_workgroup_gemm_f16", invocations, A.ptr, B.ptr, C_.ptr, M, N, K, _ld(A), _ld(B),
+              _ld(C_), layout, stream)
+    return C_
 
 
 def dot4x8(a: int, b: int, y: int, n: int, stream: Optional[int] = None) -> None:

@@ -233,10 +233,23 @@ def library_shapes() -> tuple:
     return tuple(rows)
 
 
+def library_wggran() -> tuple:
+    """The workgroup-scope table compiled into liblava_hip.so, rows (invocations, M, N, K):
+    a workgroup of `invocations` lanes holds the matrix as invocations/64 wavefronts of
+    16 x 16 MFMA tiles (no GPU needed)."""
+    from . import _lib
+    n = C.c_int()
+    _lib.call("lava_hip_workgroup_shapes", None, 0, C.byref(n))
+    buf = (C.c_int32 * (4 * n.value))()
+    _lib.call("lava_hip_workgroup_shapes", buf, n.value, C.byref(n))
+    return tuple(tuple(int(x) for x in buf[4 * i:4 * i + 4]) for i in range(n.value))
+
+
 def caps() -> DeviceCaps:
-    """`caps(backend)` for the MI355X this process sees (needs a GPU)."""
+    """`caps(backend)` for the MI355X this process sees (needs a GPU): the device record
+    from hipDeviceProp, the MFMA shape table and the workgroup-scope table."""
     p = device_properties()
     return DeviceCaps(coopmat=bool(p["coopmat"]), tile=p["tile"], subgroup=p["subgroup"],
                       coopmatsubgroup=p["coopmatsubgroup"], sharedbudget=p["sharedbudget"],
                       workgrouplimit=p["workgrouplimit"], cores=p["cores"], warps=p["warps"],
-                      wggran=(), shapes=library_shapes())
+                      wggran=library_wggran(), shapes=library_shapes())

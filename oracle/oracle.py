@@ -231,6 +231,42 @@ def reduce_smear(m: np.ndarray, mask: int, combine: str) -> np.ndarray:
     return np.array(x)
 
 
+def load_tile(buf: np.ndarray, off: int, stride: int, rowmajor: bool, R: int, C: int) -> np.ndarray:
+    """coopmat_load of an R x C tile at 0-based element offset `off`: element (r, c) at
+    off + r*stride + c (RowMajor) or off + c*stride + r (ColumnMajor, the default); a
+    stride of 0 makes every column (ColumnMajor) or row (RowMajor) read the same vector
+    (src/compiler/spirv/coopmat.jl:664-744; src/device/coopmat_intrinsics.jl:57-75,
+    402-433)."""
+    r = np.arange(R)[:, None]
+    c = np.arange(C)[None, :]
+    idx = off + (r * stride + c if rowmajor else c * stride + r)
+    return np.asarray(buf)[idx]
+
+
+def store_tile(buf: np.ndarray, off: int, stride: int, rowmajor: bool, m: np.ndarray) -> np.ndarray:
+    """coopmat_store of tile m into a copy of buf (same addressing as load_tile)."""
+    out = np.array(buf, copy=True)
+    R, C = m.shape
+    r = np.arange(R)[:, None]
+    c = np.arange(C)[None, :]
+    out[off + (r * stride + c if rowmajor else c * stride + r)] = m
+    return out
+
+
+def scale_columns(m: np.ndarray, s: np.ndarray, base: int) -> np.ndarray:
+    """perelement f(r, c, e, s, base) = e * float(s[base + c]) in fp32: the W8A16 per-column
+    dequant through `extras` (src/device/coopmat_intrinsics.jl:569-572)."""
+    f = np.asarray(s, dtype=np.float32)[base:base + m.shape[1]]
+    return (np.asarray(m, dtype=np.float32) * f[None, :]).astype(np.float32)
+
+
+def scale_rows(m: np.ndarray, cs: np.ndarray, base: int) -> np.ndarray:
+    """perelement f(r, c, e, cs, base) = e * cs[base + r] in fp32: attention's rescale
+    `element * cs[base + row]` (src/device/coopmat_intrinsics.jl:569-572)."""
+    f = np.asarray(cs, dtype=np.float32)[base:base + m.shape[0]]
+    return (np.asarray(m, dtype=np.float32) * f[:, None]).astype(np.float32)
+
+
 # ---- GEMM epilogue ----------------------------------------------------------------------------
 def gelu_tanh(x: np.ndarray) -> np.ndarray:
     """0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))), fp64."""

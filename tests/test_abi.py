@@ -134,3 +134,45 @@ def test_python_errors_are_typed():
         lava_hip.gemm_raw("bf16", "f32", 16, 16, 16, -1, 1, 1, 1, 1, 1, 7)
     with pytest.raises(lava_hip.Unsupported):
         lava_hip.gemm_raw("f32", "f32", 16, 16, 16, 1, 1, 1, 1, 1, 1, 7)
+
+
+def test_vocabulary_queries_without_gpu():
+    """coopmat_length and the workgroup-scope table are host queries of the library."""
+    import lava_hip as lh
+    assert lh.coopmat_length("f32", 16, 16, "Accumulator") == 4
+    assert lh.coopmat_length("f32", 32, 32, "Accumulator") == 16
+    assert lh.coopmat_length("f16", 16, 32, "MatrixA") == 8
+    assert lh.coopmat_length("i8", 16, 64, "MatrixA") == 16
+    with pytest.raises(lh.Unsupported):
+        lh.coopmat_length("f16", 48, 16, "MatrixA")
+    rows = lh.library_wggran()
+    assert rows[0] == (64, 16, 16, 16)
+    for nt, m, n, k in rows:
+        # nt / 64 wavefronts of 16 x 16 tiles, K in steps of the 16x16x16 instruction
+        assert (m // 16) * (n // 16) * 64 == nt and k == 16
+    # coarsening: a larger workgroup never asks for smaller multiples
+    for a, b in zip(rows, rows[1:]):
+        assert b[0] > a[0] and b[1] >= a[1] and b[2] >= a[2]
+    c = lh.DeviceCaps(True, 16, 64, 64, 163840, 1024, 256, 32, wggran=rows)
+    assert lh.wggranularity(c, 512) == (64, 32, 16) and lh.wggranularity(c, 100) is None
+
+
+def test_vocabulary_entry_argument_errors():
+    import lava_hip as lh
+    L = lh.load()
+    st, msg = status_of("lava_hip_coopmat_convert_use", None, None, lh._lib.F16, 8, 0, 1, None)
+    assert st == lh._lib.ERR_INVALID_ARG and "tile" in msg
+    st, msg = status_of("lava_hip_coopmat_convert_use", None, None, lh._lib.F32, 16, 0, 1, None)
+    assert st == lh._lib.ERR_INVALID_ARG and "dtype" in msg
+    st, msg = status_of("lava_hip_coopmat_elementwise", 7, 16, None, 0, None, 0, None, 16, 0, 1, 0, None)
+    assert st == lh._lib.ERR_INVALID_ARG and "op" in msg
+    st, msg = status_of("lava_hip_coopmat_elementwise", 0, 16, 8, -1, 8, 0, 8, 16, 0, 1, 0, None)
+    assert st == lh._lib.ERR_INVALID_ARG and "stride" in msg
+    st, msg = status_of("lava_hip_coopmat_foreach_act", None, None, 16, 9, 1, None, None)
+    assert st == lh._lib.ERR_INVALID_ARG and "act" in msg
+    st, msg = status_of("lava_hip_coopmat_workgroup_gemm_f16", 96, None, None, None, 16, 16, 16, 16, 16, 16, 0, None)
+    assert st == lh._lib.ERR_UNSUPPORTED and "96" in msg
+    st, msg = status_of("lava_hip_coopmat_workgroup_gemm_f16", 256, 8, 8, 8, 48, 32, 16, 48, 16, 48, 0, None)
+    assert st == lh._lib.ERR_INVALID_ARG and "multiples" in msg
+    # zero tiles is a no-op that needs no device
+    assert L.lava_hip_coopmat_perelement_scale(None, None, 16, 0, None, 0, 0, None) == 0

@@ -427,3 +427,63 @@ def test_tensor_clamp_one_gives_row_sums(oracle):
     D = P @ Vp
     np.testing.assert_allclose(D[:, :E], P @ V.reshape(16, E), rtol=1e-14)
     np.testing.assert_allclose(D[:, E:], np.repeat(P.sum(axis=1, keepdims=True), 16 - E, axis=1), rtol=1e-14)
+
+
+# ---------------------------------------------------------------- tile addressing and per-element scales
+def test_load_tile_matches_numpy_reshapes_and_strided_views(oracle):
+    rng = np.random.default_rng(3)
+    buf = rng.standard_normal(4096).astype(np.float32)
+    R, C, off = 16, 32, 7
+    # packed: numpy's own F / C reshapes of the contiguous run
+    np.testing.assert_array_equal(oracle.load_tile(buf, off, R, False, R, C),
+                                  buf[off:off + R * C].reshape(R, C, order="F"))
+    np.testing.assert_array_equal(oracle.load_tile(buf, off, C, True, R, C),
+                                  buf[off:off + R * C].reshape(R, C))
+    # padded strides: numpy's strided view of the same memory
+    isz = buf.itemsize
+    for s in (R + 3, 40):
+        view = np.lib.stride_tricks.as_strided(buf[off:], shape=(R, C), strides=(isz, s * isz))
+        np.testing.assert_array_equal(oracle.load_tile(buf, off, s, False, R, C), view)
+    view = np.lib.stride_tricks.as_strided(buf[off:], shape=(R, C), strides=(45 * isz, isz))
+    np.testing.assert_array_equal(oracle.load_tile(buf, off, 45, True, R, C), view)
+
+
+def test_load_tile_stride_zero_broadcasts(oracle):
+    """Stride 0: every column (column-major) reads the same R-vector -- a per-row factor;
+    every row (row-major) reads the same C-vector -- a per-column factor."""
+    v = np.arange(100, dtype=np.float32) * 0.5
+    np.testing.assert_array_equal(oracle.load_tile(v, 3, 0, False, 16, 16),
+                                  np.broadcast_to(v[3:19][:, None], (16, 16)))
+    np.testing.assert_array_equal(oracle.load_tile(v, 5, 0, True, 16, 32),
+                                  np.broadcast_to(v[5:37][None, :], (16, 32)))
+    # a planted transposition (the column-major rule read row-major) fails it
+    wrong = oracle.load_tile(v, 3, 0, True, 16, 16)
+    assert not np.array_equal(wrong, np.broadcast_to(v[3:19][:, None], (16, 16)))
+
+
+def test_store_tile_round_trip_and_untouched(oracle):
+    rng = np.random.default_rng(4)
+    buf = np.zeros(2048, np.float32)
+    m = rng.standard_normal((32, 32)).astype(np.float32)
+    for rowmajor in (False, True):
+        out = oracle.store_tile(buf, 11, 50, rowmajor, m)
+        np.testing.assert_array_equal(oracle.load_tile(out, 11, 50, rowmajor, 32, 32), m)
+        assert np.count_nonzero(out) == np.count_nonzero(m)   # nothing else written
+        assert out[:11].sum() == 0
+
+
+def test_scale_columns_and_rows_are_diagonal_products(oracle):
+    """Per-column scaling is M diag(s); per-row is diag(cs) M: numpy matmul in fp64 of the
+    same values (each element one product, so fp32 rounding of it is exact to 1 ulp)."""
+    rng = np.random.default_rng(5)
+    m = rng.standard_normal((16, 16)).astype(np.float32)
+    s = rng.uniform(0.001, 0.02, 64).astype(np.float16)
+    got = oracle.scale_columns(m, s, 9)
+    ref = m.astype(np.float64) @ np.diag(s[9:25].astype(np.float64))
+    np.testing.assert_array_equal(got, ref.astype(np.float32))
+    cs = rng.standard_normal(64).astype(np.float32)
+    got = oracle.scale_rows(m, cs, 30)
+    ref = np.diag(cs[30:46].astype(np.float64)) @ m.astype(np.float64)
+    np.testing.assert_array_equal(got, ref.astype(np.float32))
+    # a planted row/column swap fails
+    assert not np.array_equal(oracle.scale_rows(m, s.astype(np.float32), 9), oracle.scale_columns(m, s, 9))
