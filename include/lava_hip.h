@@ -8,8 +8,11 @@
  *     crosses the ABI.
  *   - pointers to device memory are plain addresses (hipMalloc'd or any other
  *     device allocation); the caller owns every buffer.
- *   - `stream` is a hipStream_t passed as void*; NULL is the default stream.
- *     Launches are asynchronous on that stream.
+ *   - `stream` is a hipStream_t passed as void*; NULL is the default (NULL) stream.
+ *     Launches are asynchronous on that stream.  lava_hip_stream_create makes a
+ *     NON-BLOCKING stream (hipStreamNonBlocking): it is not ordered after work on
+ *     the NULL stream, so a caller that fills inputs on the NULL stream synchronises
+ *     (lava_hip_synchronize, or an event) before launching on it.
  *   - element strides (lda, ldb, ...) are in elements, not bytes.
  *   - argument checks happen on the host before any GPU call, so a bad call
  *     fails with LAVA_HIP_ERR_INVALID_ARG / _UNSUPPORTED and touches no device.
@@ -87,7 +90,10 @@ int lava_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int lava_hip_fill_bytes(void* dst, uint8_t value, size_t bytes, void* stream);
 int lava_hip_synchronize(void);
 int lava_hip_stream_synchronize(void* stream);
+/* A non-blocking stream (hipStreamNonBlocking, default priority). */
 int lava_hip_stream_create(void** stream);
+/* Waits for the stream's work, frees the W8A16 workspace the library kept for it, then
+ * destroys it. */
 int lava_hip_stream_destroy(void* stream);
 int lava_hip_event_create(void** event);
 int lava_hip_event_destroy(void* event);
@@ -370,8 +376,14 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
 /* W8A16 (coopmat2 per-element dequant callback, src/device/coopmat_intrinsics.jl:535-628
  * with the scale pointer in `extras`, :569-572):
  *   Y (M x N, fp32) = (X (M x K, fp16) * float(W (K x N, int8))) .* s[col] (fp16).
- * layout: bit0 X row-major, bit1 W row-major, bit2 Y row-major; this build
- * implements X row-major, W row-major, Y row-major (layout == 7). */
+ * layout: bit0 X row-major, bit1 W row-major, bit2 Y row-major.  The weight-streaming
+ * kernels take layout 7 with K a multiple of 32 and N a multiple of 64; any other layout
+ * or shape runs on a generic kernel.  Wide N runs as one launch; narrower N splits K
+ * across workgroups into a split-K workspace the library owns, one per (device, stream):
+ * a call that grows it allocates (hipMalloc) and so is not capturable -- make one call of
+ * the largest shape outside capture first.  Calls on one stream from several threads are
+ * serialised around the workspace; lava_hip_stream_destroy frees it.  Results are
+ * deterministic (fixed summation order). */
 int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N, int64_t K,
                         int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream);
 

@@ -29,6 +29,7 @@
 
 #include <map>
 #include <mutex>
+#include <vector>
 
 #include "lava_coopmat.hpp"
 #include "lava_hip_internal.hpp"
@@ -45,6 +46,15 @@ __device__ __forceinline__ uint32_t w8_pair(uint32_t lo_row, uint32_t hi_row, in
     const uint32_t sel = (uint32_t)byte | 0x0c00u | ((uint32_t)(byte + 4) << 16) | 0x0c000000u;
     return __builtin_amdgcn_perm(hi_row, lo_row, sel) ^ 0x64806480u;
 }
+
+// The dequant callback f(r, c, e, s, base) = e * s[base + STRIDE c]: tile column c of a
+// kernel whose tile t holds the columns base = n0 + t, n0 + t + STRIDE, ...
+template <int STRIDE>
+struct ScaleStrided {
+    __device__ float operator()(uint32_t, uint32_t col, float e, const f16* s, uint32_t base) const {
+        return e * (float)s[base + STRIDE * col];
+    }
+};
 
 // Wavefront gw = split * W8_WAVES + w takes the 32-row steps [gw ks, min((gw + 1) ks,
 // total_steps)) of K.  KSTEPS > 0: the host guarantees exactly KSTEPS each, fully
@@ -130,11 +140,18 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
             for (int u = 0; u < DEPTH; ++u)
                 if (s0 + u < ksteps) step(u, s0 + u);
     }
-    // acc[t] lane holds column 8q + t and rows 4g + j of this wave's partial
+    // acc[t] lane holds column 8q + t and rows 4g + j of this wave's partial: the 16 x 16
+    // Accumulator tile t whose column c is n0 + 8c + t.  The dequant scale is applied to
+    // it by the per-element callback with the scale pointer in `extras`.
 #pragma unroll
-    for (int t = 0; t < 8; ++t)
+    for (int t = 0; t < 8; ++t) {
+        Frag<float, 16, 16, Accumulator> f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) red[w][4 * g + j][8 * q + t] = acc[t][j];
+        for (int j = 0; j < 4; ++j) f.v[j] = acc[t][j];
+        f = perelement(ScaleStrided<8>{}, f, scale, (uint32_t)(n0 + t));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) red[w][4 * g + j][8 * q + t] = f.v[j];
+    }
     __syncthreads();
 
     // workgroup sum over the 4 wavefronts: thread -> (row, 8 consecutive columns)
@@ -156,13 +173,12 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
     if (grow < M) {
         float* yp = Y + (int64_t)grow * ldy + n0 + c8;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) yp[i] = v[i] * (float)scale[n0 + c8 + i];
+        for (int i = 0; i < 8; ++i) yp[i] = v[i];
     }
 }
 
-// Y[r, c] = s[c] * sum over splits (in split order) of the partial blocks; 4 columns per thread.
-__global__ void __launch_bounds__(256) w8a16_reduce_kernel(const float* __restrict__ partial,
-                                                           const f16* __restrict__ scale, float* __restrict__ Y,
+// Y[r, c] = the sum over splits (in split order) of the scaled partial blocks; 4 columns per thread.
+__global__ void __launch_bounds__(256) w8a16_reduce_kernel(const float* __restrict__ partial, float* __restrict__ Y,
                                                            int M, int N, int64_t ldy, int splits, int64_t rows_pad) {
     const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // (row, 4-column group)
     const int64_t groups = N / 4;
@@ -175,7 +191,7 @@ __global__ void __launch_bounds__(256) w8a16_reduce_kernel(const float* __restri
     }
     float* yp = Y + r * ldy + c;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) yp[i] = acc[i] * (float)scale[c + i];
+    for (int i = 0; i < 4; ++i) yp[i] = acc[i];
 }
 
 // Any layout, any shape: one thread per output element, fp32 sums.
@@ -195,33 +211,128 @@ __global__ void w8a16_generic_kernel(const f16* __restrict__ X, const int8_t* __
     Y[yrow ? r * ldy + c : c * ldy + r] = s * (float)scale[c];
 }
 
-// Per-(device, stream) workspace for the split-K partial blocks, grown on demand;
-// calls on one stream are ordered, so they can share it.
+// ---- launch planning ----------------------------------------------------------------------
+enum W8Path { W8_GENERIC = 0, W8_SPLIT = 1 };
+
+struct W8Plan {
+    W8Path path = W8_GENERIC;
+    int64_t cblocks = 0, mblocks = 0, total_steps = 0, ks = 0;
+    int splits = 1;
+    int ksteps = 0;              // the per-wavefront step count of an unrolled instance, or 0
+    size_t scratch_bytes = 0;    // split-K partial blocks (W8_SPLIT with splits > 1)
+};
+
+static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
+                         uint32_t layout) {
+    W8Plan p;
+    const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 && K / W8_KSTEP <= 0x7fffffff &&
+                      ldw % 8 == 0 && ldx % 8 == 0 && aligned(W, 8) && aligned(X, 16) && N <= 0x7fffffff &&
+                      M <= 0x7fffffff && (M + 15) / 16 <= 65535;
+    if (!fast) return p;
+    p.path = W8_SPLIT;
+    p.mblocks = (M + 15) / 16;
+    p.total_steps = K / W8_KSTEP;
+    p.cblocks = N / W8_COLS;
+    // split K (up to 16 ways; the partial blocks cost 8 * splits bytes per output element of
+    // extra traffic) while the grid still fits the 256 CUs in one round, keeping >= 4 steps per
+    // wavefront: at 16 x 4096 . 4096 x 14336 the 224-workgroup grid (2 splits) streams ~6 %
+    // faster than the 448-workgroup one (4 splits), and 1 split (112) or 8 (896) are 20 % slower
+    while (p.splits < 16 && p.cblocks * p.mblocks * p.splits * 2 <= 256 &&
+           p.total_steps / (W8_WAVES * p.splits * 2) >= 4)
+        p.splits *= 2;
+    p.ks = (p.total_steps + W8_WAVES * p.splits - 1) / (W8_WAVES * p.splits);
+    p.ksteps = p.ks * W8_WAVES * p.splits == p.total_steps ? (int)p.ks : 0;   // unrolled instances need equal shares
+    if (p.splits > 1) p.scratch_bytes = (size_t)p.splits * (size_t)p.mblocks * 16 * (size_t)N * sizeof(float);
+    return p;
+}
+
+template <int KS>
+static void launch_split_ks(const W8Plan& p, const void* X, const void* W, const void* scale, void* Y, float* partial,
+                            int64_t M, int64_t N, int64_t ldx, int64_t ldw, int64_t ldy, hipStream_t s) {
+    hipLaunchKernelGGL(w8a16_kernel<KS>, dim3((unsigned)p.cblocks, (unsigned)p.splits, (unsigned)p.mblocks), dim3(256),
+                       0, s, (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, partial, (int)M, (int)N,
+                       ldx, ldw, ldy, p.splits, (int)p.ks, (int)p.total_steps);
+}
+
+// Enqueues the plan's kernels on `s`.  `partial` holds p.scratch_bytes when p.splits > 1.
+static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const void* scale, void* Y, float* partial,
+                        int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout,
+                        hipStream_t s) {
+    if (p.path == W8_SPLIT) {
+        switch (p.ksteps) {   // the usual counts fully unrolled, any other in groups of W8_DEPTH
+        case 1: launch_split_ks<1>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
+        case 2: launch_split_ks<2>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
+        case 4: launch_split_ks<4>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
+        case 8: launch_split_ks<8>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
+        case 16: launch_split_ks<16>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
+        case 32: launch_split_ks<32>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
+        default: launch_split_ks<0>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
+        }
+        LAVA_LAUNCH_CHECK("w8a16_kernel");
+        if (p.splits > 1) {
+            const int64_t threads = M * (N / 4);
+            hipLaunchKernelGGL(w8a16_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                               (const float*)partial, (float*)Y, (int)M, (int)N, ldy, p.splits, p.mblocks * 16);
+            LAVA_LAUNCH_CHECK("w8a16_reduce_kernel");
+        }
+        return LAVA_HIP_OK;
+    }
+    // any layout, any shape
+    const int64_t total = M * N;
+    hipLaunchKernelGGL(w8a16_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (const f16*)X,
+                       (const int8_t*)W, (const f16*)scale, (float*)Y, M, N, K, ldx, ldw, ldy, layout);
+    LAVA_LAUNCH_CHECK("w8a16_generic_kernel");
+    return LAVA_HIP_OK;
+}
+
+static int check_w8a16_args(const void* X, const void* W, const void* scale, const void* Y, int64_t M, int64_t N,
+                            int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, const char* name) {
+    LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative extent (M=%lld N=%lld K=%lld)", name, (long long)M,
+             (long long)N, (long long)K);
+    LAVA_ARG(layout <= 7u, "%s: layout %u has bits beyond X/W/Y row-major", name, layout);
+    if (M == 0 || N == 0) return LAVA_HIP_OK;
+    LAVA_ARG(Y != nullptr && scale != nullptr, "%s: null Y or scale", name);
+    LAVA_ARG(K == 0 || (X != nullptr && W != nullptr), "%s: null X or W", name);
+    const bool xrow = layout & 1u, wrow = layout & 2u, yrow = layout & 4u;
+    LAVA_ARG(ldx >= (xrow ? (K > 0 ? K : 1) : M), "%s: ldx = %lld too small", name, (long long)ldx);
+    LAVA_ARG(ldw >= (wrow ? N : (K > 0 ? K : 1)), "%s: ldw = %lld too small", name, (long long)ldw);
+    LAVA_ARG(ldy >= (yrow ? N : M), "%s: ldy = %lld too small", name, (long long)ldy);
+    LAVA_ARG(aligned(X, 2) && aligned(scale, 2) && aligned(Y, 4), "%s: misaligned X, scale or Y", name);
+    LAVA_REQUIRE((M * N + 255) / 256 <= 0x7fffffff && M * (N / 4) / 256 < 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED,
+                 "%s: problem too large", name);
+    return LAVA_HIP_OK;
+}
+
+// ---- the split-K workspace of lava_hip_gemm_w8a16 ------------------------------------------
+// One buffer per (device, stream), owned by the library.  The lock is held from the
+// workspace lookup through both launches, so the kernel pair of one call is enqueued
+// without another thread's pair between its halves on the same stream.  A buffer that
+// grows is retired, not freed -- work already enqueued or a graph captured earlier may
+// still use it -- and every buffer of a stream is freed by lava_hip_stream_destroy
+// (after the stream drains); buffers of the NULL stream live until the process ends.
 struct W8Workspace {
     void* buf = nullptr;
     size_t bytes = 0;
+    std::vector<void*> retired;
 };
 static std::mutex g_ws_mutex;
 static std::map<std::pair<int, void*>, W8Workspace> g_ws;
 
-static int get_workspace(void* stream, size_t partial_bytes, float** partial) {
-    int dev = 0;
-    LAVA_HIP_TRY(hipGetDevice(&dev));
+void w8a16_release_stream(void* stream) {
     std::lock_guard<std::mutex> lock(g_ws_mutex);
-    W8Workspace& ws = g_ws[{dev, stream}];
-    if (ws.bytes < partial_bytes) {
-        if (ws.buf) {
-            LAVA_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
-            LAVA_HIP_TRY(hipFree(ws.buf));
-            ws = W8Workspace{};
+    for (auto it = g_ws.begin(); it != g_ws.end();) {
+        if (it->first.second != stream) {
+            ++it;
+            continue;
         }
-        void* p = nullptr;
-        LAVA_HIP_TRY(hipMalloc(&p, partial_bytes));
-        ws.buf = p;
-        ws.bytes = partial_bytes;
+        int cur = 0;
+        (void)hipGetDevice(&cur);
+        (void)hipSetDevice(it->first.first);
+        for (void* b : it->second.retired) (void)hipFree(b);
+        if (it->second.buf) (void)hipFree(it->second.buf);
+        (void)hipSetDevice(cur);
+        it = g_ws.erase(it);
     }
-    *partial = static_cast<float*>(ws.buf);
-    return LAVA_HIP_OK;
 }
 
 }  // namespace lava
@@ -230,77 +341,23 @@ using namespace lava;
 
 extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N,
                                    int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream) {
-    LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "gemm_w8a16: negative extent (M=%lld N=%lld K=%lld)", (long long)M,
-             (long long)N, (long long)K);
-    LAVA_ARG(layout <= 7u, "gemm_w8a16: layout %u has bits beyond X/W/Y row-major", layout);
-    if (M == 0 || N == 0) return LAVA_HIP_OK;
-    LAVA_ARG(Y != nullptr && scale != nullptr, "gemm_w8a16: null Y or scale");
-    LAVA_ARG(K == 0 || (X != nullptr && W != nullptr), "gemm_w8a16: null X or W");
-    const bool xrow = layout & 1u, wrow = layout & 2u, yrow = layout & 4u;
-    LAVA_ARG(ldx >= (xrow ? (K > 0 ? K : 1) : M), "gemm_w8a16: ldx = %lld too small", (long long)ldx);
-    LAVA_ARG(ldw >= (wrow ? N : (K > 0 ? K : 1)), "gemm_w8a16: ldw = %lld too small", (long long)ldw);
-    LAVA_ARG(ldy >= (yrow ? N : M), "gemm_w8a16: ldy = %lld too small", (long long)ldy);
-    LAVA_ARG(aligned(X, 2) && aligned(scale, 2) && aligned(Y, 4), "gemm_w8a16: misaligned X, scale or Y");
-    int rc = lava_hip_init();
+    int rc = check_w8a16_args(X, W, scale, Y, M, N, K, ldx, ldw, ldy, layout, "gemm_w8a16");
+    if (rc != LAVA_HIP_OK || M == 0 || N == 0) return rc;
+    rc = lava_hip_init();
     if (rc != LAVA_HIP_OK) return rc;
+    const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout);
     hipStream_t s = as_stream(stream);
-
-    // fast path: all row-major, N in 128-column blocks, K in 32-row steps
-    const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 && K / W8_KSTEP <= 0x7fffffff &&
-                      ldw % 8 == 0 && ldx % 8 == 0 && aligned(W, 8) && aligned(X, 16) && N <= 0x7fffffff &&
-                      M <= 0x7fffffff;
-    if (fast) {
-        // split K (up to 16 ways; the partial blocks cost 8 * splits bytes per output
-        // element of extra traffic) while the grid still fits the 256 CUs in one round,
-        // keeping >= 4 steps per wavefront: at 16 x 4096 . 4096 x 14336 the 224-workgroup
-        // grid (2 splits) streams ~6 % faster than the 448-workgroup one (4 splits), and
-        // 1 split (112) or 8 (896) are 20 % slower
-        const int64_t cblocks = N / W8_COLS, mblocks = (M + 15) / 16;
-        const int64_t total_steps = K / W8_KSTEP;
-        int splits = 1;
-        while (splits < 16 && cblocks * mblocks * splits * 2 <= 256 && total_steps / (W8_WAVES * splits * 2) >= 4)
-            splits *= 2;
-        const int64_t ks = (total_steps + W8_WAVES * splits - 1) / (W8_WAVES * splits);
-        const bool even = ks * W8_WAVES * splits == total_steps;
-        const int64_t ksteps = even ? ks : 0;   // the unrolled instances need equal shares
-        LAVA_REQUIRE(mblocks <= 65535 && cblocks <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: grid too large");
-        float* partial = nullptr;
-        if (splits > 1) {
-            rc = get_workspace(stream, (size_t)splits * (size_t)mblocks * 16 * (size_t)N * sizeof(float), &partial);
-            if (rc != LAVA_HIP_OK) return rc;
-        }
-        const dim3 grid((unsigned)cblocks, (unsigned)splits, (unsigned)mblocks);
-#define LAVA_W8_LAUNCH(KS)                                                                                        \
-    hipLaunchKernelGGL(w8a16_kernel<KS>, grid, dim3(256), 0, s, (const f16*)X, (const int8_t*)W,                \
-                       (const f16*)scale, (float*)Y, partial, (int)M, (int)N, ldx, ldw, ldy, splits, (int)ks,     \
-                       (int)total_steps)
-        switch (ksteps) {   // the usual counts fully unrolled, any other in groups of W8_DEPTH
-        case 1: LAVA_W8_LAUNCH(1); break;
-        case 2: LAVA_W8_LAUNCH(2); break;
-        case 4: LAVA_W8_LAUNCH(4); break;
-        case 8: LAVA_W8_LAUNCH(8); break;
-        case 16: LAVA_W8_LAUNCH(16); break;
-        case 32: LAVA_W8_LAUNCH(32); break;
-        default: LAVA_W8_LAUNCH(0); break;
-        }
-#undef LAVA_W8_LAUNCH
-        LAVA_LAUNCH_CHECK("w8a16_kernel");
-        if (splits > 1) {
-            const int64_t threads = M * (N / 4);
-            LAVA_REQUIRE((threads + 255) / 256 <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: problem too large");
-            hipLaunchKernelGGL(w8a16_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                               (const float*)partial, (const f16*)scale, (float*)Y, (int)M, (int)N, ldy, splits,
-                               mblocks * 16);
-            LAVA_LAUNCH_CHECK("w8a16_reduce_kernel");
-        }
-        return LAVA_HIP_OK;
+    if (p.scratch_bytes == 0) return launch_w8a16(p, X, W, scale, Y, nullptr, M, N, K, ldx, ldw, ldy, layout, s);
+    int dev = 0;
+    LAVA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    W8Workspace& ws = g_ws[{dev, stream}];
+    if (ws.bytes < p.scratch_bytes) {
+        void* buf = nullptr;
+        LAVA_HIP_TRY(hipMalloc(&buf, p.scratch_bytes));
+        if (ws.buf) ws.retired.push_back(ws.buf);
+        ws.buf = buf;
+        ws.bytes = p.scratch_bytes;
     }
-{   // any layout, any shape
-    const int64_t total = M * N;
-    LAVA_REQUIRE((total + 255) / 256 <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "gemm_w8a16: problem too large");
-    hipLaunchKernelGGL(w8a16_generic_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, (const f16*)X,
-                       (const int8_t*)W, (const f16*)scale, (float*)Y, M, N, K, ldx, ldw, ldy, layout);
-    LAVA_LAUNCH_CHECK("w8a16_generic_kernel");
-    return LAVA_HIP_OK;
-}
+    return launch_w8a16(p, X, W, scale, Y, static_cast<float*>(ws.buf), M, N, K, ldx, ldw, ldy, layout, s);
 }

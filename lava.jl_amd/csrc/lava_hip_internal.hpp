@@ -17,6 +17,10 @@ int check_launch(const char* kernel);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Frees the W8A16 split-K workspaces kept for `stream` (called by lava_hip_stream_destroy
+// once the stream has drained).
+void w8a16_release_stream(void* stream);
+
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 }  // namespace lava

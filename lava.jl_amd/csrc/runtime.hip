@@ -195,6 +195,9 @@ int lava_hip_stream_create(void** stream) {
 
 int lava_hip_stream_destroy(void* stream) {
     if (stream == nullptr) return LAVA_HIP_OK;
+    // the stream's W8A16 workspace may be in use by work still queued on it
+    LAVA_HIP_TRY(hipStreamSynchronize(as_stream(stream)));
+    lava::w8a16_release_stream(stream);
     LAVA_HIP_TRY(hipStreamDestroy(as_stream(stream)));
     return LAVA_HIP_OK;
 }

@@ -152,6 +152,9 @@ def test_gemm_streams_and_repeat(gpu, oracle):
     lh = gpu
     announce("gemm bf16 1024^3 on a stream, twice")
     A, B = make_inputs(gpu, "bf16", 1024, 1024, 1024, 1, 5, 6)
+    # the inputs were filled on the NULL stream; a library stream is non-blocking, so it is
+    # not ordered after that work without a synchronisation
+    lh.synchronize()
     s = lh.Stream()
     C1 = lh.HIPDeviceArray("f32", (1024, 1024), order="C")
     C2 = lh.HIPDeviceArray("f32", (1024, 1024), order="C")

@@ -31,7 +31,9 @@ def w8_inputs(lh, M, N, K, seed_cfg=3, order="C"):
                                    # per wavefront before the split (decode shapes of common models), 3
                                    (16, 4096, 11008), (16, 4096, 14336), (1, 1024, 384), (48, 256, 1408),
                                    # K a multiple of 32 only: unequal per-wavefront shares, some empty
-                                   (16, 256, 96), (7, 384, 1120), (16, 128, 32)])
+                                   (16, 256, 96), (7, 384, 1120), (16, 128, 32),
+                                   # wide N: one split, several row blocks with uneven shares, M = 1
+                                   (16, 11008, 4096), (33, 6144, 1120), (1, 10240, 64), (16, 12288, 96)])
 def test_w8a16(gpu, oracle, M, N, K):
     lh = gpu
     announce(f"w8a16 M={M} N={N} K={K}")
@@ -46,6 +48,63 @@ def test_w8a16(gpu, oracle, M, N, K):
     Y2 = lh.HIPDeviceArray("f32", (M, N), order="C")
     lh.w8a16(Y2, X, W, s)
     np.testing.assert_array_equal(Y.to_numpy(), Y2.to_numpy())
+
+
+def test_w8a16_two_threads_one_stream(gpu, oracle):
+    """Split-K calls from two host threads on the NULL stream: each call's kernel pair is
+    enqueued whole, so neither thread's partial sums are overwritten by the other's."""
+    import threading
+    lh = gpu
+    announce("w8a16 split-K from two threads on one stream")
+    shapes = [(16, 4096, 4096), (8, 2048, 8192)]
+    cases = []
+    for i, (M, N, K) in enumerate(shapes):
+        X, W, s = w8_inputs(lh, M, N, K, seed_cfg=20 + i)
+        Y = lh.HIPDeviceArray("f32", (M, N), order="C")
+        lh.w8a16(Y, X, W, s)
+        lh.synchronize()
+        cases.append((X, W, s, Y, Y.to_numpy()))
+    errors = []
+
+    def worker(case):
+        X, W, s, Y, _ = case
+        try:
+            for _ in range(30):
+                lh.w8a16(Y, X, W, s)
+        except Exception as e:   # pragma: no cover - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=worker, args=(c,)) for c in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    lh.synchronize()
+    assert not errors, errors
+    for (M, N, K), (X, W, s, Y, first) in zip(shapes, cases):
+        np.testing.assert_array_equal(Y.to_numpy(), first)
+        ref = oracle.w8a16_rows(X.to_numpy(), W.to_numpy(), s.to_numpy(), N, K, K, N, np.arange(M))
+        assert oracle.rel_frobenius(first, ref) <= 1e-3
+
+
+def test_w8a16_stream_destroy_releases_workspace(gpu, oracle):
+    """A split-K call on a library stream, then the stream destroyed (it drains first);
+    a new stream gets a new workspace and the same result."""
+    lh = gpu
+    announce("w8a16 split-K on a stream, stream destroyed, again on another")
+    M, N, K = 16, 4096, 4096
+    X, W, s = w8_inputs(lh, M, N, K, seed_cfg=22)
+    lh.synchronize()
+    outs = []
+    for _ in range(2):
+        st = lh.Stream()
+        Y = lh.HIPDeviceArray("f32", (M, N), order="C")
+        lh.w8a16(Y, X, W, s, stream=st.handle)
+        st.close()
+        outs.append(Y.to_numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+    ref = oracle.w8a16_rows(X.to_numpy(), W.to_numpy(), s.to_numpy(), N, K, K, N, np.arange(M))
+    assert oracle.rel_frobenius(outs[0], ref) <= 1e-3
 
 
 def test_w8a16_column_major_generic(gpu, oracle):
