@@ -387,6 +387,19 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
 int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N, int64_t K,
                         int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream);
 
+/* lava_hip_gemm_w8a16 without any allocation: the same kernels and results (bit for bit),
+ * with the split-K partial blocks in a fixed per-GPU device array of
+ * LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES instead of a library-allocated workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  No call makes a hipMalloc,
+ * hipFree or other allocating call; a shape whose plan needs more scratch than the array holds
+ * is refused with LAVA_HIP_ERR_INVALID_ARG (no plan of the split rule does).  Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (two streams, two threads) race
+ * and must be serialised by the caller. */
+#define LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES ((size_t)2 << 20)
+int lava_hip_gemm_w8a16_noalloc(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N,
+                                int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream);
+
 /* Flash-attention forward, fp16 Q/K/V/O, fp32 running max and sum:
  *   O = softmax(Q K^T * scale + mask) V  per (head, batch),
  * the `attn_flash_rows!` / flash_attn_cm2 form (src/vocabulary/coopmat.jl:158;

@@ -335,6 +335,36 @@ void w8a16_release_stream(void* stream) {
     }
 }
 
+// ---- the no-allocation entry's scratch --------------------------------------------------------
+// lava_hip_gemm_w8a16_noalloc keeps its split-K partial blocks in this fixed device array, one
+// copy per GPU, reached through the address hipGetSymbolAddress returns for it on that GPU (the
+// array's name is only a host-side stand-in).  The split rule keeps a grid at <= 256 workgroups,
+// each writing one 16 x 128 fp32 block, so no plan needs more than 2 MiB.  Every block a
+// reduction reads is written by the same call first: nothing needs clearing between calls.
+static_assert(LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES >= 256 * 16 * W8_COLS * sizeof(float),
+              "the no-allocation scratch must hold the largest split-K plan");
+static __device__ __attribute__((used)) __align__(256) float scratch[LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+constexpr int W8_MAX_DEVICES = 64;
+static std::mutex g_scratch_mutex;
+static float* g_scratch_ptr[W8_MAX_DEVICES];
+
+// The device address of `scratch` on the current device, looked up once per device.
+static int scratch_for_device(float** out) {
+    int dev = 0;
+    LAVA_HIP_TRY(hipGetDevice(&dev));
+    LAVA_REQUIRE(dev >= 0 && dev < W8_MAX_DEVICES, LAVA_HIP_ERR_UNSUPPORTED,
+                 "gemm_w8a16_noalloc: device %d beyond the %d this library tracks", dev, W8_MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        LAVA_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        LAVA_REQUIRE(ptr != nullptr, LAVA_HIP_ERR_HIP, "gemm_w8a16_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = static_cast<float*>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return LAVA_HIP_OK;
+}
+
 }  // namespace lava
 
 using namespace lava;
@@ -360,4 +390,24 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
         ws.bytes = p.scratch_bytes;
     }
     return launch_w8a16(p, X, W, scale, Y, static_cast<float*>(ws.buf), M, N, K, ldx, ldw, ldy, layout, s);
+}
+
+extern "C" int lava_hip_gemm_w8a16_noalloc(const void* X, const void* W, const void* scale, void* Y, int64_t M,
+                                           int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy,
+                                           uint32_t layout, void* stream) {
+    int rc = check_w8a16_args(X, W, scale, Y, M, N, K, ldx, ldw, ldy, layout, "gemm_w8a16_noalloc");
+    if (rc != LAVA_HIP_OK || M == 0 || N == 0) return rc;
+    const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout);
+    LAVA_ARG(p.scratch_bytes <= LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES,
+             "gemm_w8a16_noalloc: this shape needs %zu bytes of split-K scratch; the no-allocation entry holds at most "
+             "%zu (M = %lld, N = %lld, K = %lld)", p.scratch_bytes, (size_t)LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES,
+             (long long)M, (long long)N, (long long)K);
+    rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    float* partial = nullptr;
+    if (p.scratch_bytes > 0) {
+        rc = scratch_for_device(&partial);
+        if (rc != LAVA_HIP_OK) return rc;
+    }
+    return launch_w8a16(p, X, W, scale, Y, partial, M, N, K, ldx, ldw, ldy, layout, as_stream(stream));
 }

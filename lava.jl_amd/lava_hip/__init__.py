@@ -12,7 +12,7 @@ from .kernels import (coopmat_accinit_muladd, coopmat_convert, coopmat_convert_u
                       coopmat_muladd_16x16x16, coopmat_perelement_pair, coopmat_perelement_rowcol,
                       coopmat_perelement_scale, coopmat_reduce, coopmat_workgroup_gemm, dot4x8, fill_i8, fill_normal,
                       fill_uniform, flash_attn_fwd, flash_attn_fwd_raw, gemm, gemm_ex, gemm_ex_raw, gemm_raw, w8a16,
-                      w8a16_raw)
+                      w8a16_noalloc, w8a16_raw)
 from .tensor import (TENSOR_CLAMP_CONSTANT, TENSOR_CLAMP_TO_EDGE, TENSOR_CLAMP_UNDEFINED, TensorLayout, TensorView,
                      gemm_cm2, tensor_clampbits, tensor_layout, tensor_load_tile, tensor_muladd_16x16x16,
                      tensor_setclampvalue, tensor_setdim, tensor_setstride, tensor_slice, tensor_store_tile,

@@ -107,6 +107,7 @@ PROTOTYPES: dict[str, tuple] = {
     "lava_hip_tensor_muladd_16x16x16": (ci, [vp, vp, vp, vp, ci, vp, vp]),
     "lava_hip_gemm_cm2_f16": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_gemm_w8a16": (ci, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
+    "lava_hip_gemm_w8a16_noalloc": (ci, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_flash_attn_fwd_f16": (ci, [vp, vp, vp, vp, i64, i64, i64, i64, C.POINTER(i64),
                                          C.POINTER(i64), C.c_float, ci, vp]),
 }

@@ -119,6 +119,20 @@ def w8a16(Y: HIPDeviceArray, X: HIPDeviceArray, W: HIPDeviceArray, scale: HIPDev
     return Y
 
 
+def w8a16_noalloc(Y: HIPDeviceArray, X: HIPDeviceArray, W: HIPDeviceArray, scale: HIPDeviceArray,
+                  stream: Optional[int] = None) -> HIPDeviceArray:
+    """`w8a16` through the entry point that allocates nothing: the split-K partials live in a
+    fixed per-GPU device array (shared by every call on that GPU: overlapping calls race)."""
+    M, K = X.dims
+    K2, N = W.dims
+    if K2 != K or Y.dims != (M, N) or scale.size != N:
+        raise ValueError(f"shape mismatch: X {X.dims}, W {W.dims}, scale {scale.dims}, Y {Y.dims}")
+    layout = (1 if X.order == "C" else 0) | (2 if W.order == "C" else 0) | (4 if Y.order == "C" else 0)
+    _lib.call("lava_hip_gemm_w8a16_noalloc", X.ptr, W.ptr, scale.ptr, Y.ptr, M, N, K, _ld(X), _ld(W), _ld(Y), layout,
+              stream)
+    return Y
+
+
 def w8a16_raw(X: int, W: int, scale: int, Y: int, M: int, N: int, K: int, ldx: int, ldw: int, ldy: int,
               layout: int = 7, stream: Optional[int] = None) -> None:
     _lib.call("lava_hip_gemm_w8a16", X, W, scale, Y, M, N, K, ldx, ldw, ldy, layout, stream)

@@ -1,0 +1,55 @@
+"""The W8A16 entry point that allocates nothing, through the C ABI: the same results as
+lava_hip_gemm_w8a16 (bit for bit: the same kernels and summation order) on two calls in a
+row, the second smaller, and on a shape that needs no split-K scratch at all."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import lava_hip as lh_mod
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(lh, M, N, K, cfg):
+    X = lh.HIPDeviceArray("f16", (M, K), order="C")
+    W = lh.HIPDeviceArray("i8", (K, N), order="C")
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(X, lh_mod.seed(cfg, 0))
+    lh.fill_i8(W, lh_mod.seed(cfg, 1), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(cfg, 2), 0.001, 0.02)
+    return X, W, s
+
+
+def _both(lh, M, N, K, cfg):
+    X, W, s = _inputs(lh, M, N, K, cfg)
+    Y_ref = lh.HIPDeviceArray("f32", (M, N), order="C")
+    Y_na = lh.HIPDeviceArray("f32", (M, N), order="C")
+    Y_na.fill_bytes(0xFF)
+    lh.w8a16(Y_ref, X, W, s)
+    lh._lib.call("lava_hip_gemm_w8a16_noalloc", X.ptr, W.ptr, s.ptr, Y_na.ptr, M, N, K, K, N, N, 7, None)
+    lh.synchronize()
+    return X, W, s, Y_ref.to_numpy(), Y_na.to_numpy()
+
+
+def test_noalloc_matches_allocating_entry_twice(gpu, oracle):
+    lh = gpu
+    # split-K shapes (8 and 4 splits): the partial blocks go through the static scratch;
+    # the second call is smaller and reuses the array the first one left behind
+    for i, (M, N, K) in enumerate([(16, 4096, 4096), (8, 2048, 2048)]):
+        announce(f"w8a16_noalloc call {i + 1}: M={M} N={N} K={K}")
+        X, W, s, ref_entry, got = _both(lh, M, N, K, 40 + i)
+        np.testing.assert_array_equal(got, ref_entry)
+        ref = oracle.w8a16_rows(X.to_numpy(), W.to_numpy(), s.to_numpy(), N, K, K, N, np.arange(M))
+        assert oracle.rel_frobenius(got, ref) <= 1e-3
+
+
+def test_noalloc_without_split_and_argument_errors(gpu, oracle):
+    lh = gpu
+    announce("w8a16_noalloc: one split (no scratch), ragged generic shape, bad arguments")
+    for (M, N, K), cfg in (((16, 14336, 4096), 42), ((3, 7, 5), 43)):
+        X, W, s, ref_entry, got = _both(lh, M, N, K, cfg)
+        np.testing.assert_array_equal(got, ref_entry)
+    with pytest.raises(lh.InvalidArgument):
+        lh._lib.call("lava_hip_gemm_w8a16_noalloc", 16, 16, 16, 16, 16, 128, 256, 256, 100, 128, 7, None)
