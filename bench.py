@@ -16,6 +16,13 @@ A step is one kernel launch over the whole problem.  Kernel time is the median
 of the K per-launch times that HIP events recorded on the launch stream give
 (`kernel_ms`; the mean is `kernel_ms_mean`); wall time comes from a synchronised
 host clock around the same region.
+
+Clock settling: an idle MI355X holds a low engine clock (rocm-smi shows sclk at
+114-811 MHz) and needs about half a second of sustained load to reach its
+steady loaded clock (~1.9 GHz under these kernels).  So that the K steps are not
+timed during that ramp, each workload first runs untimed for --settle seconds
+(default 1.0, reported as `clock_settle_s`), then the W warmup steps, then the
+K timed steps.
 """
 from __future__ import annotations
 
@@ -41,10 +48,17 @@ PEAK_HBM_GBS = 8000.0
 
 
 def timed(lh, launch, steps: int, warmup: int, stream):
-    """Warm up, then time exactly `steps` launches.  An event recorded on `stream`
-    after every launch splits the region into per-launch kernel times; the median of
-    them is the kernel time (the mean is returned beside it).  A synchronised host
-    clock around the same region gives the wall time per step."""
+    """Settle the clock, warm up, then time exactly `steps` launches.  The workload
+    runs untimed for SETTLE_S[0] seconds first (the engine clock's ramp from idle).
+    An event recorded on `stream` after every launch splits the region into
+    per-launch kernel times; the median of them is the kernel time (the mean is
+    returned beside it).  A synchronised host clock around the same region gives
+    the wall time per step."""
+    t_end = time.perf_counter() + SETTLE_S[0]
+    while time.perf_counter() < t_end:
+        for _ in range(4):
+            launch()
+        lh.synchronize()
     for _ in range(warmup):
         launch()
     lh.synchronize()
@@ -63,6 +77,8 @@ def timed(lh, launch, steps: int, warmup: int, stream):
 
 # mean of the per-launch kernel times of the last timed() call (reported beside the median)
 TIMED_MEAN_MS = [0.0]
+# seconds of untimed load before each workload's warmup (--settle)
+SETTLE_S = [1.0]
 
 
 def load_traffic(name: str):
@@ -220,7 +236,10 @@ def main():
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--settle", type=float, default=1.0,
+                    help="seconds of untimed load before the warmup, for the clock to leave its idle state")
     args = ap.parse_args()
+    SETTLE_S[0] = max(0.0, args.settle)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -233,7 +252,8 @@ def main():
     s = lh.Stream()
     stream = s.handle
     K, W = args.steps, args.warmup
-    out = {"metric": METRIC, "n_gpus": 1, "steps": K, "warmup": W, "higher_is_better": True, "scaling": "weak",
+    out = {"metric": METRIC, "n_gpus": 1, "steps": K, "warmup": W, "clock_settle_s": SETTLE_S[0],
+           "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "data": "synthetic (seeded: uniform[-1,1] GEMM inputs, normal(0,1) Q/K/V), "
                                          "generated on the device before timing"}
 

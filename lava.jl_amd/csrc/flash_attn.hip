@@ -64,6 +64,7 @@ struct FaParams {
     int S, H, B;
     float scale_log2;        // softmax scale * log2(e)
     int causal;
+    int o16;                 // O and its strides allow 16-byte row stores
 };
 
 // Workgroup -> (batch * head, query block).  Workgroups are dispatched round-robin
@@ -703,7 +704,8 @@ constexpr int F5_PAIRS = 4;
 constexpr int F5_BQ = 64 * F5_PAIRS;   // 256 queries per workgroup
 constexpr int F5_BK = 64;
 constexpr int F5_KST = 3, F5_VST = 2;
-constexpr int F5_PF = 3;               // fragments read ahead of the MFMA that uses them
+constexpr int F5_PFK = 4;              // K fragments read ahead of the MFMA that uses them
+constexpr int F5_PFV = 5;              // V fragments read ahead
 
 typedef _Float16 f5_h2 __attribute__((ext_vector_type(2)));
 typedef uint32_t f5_u32x4 __attribute__((ext_vector_type(4)));
@@ -751,27 +753,30 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
     const int nkb = CAUSAL ? min((qb + 1) * (F5_BQ / F5_BK), nkb_s) : nkb_s;
     const int last = CAUSAL ? min(nkb - 1, (q0 + 63) / F5_BK) : nkb - 1;   // this pair's last key block
 
-    // LDS-DMA of K (score wavefronts) or V (output wavefronts): wavefront pr moves rows
-    // 16 pr + 4 i + lane / 16 of a tile, physical chunk lane % 16; blocks past the end
-    // re-read the last one (every iteration issues the same DMAs); rows at or past S
-    // read zero.
+    // LDS-DMA of K and V (issued by the output wavefronts): wavefront pr moves rows
+    // 16 pr + 4 i + lane / 16 of a tile, physical chunk lane % 16 (K chunk ^ key % 16, V
+    // chunk ^ 4 (key % 4)).  The lane offsets are the same for every block; the buffer
+    // resource of a block starts at its first row and ends at the sequence's end, so rows
+    // at or past S read zero.  Blocks past the end re-read the last one (every iteration
+    // issues the same DMAs).
     const uint32_t row_bytes = (uint32_t)(p.sl * 2);
-    const f3_v4i rsrc_k = f3_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
-    const f3_v4i rsrc_v = f3_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
-    auto dma1 = [&](bool is_k, int j, int i) __attribute__((always_inline)) {
-        const int src = j < nkb ? j : nkb - 1;
-        const uint32_t soff = (uint32_t)src * F5_BK * row_bytes;
-        const int row = 16 * pr + 4 * i + lane / CH;
-        const uint32_t swz = is_k ? (uint32_t)((lane % CH) ^ (row & 15)) : (uint32_t)((lane % CH) ^ (4 * (row & 3)));
-        uint32_t v = (uint32_t)row * row_bytes + 16u * swz;
-        if ((src + 1) * F5_BK > p.S) v = src * F5_BK + row < p.S ? v : 0x80000000u;
-        const uint32_t dst = f3_lds_addr(is_k ? &kbuf[0][0] : &vbuf[0][0]) + (uint32_t)pr * 16 * RB +
-                             (uint32_t)(j % (is_k ? F5_KST : F5_VST)) * TILE + 1024u * i;
-        const f3_v4i& rs = is_k ? rsrc_k : rsrc_v;
-        f3_v4i r;
+    uint32_t dv_k[DPT], dv_v[DPT];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = __builtin_amdgcn_readfirstlane(rs[e]);
-        f3_dma16(r, v, __builtin_amdgcn_readfirstlane(soff), __builtin_amdgcn_readfirstlane(dst));
+    for (int i = 0; i < DPT; ++i) {
+        const int row = 16 * pr + 4 * i + lane / CH;
+        dv_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CH) ^ (row & 15));
+        dv_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CH) ^ (4 * (row & 3)));
+    }
+    auto dma_tile = [&](bool is_k, int j) __attribute__((always_inline)) {
+        const int src = j < nkb ? j : nkb - 1;
+        const f16* base = (is_k ? p.K : p.V) + head + (int64_t)src * F5_BK * p.sl;
+        const uint32_t rows = (uint32_t)min(F5_BK, p.S - src * F5_BK);
+        const f3_v4i rs = f3_rsrc(base, rows * row_bytes);
+        const uint32_t dst = f3_lds_addr(is_k ? &kbuf[0][0] : &vbuf[0][0]) + (uint32_t)pr * 16 * RB +
+                             (uint32_t)(j % (is_k ? F5_KST : F5_VST)) * TILE;
+#pragma unroll
+        for (int i = 0; i < DPT; ++i)
+            f3_dma16(rs, is_k ? dv_k[i] : dv_v[i], 0u, __builtin_amdgcn_readfirstlane(dst + 1024u * i));
     };
     typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
     typedef __attribute__((address_space(3))) f3_s16x4 lds_s16x4;
@@ -784,27 +789,35 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
     // prologue DMAs (output wavefronts): K_0, K_1, K_2, V_0
     if (!is_s) {
 #pragma unroll
-        for (int t = 0; t < 3; ++t)
-#pragma unroll
-            for (int i = 0; i < DPT; ++i) dma1(true, t, i);
-#pragma unroll
-        for (int i = 0; i < DPT; ++i) dma1(false, 0, i);
+        for (int t = 0; t < 3; ++t) dma_tile(true, t);
+        dma_tile(false, 0);
     }
 
     if (is_s) {
         // ================= score wavefront =================
-        f16x8 qf[2][NKS];   // Q^T B operands: query q0 + 32 qh + r32, d = 16 ks + 8 h + [0, 8)
+        // The pair's 64 Q rows go to LDS first (this pair's P buffers, free until the first
+        // block's P is written), in the K tile's layout -- LDS-DMA of 4 whole rows per
+        // instruction, chunk ^ row % 16, rows at or past S read zero -- and the Q^T
+        // fragments are read from there: whole-row reads instead of 32 rows x 32 bytes per
+        // load instruction.
+        const uint32_t qst[2] = {f3_lds_addr(&pbuf[0][pr][0]), f3_lds_addr(&pbuf[1][pr][0])};
+        {
+            const uint32_t rows = (uint32_t)max(0, min(64, p.S - q0));
+            const f3_v4i rs = f3_rsrc(p.Q + head + (int64_t)q0 * p.sl, rows * row_bytes);
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh) {
-            const int q = q0 + 32 * qh + r32;
-            const f16* qrow = p.Q + head + (int64_t)q * p.sl + 8 * h;
-#pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) qf[qh][ks] = f16x8{};
-            if (q < p.S) {
-#pragma unroll
-                for (int ks = 0; ks < NKS; ++ks) qf[qh][ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
+            for (int i = 0; i < 16; ++i) {
+                const int row = 4 * i + lane / CH;
+                const uint32_t v = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CH) ^ (row & 15));
+                f3_dma16(rs, v, 0u, __builtin_amdgcn_readfirstlane(qst[i / 8] + (uint32_t)((4 * i) % 32) * RB));
             }
         }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        f16x8 qf[2][NKS];   // Q^T B operands: query q0 + 32 qh + r32, d = 16 ks + 8 h + [0, 8)
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks)
+                qf[qh][ks] = *(const lds_f16x8*)(uintptr_t)(qst[qh] + (uint32_t)(r32 * RB + (((2 * ks + h) ^ (r32 & 15)) << 4)));
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
@@ -812,17 +825,37 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                 const uint4 u = __builtin_bit_cast(uint4, qf[qh][ks]);
                 asm volatile("" ::"v"(u.x), "v"(u.y), "v"(u.z), "v"(u.w));
             }
+        // The base-2 softmax scale c is folded into Q^T (one fp16 rounding of q * c) when
+        // that cannot overflow (c <= 1), and the running maximum enters the product as a
+        // bias k-step: ones (key rows, k = 0) times -m (query columns, k = 0).  The
+        // accumulator then holds S' = c q.k - m directly and P = exp2(S') needs no
+        // per-score multiply-add.  m is kept fp16-representable for that; a rescaled block,
+        // c > 1, or a maximum beyond +-60000 (after which the wavefront stays on this path)
+        // take P = exp2(fma(S, c', -m')) in fp32 instead.
+        const float c = p.scale_log2;
+        bool fast = c <= 1.f;                    // wavefront-uniform
+        if (fast) {
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+                for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) qf[qh][ks][e] = (f16)((float)qf[qh][ks][e] * c);
+        }
+        const float c_raw = fast ? 1.f : c;      // the multiplier S needs on the fp32 path
+        f16x8 ones{};                            // bias A operand: 1 at k = 0 of every key row
+        ones[0] = h == 0 ? (f16)1.f : (f16)0.f;
+        f16x8 qm[2] = {f16x8{}, f16x8{}};         // bias B operand: -m at k = 0 of each query
         // K fragment (kt, ks): row 32 kt + r32, chunk (2 ks + h) ^ (r32 % 16)
         uint32_t kb0[NKS];
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks)
             kb0[ks] = f3_lds_addr(&kbuf[0][0]) + (uint32_t)(r32 * RB + (((2 * ks + h) ^ (r32 & 15)) << 4));
         f32x16 st[2][2];           // st[kt][qh] register r: key 32 kt + 8 (r / 4) + 4 h + r % 4
-        float m_run[2] = {-INFINITY, -INFINITY};
-        const float c = p.scale_log2;
+        float m_run[2] = {0.f, 0.f};
 
-        // S_kb = K_kb Q^T, the softmax, P^T and the rescale factors into buffer b
-        auto block = [&](int kb, int b) __attribute__((always_inline)) {
+        // S_kb = K_kb Q^T (minus m), the softmax, P^T and the rescale factors into buffer b
+        auto block = [&](int kb, int b, bool first) __attribute__((always_inline)) {
             uint32_t ka[NKS];
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) {
@@ -832,15 +865,23 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
             auto kread = [&](int f) __attribute__((always_inline)) -> f16x8 {   // f = 2 ks + kt
                 return *(const lds_f16x8*)(uintptr_t)(ka[f >> 1] + (uint32_t)((f & 1) * 32 * RB));
             };
-            f16x8 fr[F5_PF];
+            // reads F5_PFK fragments ahead of their MFMAs; sched_barrier keeps this order
+            // (the scheduler otherwise moves each read next to its use)
+            f16x8 fr[F5_PFK];
 #pragma unroll
-            for (int f = 0; f < F5_PF; ++f) fr[f] = kread(f);
+            for (int f = 0; f < F5_PFK; ++f) fr[f] = kread(f);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int qh = 0; qh < 2; ++qh)
+                    st[kt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, qm[qh], f32x16{}, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < 32; ++i) {   // MFMA i: fragment f = i / 2 (ks = f / 2, kt = f % 2), qh = i % 2
                 const int f = i >> 1, qh = i & 1, ks = f >> 1, kt = f & 1;
-                st[kt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[f % F5_PF], qf[qh][ks],
-                                                                    ks == 0 ? f32x16{} : st[kt][qh], 0, 0, 0);
-                if (qh == 1 && f + F5_PF < 16) fr[f % F5_PF] = kread(f + F5_PF);
+                st[kt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[f % F5_PFK], qf[qh][ks], st[kt][qh], 0, 0, 0);
+                if (qh == 1 && f + F5_PFK < 16) fr[f % F5_PFK] = kread(f + F5_PFK);
+                __builtin_amdgcn_sched_barrier(0);
             }
             // mask: causal key > query (the diagonal block and any past it); else keys >= S
             if (CAUSAL ? kb >= last : (kb + 1) * F5_BK > p.S) {
@@ -857,7 +898,9 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                             st[kt][qh][r] = off ? -INFINITY : st[kt][qh][r];
                         }
             }
-            float mx[2];
+            // t = how far this block's largest exponent lies above the running maximum
+            const bool fast_blk = fast;           // st holds S' (fast) or S (fp32 path)
+            float t[2];
 #pragma unroll
             for (int qh = 0; qh < 2; ++qh) {
                 float v = -INFINITY;
@@ -867,50 +910,76 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                     for (int r = 0; r < 16; ++r) v = fmaxf(v, st[kt][qh][r]);
                 float a, bb2;
                 f5_xor32_pair(v, a, bb2);
-                mx[qh] = fmaxf(a, bb2) * c;
+                const float mx = fmaxf(a, bb2);
+                t[qh] = fast_blk ? mx : fmaf(mx, c_raw, -m_run[qh]);
             }
-            const bool rescale =
-                __builtin_amdgcn_ballot_w64(mx[0] > m_run[0] + F3_RESCALE || mx[1] > m_run[1] + F3_RESCALE) != 0;
-            float alpha[2];
-#pragma unroll
-            for (int qh = 0; qh < 2; ++qh) {
-                const float m_new = rescale ? fmaxf(m_run[qh], mx[qh]) : m_run[qh];
-                alpha[qh] = __builtin_amdgcn_exp2f(m_run[qh] - m_new);
-                m_run[qh] = m_new;
-            }
+            const bool rescale = first || __builtin_amdgcn_ballot_w64(t[0] > F3_RESCALE || t[1] > F3_RESCALE) != 0;
+            float sub[2] = {0.f, 0.f};
             if (rescale) {
+                float mn[2];
+                bool ovf = false;
+#pragma unroll
+                for (int qh = 0; qh < 2; ++qh) {
+                    // the first block sets m to its maximum (it always holds key 0, so it
+                    // is never fully masked); later ones only raise it
+                    mn[qh] = m_run[qh] + (first ? t[qh] : fmaxf(t[qh], 0.f));
+                    ovf = ovf || !(fabsf(mn[qh]) <= 60000.f);
+                }
+                if (fast && __builtin_amdgcn_ballot_w64(ovf) != 0) fast = false;
+                float alpha[2];
+#pragma unroll
+                for (int qh = 0; qh < 2; ++qh) {
+                    if (fast) mn[qh] = (float)(f16)mn[qh];
+                    alpha[qh] = __builtin_amdgcn_exp2f(m_run[qh] - mn[qh]);
+                    sub[qh] = fast_blk ? mn[qh] - m_run[qh] : mn[qh];
+                    m_run[qh] = mn[qh];
+                    qm[qh][0] = (fast && h == 0) ? (f16)(-mn[qh]) : (f16)0.f;
+                }
                 if (h == 0) {
                     abuf[b][pr][r32] = alpha[0];
                     abuf[b][pr][32 + r32] = alpha[1];
                 }
+            } else if (!fast_blk) {
+                sub[0] = m_run[0];
+                sub[1] = m_run[1];
             }
             if (lane == 0) fbuf[b][pr] = rescale ? 1 : 0;
-            // P = exp2(s c - m) in fp16 (RNE), stored as the output wavefront's B operands
+            // P = exp2(S') (or exp2(S c' - m')) in fp16 (RNE), stored as the output wavefront's B operands
+            auto pstore = [&](auto plain) __attribute__((always_inline)) {
+                const float cb = fast_blk ? 1.f : c_raw;
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+                for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
+                    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                    for (int qh = 0; qh < 2; ++qh) {
-                        f5_u32x4 u;
-                        const float mneg = -m_run[qh];
+                        for (int qh = 0; qh < 2; ++qh) {
+                            f5_u32x4 u;
+                            const float msub = -sub[qh];
 #pragma unroll
-                        for (int k = 0; k < 4; ++k) {
-                            const int r0 = 8 * ks + 2 * k;
-                            const float e0 = __builtin_amdgcn_exp2f(fmaf(st[kt][qh][r0], c, mneg));
-                            const float e1 = __builtin_amdgcn_exp2f(fmaf(st[kt][qh][r0 + 1], c, mneg));
-                            const f5_h2 hv = {(_Float16)e0, (_Float16)e1};
-                            u[k] = __builtin_bit_cast(uint32_t, hv);
+                            for (int k = 0; k < 4; ++k) {
+                                const int r0 = 8 * ks + 2 * k;
+                                float x0 = st[kt][qh][r0], x1 = st[kt][qh][r0 + 1];
+                                if constexpr (!decltype(plain)::value) {
+                                    x0 = fmaf(x0, cb, msub);
+                                    x1 = fmaf(x1, cb, msub);
+                                }
+                                const f5_h2 hv = {(_Float16)__builtin_amdgcn_exp2f(x0), (_Float16)__builtin_amdgcn_exp2f(x1)};
+                                u[k] = __builtin_bit_cast(uint32_t, hv);
+                            }
+                            *(__attribute__((address_space(3))) f5_u32x4*)(uintptr_t)paddr(b, kt, ks, qh) = u;
                         }
-                        *(__attribute__((address_space(3))) f5_u32x4*)(uintptr_t)paddr(b, kt, ks, qh) = u;
-                    }
+            };
+            if (fast_blk && !rescale)
+                pstore(f3_tag<true>{});
+            else
+                pstore(f3_tag<false>{});
         };
 
         __syncthreads();                         // K_0 .. K_2, V_0 in LDS
-        block(0, 0);
+        block(0, 0, true);
         __syncthreads();                         // P_0 published
         for (int j = 0; j < nkb; ++j) {
-            if (j + 1 <= last) block(j + 1, (j + 1) & 1);
+            if (j + 1 <= last) block(j + 1, (j + 1) & 1, false);
             __syncthreads();
         }
     } else {
@@ -940,10 +1009,8 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
         for (int j = 0; j < nkb; ++j) {
             const int b = j & 1;
             // K_{j+3} into K_j's stage and V_{j+1} into V_{j-1}'s (both read in iteration j - 1)
-#pragma unroll
-            for (int i = 0; i < DPT; ++i) dma1(true, j + 3, i);
-#pragma unroll
-            for (int i = 0; i < DPT; ++i) dma1(false, j + 1, i);
+            dma_tile(true, j + 3);
+            dma_tile(false, j + 1);
             if (j <= last) {
                 if (j > 0 && fbuf[b][pr] != 0) {   // the maximum moved at block j: O *= alpha
                     const float a0 = abuf[b][pr][r32], a1 = abuf[b][pr][32 + r32];
@@ -974,12 +1041,14 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                 auto pread = [&](int kk, int qh) __attribute__((always_inline)) -> f16x8 {
                     return *(const lds_f16x8*)(uintptr_t)paddr(b, kk >> 1, kk & 1, qh);
                 };
-                f16x8 fr[F5_PF];
+                // V fragments F5_PFV ahead, P one key step ahead; sched_barrier keeps the order
+                f16x8 fr[F5_PFV];
                 f16x8 pp[2][2];   // [kk % 2][qh]
-#pragma unroll
-                for (int f = 0; f < F5_PF; ++f) fr[f] = vread(f);
                 pp[0][0] = pread(0, 0);
                 pp[0][1] = pread(0, 1);
+#pragma unroll
+                for (int f = 0; f < F5_PFV; ++f) fr[f] = vread(f);
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int i = 0; i < 32; ++i) {   // MFMA i: V fragment f = i / 2 (kk = f / 4, dt = f % 4), qh = i % 2
                     const int f = i >> 1, qh = i & 1, kk = f >> 2, dt = f & 3;
@@ -995,32 +1064,61 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                                 l_run[qq] = __builtin_amdgcn_fdot2(f5_h2{pp[kk & 1][qq][2 * e], pp[kk & 1][qq][2 * e + 1]},
                                                                    ones, l_run[qq], false);
                     }
-                    o[dt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[f % F5_PF], pp[kk & 1][qh], o[dt][qh], 0, 0,
+                    o[dt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[f % F5_PFV], pp[kk & 1][qh], o[dt][qh], 0, 0,
                                                                        0);
-                    if (qh == 1 && f + F5_PF < 16) fr[f % F5_PF] = vread(f + F5_PF);
+                    if (qh == 1 && f + F5_PFV < 16) fr[f % F5_PFV] = vread(f + F5_PFV);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // K_{j+3}, V_{j+1} landed
             __syncthreads();
         }
         // ---- O / L, fp16.  o[dt][qh] register r: d = 32 dt + 8 (r / 4) + 4 h + r % 4 of query q0 + 32 qh + r32.
+        float inv[2];
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) {
-            const int q = q0 + 32 * qh + r32;
             float la, lb;
             f5_xor32_pair(l_run[qh], la, lb);
-            const float inv = 1.f / (la + lb);
-            if (q >= p.S) continue;
-            f16* orow = Ob + (int64_t)q * p.osl;
+            inv[qh] = 1.f / (la + lb);
+        }
+        if (p.o16) {
+            // Staged through this pair's P buffers (no wavefront reads them after the last
+            // barrier) as 64 rows of 256 bytes, chunk ^ row % 16, then stored 4 whole rows per
+            // instruction (16 bytes per lane) instead of 32 rows x 16 bytes.
+            const uint32_t ost[2] = {f3_lds_addr(&pbuf[0][pr][0]), f3_lds_addr(&pbuf[1][pr][0])};
+            typedef __attribute__((address_space(3))) f16x4 lds_f16x4;
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
+            for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
-                for (int g4 = 0; g4 < 4; ++g4) {
-                    const int d = 32 * dt + 8 * g4 + 4 * h;
-                    f16x4 v = {(f16)(o[dt][qh][4 * g4 + 0] * inv), (f16)(o[dt][qh][4 * g4 + 1] * inv),
-                               (f16)(o[dt][qh][4 * g4 + 2] * inv), (f16)(o[dt][qh][4 * g4 + 3] * inv)};
-                    *reinterpret_cast<f16x4*>(orow + d) = v;
-                }
+                for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4) {
+                        const f16x4 v = {(f16)(o[dt][qh][4 * g4 + 0] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 1] * inv[qh]),
+                                         (f16)(o[dt][qh][4 * g4 + 2] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 3] * inv[qh])};
+                        *(lds_f16x4*)(uintptr_t)(ost[qh] + (uint32_t)(r32 * RB + (((4 * dt + g4) ^ (r32 & 15)) << 4) + 8 * h)) = v;
+                    }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int row = 4 * i + lane / CH, c = lane % CH;
+                const f16x8 v = *(const lds_f16x8*)(uintptr_t)(ost[i / 8] + (uint32_t)((row % 32) * RB + ((c ^ (row & 15)) << 4)));
+                if (q0 + row < p.S) *reinterpret_cast<f16x8*>(Ob + (int64_t)(q0 + row) * p.osl + 8 * c) = v;
+            }
+        } else {
+#pragma unroll
+            for (int qh = 0; qh < 2; ++qh) {
+                const int q = q0 + 32 * qh + r32;
+                if (q >= p.S) continue;
+                f16* orow = Ob + (int64_t)q * p.osl;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4) {
+                        const int d = 32 * dt + 8 * g4 + 4 * h;
+                        f16x4 v = {(f16)(o[dt][qh][4 * g4 + 0] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 1] * inv[qh]),
+                                   (f16)(o[dt][qh][4 * g4 + 2] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 3] * inv[qh])};
+                        *reinterpret_cast<f16x4*>(orow + d) = v;
+                    }
+            }
         }
     }
 }
@@ -1097,6 +1195,7 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     p.B = (int)B;
     p.scale_log2 = scale * 1.4426950408889634f;
     p.causal = causal != 0;
+    p.o16 = aligned(O, 16) && os[1] % 8 == 0 && os[2] % 8 == 0 && os[3] % 8 == 0;
     hipStream_t s = as_stream(stream);
 
     // D = 128 or 64 with 16-byte rows: the MFMA kernels.  D = 128 runs on

@@ -272,6 +272,49 @@ def test_flash_full_config(gpu, oracle):
 
 
 @pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("scale", [1.0, 0.6, 0.05])
+@pytest.mark.parametrize("L", [300, 512])
+def test_flash_d128_scales(gpu, oracle, causal, scale, L):
+    """The D = 128 kernel folds scale * log2(e) into Q^T when it is at most 1 (0.6, 0.05:
+    P = exp2 of the accumulator, the running maximum entering as a bias k-step) and
+    multiplies in fp32 otherwise (1.0: scale * log2(e) = 1.44)."""
+    lh = gpu
+    E, H, B = 128, 2, 1
+    announce(f"flash D=128 scale={scale} S={L} causal={causal}")
+    Q, K, V = attn_inputs(lh, E, L, H, B, cfg=11)
+    O = lh.HIPDeviceArray("f16", (E, L, H, B))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, scale=scale, causal=causal)
+    rows = np.unique(np.concatenate([np.arange(0, L, 3), [L - 1]]))
+    check_heads(oracle, Q, K, V, O, scale, causal, [(0, 0), (0, 1)], rows)
+    assert not np.isnan(O.to_numpy()).any()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_d128_maximum_beyond_fp16(gpu, oracle, causal):
+    """Scores whose running maximum (in base-2 units) lies beyond +-60000, where the bias
+    k-step cannot carry it in fp16: the wavefront switches to the fp32 path.  Scores are
+    exact in fp32 (integers): q0 = k0 = 256 plus small integer parts, so every score is
+    65536 + q1 k1 with q1, k1 in 0..3 and the softmax stays well conditioned."""
+    lh = gpu
+    E, L, H, B = 128, 384, 2, 1
+    announce(f"flash D=128 maximum beyond fp16 causal={causal}")
+    rng = np.random.default_rng(21)
+    q = np.zeros((E, L, H, B), np.float16)
+    k = np.zeros((E, L, H, B), np.float16)
+    q[0], k[0] = 256, 256
+    q[1] = rng.integers(0, 4, (L, H, B))
+    k[1] = rng.integers(0, 4, (L, H, B))
+    v = rng.standard_normal((E, L, H, B)).astype(np.float16)
+    Q, K, V = (lh.HIPDeviceArray.from_numpy(np.asfortranarray(a), "f16") for a in (q, k, v))
+    O = lh.HIPDeviceArray("f16", (E, L, H, B))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, scale=0.69, causal=causal)
+    check_heads(oracle, Q, K, V, O, 0.69, causal, [(0, 0), (0, 1)], np.arange(L))
+    assert not np.isnan(O.to_numpy()).any()
+
+
+@pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("E,L", [(128, 300), (64, 512)])
 def test_flash_strided_layouts(gpu, oracle, causal, E, L):
     """Q, K, V in (B, L, H, D) memory order (strides 1, D*H, D, D*H*L) and O with padded rows
@@ -299,4 +342,28 @@ def test_flash_strided_layouts(gpu, oracle, causal, E, L):
         got = o[idx].astype(np.float64)
         assert oracle.rel_frobenius(got, ref) <= 2e-3, (b, h)
         pad = o[(np.arange(8)[None, :] + E) + rows[:, None] * ost[1] + h * ost[2] + b * ost[3]]
+        assert np.all(pad.view(np.uint16) == 0xFFFF), "row padding of O written"
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_o_rows_8_byte_aligned(gpu, oracle, causal):
+    """O with a row stride of D + 4 elements (rows 8-byte aligned only): the D = 128 kernel
+    stores O rows in 8-byte pieces instead of staging whole 16-byte-aligned rows."""
+    lh = gpu
+    E, L, H, B = 128, 320, 2, 1
+    announce(f"flash D=128 O rows 8-byte aligned causal={causal}")
+    st = (1, E, E * L, E * L * H)
+    ost = (1, E + 4, (E + 4) * L, (E + 4) * L * H)
+    Q, K, V = attn_inputs(lh, E, L, H, B, cfg=12)
+    O = lh.HIPDeviceArray("f16", ((E + 4) * L * H * B,))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd_raw(Q.ptr, K.ptr, V.ptr, O.ptr, B, H, L, E, st, ost, None, causal)
+    q, k, v = (a.to_numpy().ravel(order="F") for a in (Q, K, V))
+    o = O.to_numpy()
+    rows = np.arange(L)
+    for h in range(H):
+        ref = oracle.attn_rows(q, k, v, L, E, st, 1 / math.sqrt(E), causal, 0, h, rows)
+        idx = np.arange(E)[None, :] + rows[:, None] * ost[1] + h * ost[2]
+        assert oracle.rel_frobenius(o[idx].astype(np.float64), ref) <= 2e-3, h
+        pad = o[(np.arange(4)[None, :] + E) + rows[:, None] * ost[1] + h * ost[2]]
         assert np.all(pad.view(np.uint16) == 0xFFFF), "row padding of O written"
