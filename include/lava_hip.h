@@ -377,26 +377,27 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
  * with the scale pointer in `extras`, :569-572):
  *   Y (M x N, fp32) = (X (M x K, fp16) * float(W (K x N, int8))) .* s[col] (fp16).
  * layout: bit0 X row-major, bit1 W row-major, bit2 Y row-major.  The weight-streaming
- * kernels take layout 7 with K a multiple of 32 and N a multiple of 64; any other layout
- * or shape runs on a generic kernel.  Wide N runs as one launch; narrower N splits K
- * across workgroups into a split-K workspace the library owns, one per (device, stream):
- * a call that grows it allocates (hipMalloc) and so is not capturable -- make one call of
- * the largest shape outside capture first.  Calls on one stream from several threads are
- * serialised around the workspace; lava_hip_stream_destroy frees it.  Results are
- * deterministic (fixed summation order). */
+ * kernels take layout 7 with K a multiple of 32 and N a multiple of 128; any other layout
+ * or shape runs on a generic kernel.  Every call is one launch.  Narrower N splits K across
+ * workgroups through a split-K workspace the library owns, one per (device, stream), whose
+ * last-arriving workgroup per column block adds the partial blocks: a call that grows it
+ * allocates (hipMalloc) and so is not capturable -- make one call of the largest shape
+ * outside capture first.  Calls on one stream from several threads are serialised around
+ * the workspace; lava_hip_stream_destroy frees it.  Results are deterministic (fixed
+ * summation order). */
 int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N, int64_t K,
                         int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream);
 
 /* lava_hip_gemm_w8a16 without any allocation: the same kernels and results (bit for bit),
- * with the split-K partial blocks in a fixed per-GPU device array of
- * LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES instead of a library-allocated workspace.  No
+ * with the split-K workspace (arrival counters and partial blocks) in a fixed per-GPU device
+ * array of LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES instead of a library-allocated one.  No
  * counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  No call makes a hipMalloc,
  * hipFree or other allocating call; a shape whose plan needs more scratch than the array holds
  * is refused with LAVA_HIP_ERR_INVALID_ARG (no plan of the split rule does).  Every call on one
  * GPU shares that GPU's array: calls that overlap on one GPU (two streams, two threads) race
  * and must be serialised by the caller. */
-#define LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES ((size_t)2 << 20)
+#define LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES (((size_t)2 << 20) + 4096)
 int lava_hip_gemm_w8a16_noalloc(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N,
                                 int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream);
 

@@ -15,16 +15,15 @@
 //    transpose (v_perm_b32) and an exact int8 -> fp16 conversion
 //    (0x6400 | (w ^ 0x80) is the fp16 value 1152 + w; subtract 1152);
 //  * X (16 x 32 per step, fp16) is the A operand, read straight from global/L2;
-//  * 4 wavefronts per workgroup split the workgroup's K range and reduce through
+//  * 8 wavefronts per workgroup split the workgroup's K range and reduce through
 //    LDS; to occupy every CU (N / 128 column blocks alone leave most of them idle)
-//    `splits` workgroups split K further, each writing its partial block, and a
-//    second small kernel on the same stream adds the splits in a fixed order,
-//    applies s[c] and writes Y -- deterministic, and free of the device-scope
-//    fences a last-arriver reduction needs (on a multi-XCD part each such fence
-//    writes back the XCD's L2, which cost ~7x the whole weight stream);
+//    `splits` workgroups split K further.  Each writes its (scaled) partial block to a
+//    workspace and counts itself in at a per-block arrival counter; the last of the
+//    `splits` workgroups adds the partial blocks in split order (fixed: deterministic)
+//    and writes Y, and resets the counter for the next call -- one launch, no second
+//    reduction kernel;
 //  * the weight rows of up to W8_DEPTH K steps are in flight ahead of the MFMAs;
-//  * the scale multiply is the fused per-element epilogue (in the reduction when
-//    K is split).
+//  * the scale multiply is the fused per-element epilogue, applied to every partial.
 #include <hip/hip_runtime.h>
 
 #include <map>
@@ -38,7 +37,7 @@ namespace lava {
 
 constexpr int W8_COLS = 128;   // columns per workgroup
 constexpr int W8_KSTEP = 32;   // k per MFMA step
-constexpr int W8_WAVES = 4;
+constexpr int W8_WAVES = 8;
 constexpr int W8_DEPTH = 4;   // K steps of weights in flight per wavefront
 
 __device__ __forceinline__ uint32_t w8_pair(uint32_t lo_row, uint32_t hi_row, int byte) {
@@ -60,9 +59,9 @@ struct ScaleStrided {
 // total_steps)) of K.  KSTEPS > 0: the host guarantees exactly KSTEPS each, fully
 // unrolled; KSTEPS == 0: any count (zero included), in unrolled groups of W8_DEPTH.
 template <int KSTEPS>
-__global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
+__global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
                                                     const f16* __restrict__ scale, float* __restrict__ Y,
-                                                    float* __restrict__ partial, int M, int N, int64_t ldx,
+                                                    float* partial, unsigned* counters, int M, int N, int64_t ldx,
                                                     int64_t ldw, int64_t ldy, int splits, int ks, int total_steps) {
     __shared__ __attribute__((aligned(16))) float red[W8_WAVES][16][W8_COLS];
 
@@ -154,44 +153,58 @@ __global__ void __launch_bounds__(256) w8a16_kernel(const f16* __restrict__ X, c
     }
     __syncthreads();
 
-    // workgroup sum over the 4 wavefronts: thread -> (row, 8 consecutive columns)
+    // workgroup sum over the wavefronts: thread -> (row, 4 consecutive columns)
     const int tid = threadIdx.x;
-    const int row = tid >> 4, c8 = (tid & 15) * 8;
-    float v[8];
+    const int row = tid >> 5, c4 = (tid & 31) * 4;
+    f32x4 v;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        v[i] = ((red[0][row][c8 + i] + red[1][row][c8 + i]) + red[2][row][c8 + i]) + red[3][row][c8 + i];
-
+    for (int i = 0; i < 4; ++i) {
+        float a = red[0][row][c4 + i];
+#pragma unroll
+        for (int ww = 1; ww < W8_WAVES; ++ww) a += red[ww][row][c4 + i];
+        v[i] = a;
+    }
     const int grow = m0 + row;
     if (splits > 1) {
-        // partial block of this split: [split][mb * 16 + row][N], summed by w8a16_reduce_kernel
-        float* mine = partial + (((int64_t)split * gridDim.z + mb) * 16 + row) * N + n0 + c8;
+        // Partial block of this split, [split][mb * 16 + row][N].  The stores are agent-scope
+        // atomic (coherent across the XCDs' L2 caches, written through to memory) and complete
+        // (vmcnt 0) before the workgroup barrier; one thread then counts the workgroup in.
+        // The last of the `splits` arrivals reads the others' blocks with agent-scope atomic
+        // loads, adds all of them in split order and resets the counter for the next call.
+        const int64_t rows_pad = (int64_t)gridDim.z * 16;
+        float* mine = partial + ((int64_t)split * rows_pad + (int64_t)mb * 16 + row) * N + n0 + c4;
 #pragma unroll
-        for (int i = 0; i < 8; i += 4) *reinterpret_cast<float4*>(mine + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
-        return;
+        for (int i = 0; i < 4; ++i) __hip_atomic_store(mine + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        __shared__ int last;
+        if (tid == 0) {
+            unsigned* cnt = counters + (int64_t)mb * gridDim.x + cb;
+            const unsigned before = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = before == (unsigned)splits - 1u;
+            if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last) return;
+        f32x4 y = {0.f, 0.f, 0.f, 0.f};
+        for (int sp = 0; sp < splits; ++sp) {
+            f32x4 pv;
+            if (sp == split) {
+                pv = v;
+            } else {
+                const float* other = partial + ((int64_t)sp * rows_pad + (int64_t)mb * 16 + row) * N + n0 + c4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) pv[i] = __hip_atomic_load(other + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            y += pv;
+        }
+        v = y;
     }
     if (grow < M) {
-        float* yp = Y + (int64_t)grow * ldy + n0 + c8;
+        float* yp = Y + (int64_t)grow * ldy + n0 + c4;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) yp[i] = v[i];
+        for (int i = 0; i < 4; ++i) yp[i] = v[i];
     }
-}
-
-// Y[r, c] = the sum over splits (in split order) of the scaled partial blocks; 4 columns per thread.
-__global__ void __launch_bounds__(256) w8a16_reduce_kernel(const float* __restrict__ partial, float* __restrict__ Y,
-                                                           int M, int N, int64_t ldy, int splits, int64_t rows_pad) {
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;   // (row, 4-column group)
-    const int64_t groups = N / 4;
-    if (idx >= (int64_t)M * groups) return;
-    const int64_t r = idx / groups, c = (idx % groups) * 4;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < splits; ++sp) {
-        const f32x4 p = *reinterpret_cast<const f32x4*>(partial + ((int64_t)sp * rows_pad + r) * N + c);
-        acc[0] += p[0]; acc[1] += p[1]; acc[2] += p[2]; acc[3] += p[3];
-    }
-    float* yp = Y + r * ldy + c;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) yp[i] = acc[i];
 }
 
 // Any layout, any shape: one thread per output element, fp32 sums.
@@ -214,12 +227,20 @@ __global__ void w8a16_generic_kernel(const f16* __restrict__ X, const int8_t* __
 // ---- launch planning ----------------------------------------------------------------------
 enum W8Path { W8_GENERIC = 0, W8_SPLIT = 1 };
 
+// Arrival counters at the front of a split-K workspace: the split rule keeps splits * column
+// blocks * row blocks <= 256 with splits >= 2, so at most 128 counters are ever in use.
+constexpr size_t W8_COUNTER_BYTES = 4096;
+static_assert(W8_COUNTER_BYTES >= 128 * sizeof(unsigned), "counter region");
+
 struct W8Plan {
     W8Path path = W8_GENERIC;
     int64_t cblocks = 0, mblocks = 0, total_steps = 0, ks = 0;
     int splits = 1;
     int ksteps = 0;              // the per-wavefront step count of an unrolled instance, or 0
-    size_t scratch_bytes = 0;    // split-K partial blocks (W8_SPLIT with splits > 1)
+    // split-K workspace (W8_SPLIT with splits > 1): the arrival counters (one per column and
+    // row block, zero between calls) in the first counter_bytes, then the partial blocks
+    size_t counter_bytes = 0;
+    size_t scratch_bytes = 0;
 };
 
 static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
@@ -235,46 +256,49 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
     p.cblocks = N / W8_COLS;
     // split K (up to 16 ways; the partial blocks cost 8 * splits bytes per output element of
     // extra traffic) while the grid still fits the 256 CUs in one round, keeping >= 4 steps per
-    // wavefront: at 16 x 4096 . 4096 x 14336 the 224-workgroup grid (2 splits) streams ~6 %
-    // faster than the 448-workgroup one (4 splits), and 1 split (112) or 8 (896) are 20 % slower
+    // wavefront: at 16 x 4096 . 4096 x 14336 the 224-workgroup grid (2 splits) streams faster
+    // than the 448-workgroup one (4 splits), and 1 split (112 workgroups) is ~20 % slower
     while (p.splits < 16 && p.cblocks * p.mblocks * p.splits * 2 <= 256 &&
            p.total_steps / (W8_WAVES * p.splits * 2) >= 4)
         p.splits *= 2;
     p.ks = (p.total_steps + W8_WAVES * p.splits - 1) / (W8_WAVES * p.splits);
     p.ksteps = p.ks * W8_WAVES * p.splits == p.total_steps ? (int)p.ks : 0;   // unrolled instances need equal shares
-    if (p.splits > 1) p.scratch_bytes = (size_t)p.splits * (size_t)p.mblocks * 16 * (size_t)N * sizeof(float);
+    if (p.splits > 1) {
+        // the counters keep a fixed place at the front of a workspace that calls of other
+        // shapes reuse: every counter is zero between calls, and no partial block covers one
+        p.counter_bytes = W8_COUNTER_BYTES;
+        p.scratch_bytes = p.counter_bytes + (size_t)p.splits * (size_t)p.mblocks * 16 * (size_t)N * sizeof(float);
+    }
     return p;
 }
 
 template <int KS>
 static void launch_split_ks(const W8Plan& p, const void* X, const void* W, const void* scale, void* Y, float* partial,
-                            int64_t M, int64_t N, int64_t ldx, int64_t ldw, int64_t ldy, hipStream_t s) {
-    hipLaunchKernelGGL(w8a16_kernel<KS>, dim3((unsigned)p.cblocks, (unsigned)p.splits, (unsigned)p.mblocks), dim3(256),
-                       0, s, (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, partial, (int)M, (int)N,
-                       ldx, ldw, ldy, p.splits, (int)p.ks, (int)p.total_steps);
+                            unsigned* counters, int64_t M, int64_t N, int64_t ldx, int64_t ldw, int64_t ldy,
+                            hipStream_t s) {
+    hipLaunchKernelGGL(w8a16_kernel<KS>, dim3((unsigned)p.cblocks, (unsigned)p.splits, (unsigned)p.mblocks),
+                       dim3(64 * W8_WAVES), 0, s, (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, partial,
+                       counters, (int)M, (int)N, ldx, ldw, ldy, p.splits, (int)p.ks, (int)p.total_steps);
 }
 
-// Enqueues the plan's kernels on `s`.  `partial` holds p.scratch_bytes when p.splits > 1.
-static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const void* scale, void* Y, float* partial,
+// Enqueues the plan's kernel on `s`.  `ws` holds p.scratch_bytes when p.splits > 1, its
+// counters zero.
+static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const void* scale, void* Y, void* ws,
                         int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout,
                         hipStream_t s) {
     if (p.path == W8_SPLIT) {
+        unsigned* counters = static_cast<unsigned*>(ws);
+        float* partial = ws ? reinterpret_cast<float*>(static_cast<char*>(ws) + p.counter_bytes) : nullptr;
         switch (p.ksteps) {   // the usual counts fully unrolled, any other in groups of W8_DEPTH
-        case 1: launch_split_ks<1>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
-        case 2: launch_split_ks<2>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
-        case 4: launch_split_ks<4>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
-        case 8: launch_split_ks<8>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
-        case 16: launch_split_ks<16>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
-        case 32: launch_split_ks<32>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
-        default: launch_split_ks<0>(p, X, W, scale, Y, partial, M, N, ldx, ldw, ldy, s); break;
+        case 1: launch_split_ks<1>(p, X, W, scale, Y, partial, counters, M, N, ldx, ldw, ldy, s); break;
+        case 2: launch_split_ks<2>(p, X, W, scale, Y, partial, counters, M, N, ldx, ldw, ldy, s); break;
+        case 4: launch_split_ks<4>(p, X, W, scale, Y, partial, counters, M, N, ldx, ldw, ldy, s); break;
+        case 8: launch_split_ks<8>(p, X, W, scale, Y, partial, counters, M, N, ldx, ldw, ldy, s); break;
+        case 16: launch_split_ks<16>(p, X, W, scale, Y, partial, counters, M, N, ldx, ldw, ldy, s); break;
+        case 32: launch_split_ks<32>(p, X, W, scale, Y, partial, counters, M, N, ldx, ldw, ldy, s); break;
+        default: launch_split_ks<0>(p, X, W, scale, Y, partial, counters, M, N, ldx, ldw, ldy, s); break;
         }
         LAVA_LAUNCH_CHECK("w8a16_kernel");
-        if (p.splits > 1) {
-            const int64_t threads = M * (N / 4);
-            hipLaunchKernelGGL(w8a16_reduce_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
-                               (const float*)partial, (float*)Y, (int)M, (int)N, ldy, p.splits, p.mblocks * 16);
-            LAVA_LAUNCH_CHECK("w8a16_reduce_kernel");
-        }
         return LAVA_HIP_OK;
     }
     // any layout, any shape
@@ -305,8 +329,8 @@ static int check_w8a16_args(const void* X, const void* W, const void* scale, con
 
 // ---- the split-K workspace of lava_hip_gemm_w8a16 ------------------------------------------
 // One buffer per (device, stream), owned by the library.  The lock is held from the
-// workspace lookup through both launches, so the kernel pair of one call is enqueued
-// without another thread's pair between its halves on the same stream.  A buffer that
+// workspace lookup through the launch, so calls from several threads on one stream use the
+// workspace one after another (stream order).  A buffer that
 // grows is retired, not freed -- work already enqueued or a graph captured earlier may
 // still use it -- and every buffer of a stream is freed by lava_hip_stream_destroy
 // (after the stream drains); buffers of the NULL stream live until the process ends.
@@ -336,20 +360,23 @@ void w8a16_release_stream(void* stream) {
 }
 
 // ---- the no-allocation entry's scratch --------------------------------------------------------
-// lava_hip_gemm_w8a16_noalloc keeps its split-K partial blocks in this fixed device array, one
-// copy per GPU, reached through the address hipGetSymbolAddress returns for it on that GPU (the
-// array's name is only a host-side stand-in).  The split rule keeps a grid at <= 256 workgroups,
-// each writing one 16 x 128 fp32 block, so no plan needs more than 2 MiB.  Every block a
-// reduction reads is written by the same call first: nothing needs clearing between calls.
-static_assert(LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES >= 256 * 16 * W8_COLS * sizeof(float),
+// lava_hip_gemm_w8a16_noalloc keeps its split-K workspace (arrival counters, then partial
+// blocks) in this fixed device array, one copy per GPU, reached through the address
+// hipGetSymbolAddress returns for it on that GPU (the array's name is only a host-side
+// stand-in).  The split rule keeps a grid at <= 256 workgroups, each writing one 16 x 128 fp32
+// block, so no plan needs more than the counters plus 2 MiB.  The counters are cleared by a
+// fill kernel on the first call per device; every call leaves them at zero, and every block a
+// reduction reads is written by the same call first.
+static_assert(LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES >= W8_COUNTER_BYTES + 256 * 16 * W8_COLS * sizeof(float),
               "the no-allocation scratch must hold the largest split-K plan");
 static __device__ __attribute__((used)) __align__(256) float scratch[LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES / sizeof(float)];
 constexpr int W8_MAX_DEVICES = 64;
 static std::mutex g_scratch_mutex;
-static float* g_scratch_ptr[W8_MAX_DEVICES];
+static void* g_scratch_ptr[W8_MAX_DEVICES];
 
-// The device address of `scratch` on the current device, looked up once per device.
-static int scratch_for_device(float** out) {
+// The device address of `scratch` on the current device, looked up (and its counters cleared,
+// on `stream`) once per device.
+static int scratch_for_device(void** out, void* stream) {
     int dev = 0;
     LAVA_HIP_TRY(hipGetDevice(&dev));
     LAVA_REQUIRE(dev >= 0 && dev < W8_MAX_DEVICES, LAVA_HIP_ERR_UNSUPPORTED,
@@ -359,7 +386,9 @@ static int scratch_for_device(float** out) {
         void* ptr = nullptr;
         LAVA_HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
         LAVA_REQUIRE(ptr != nullptr, LAVA_HIP_ERR_HIP, "gemm_w8a16_noalloc: no device address for the scratch array");
-        g_scratch_ptr[dev] = static_cast<float*>(ptr);
+        const int rc = lava_hip_fill_bytes(ptr, 0, W8_COUNTER_BYTES, stream);
+        if (rc != LAVA_HIP_OK) return rc;
+        g_scratch_ptr[dev] = ptr;
     }
     *out = g_scratch_ptr[dev];
     return LAVA_HIP_OK;
@@ -385,11 +414,17 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
     if (ws.bytes < p.scratch_bytes) {
         void* buf = nullptr;
         LAVA_HIP_TRY(hipMalloc(&buf, p.scratch_bytes));
+        // the arrival counters start at zero (every call leaves them at zero)
+        rc = lava_hip_fill_bytes(buf, 0, W8_COUNTER_BYTES, stream);
+        if (rc != LAVA_HIP_OK) {
+            (void)hipFree(buf);
+            return rc;
+        }
         if (ws.buf) ws.retired.push_back(ws.buf);
         ws.buf = buf;
         ws.bytes = p.scratch_bytes;
     }
-    return launch_w8a16(p, X, W, scale, Y, static_cast<float*>(ws.buf), M, N, K, ldx, ldw, ldy, layout, s);
+    return launch_w8a16(p, X, W, scale, Y, ws.buf, M, N, K, ldx, ldw, ldy, layout, s);
 }
 
 extern "C" int lava_hip_gemm_w8a16_noalloc(const void* X, const void* W, const void* scale, void* Y, int64_t M,
@@ -404,10 +439,10 @@ extern "C" int lava_hip_gemm_w8a16_noalloc(const void* X, const void* W, const v
              (long long)M, (long long)N, (long long)K);
     rc = lava_hip_init();
     if (rc != LAVA_HIP_OK) return rc;
-    float* partial = nullptr;
+    void* ws = nullptr;
     if (p.scratch_bytes > 0) {
-        rc = scratch_for_device(&partial);
+        rc = scratch_for_device(&ws, stream);
         if (rc != LAVA_HIP_OK) return rc;
     }
-    return launch_w8a16(p, X, W, scale, Y, partial, M, N, K, ldx, ldw, ldy, layout, as_stream(stream));
+    return launch_w8a16(p, X, W, scale, Y, ws, M, N, K, ldx, ldw, ldy, layout, as_stream(stream));
 }

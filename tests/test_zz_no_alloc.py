@@ -35,8 +35,8 @@ def _both(lh, M, N, K, cfg):
 
 def test_noalloc_matches_allocating_entry_twice(gpu, oracle):
     lh = gpu
-    # split-K shapes (8 and 4 splits): the partial blocks go through the static scratch;
-    # the second call is smaller and reuses the array the first one left behind
+    # split-K shapes (4 and 2 splits): the arrival counters and partial blocks live in the
+    # static scratch; the second call is smaller and reuses the array the first one left behind
     for i, (M, N, K) in enumerate([(16, 4096, 4096), (8, 2048, 2048)]):
         announce(f"w8a16_noalloc call {i + 1}: M={M} N={N} K={K}")
         X, W, s, ref_entry, got = _both(lh, M, N, K, 40 + i)
@@ -47,7 +47,7 @@ def test_noalloc_matches_allocating_entry_twice(gpu, oracle):
 
 def test_noalloc_without_split_and_argument_errors(gpu, oracle):
     lh = gpu
-    announce("w8a16_noalloc: one split (no scratch), ragged generic shape, bad arguments")
+    announce("w8a16_noalloc: the headline shape (2 splits), ragged generic shape, bad arguments")
     for (M, N, K), cfg in (((16, 14336, 4096), 42), ((3, 7, 5), 43)):
         X, W, s, ref_entry, got = _both(lh, M, N, K, cfg)
         np.testing.assert_array_equal(got, ref_entry)
