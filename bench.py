@@ -9,13 +9,16 @@ tensors of the parity tests, generated on the device and resident in HBM
 before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
-                  [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|
+                  [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
                               gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|copy]
 
-A step is one kernel launch over the whole problem.  Kernel time is the median
-of the K per-launch times that HIP events recorded on the launch stream give
-(`kernel_ms`; the mean is `kernel_ms_mean`); wall time comes from a synchronised
-host clock around the same region.
+A step is one kernel launch over the whole problem (for the W8A16 and 256^3
+workloads, whose kernels take microseconds, 10 back-to-back launches:
+`launches_per_step`).  Kernel time is the median over the K steps of the
+per-launch time that HIP events recorded on the launch stream give (`kernel_ms`;
+the mean is `kernel_ms_mean`); wall time comes from a synchronised host clock
+around the same region.  `vendor_bf16` times the vendor library (hipBLASLt,
+through torch) on the headline product, for comparison only.
 
 Clock settling: an idle MI355X holds a low engine clock (rocm-smi shows sclk at
 114-811 MHz) and needs about half a second of sustained load to reach its
@@ -204,6 +207,38 @@ def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6):
     return nbytes, kern_ms, wall_ms
 
 
+def bench_vendor_bf16(steps, warmup, n=8192):
+    """The vendor library on the headline product, for the counter comparison: hipBLASLt
+    through torch.mm(A, B, out_dtype=float32), A row-major, B column-major (the transposed
+    view of a row-major B^T), bf16 inputs, fp32 C."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(1)
+    A = (torch.rand(n, n, device="cuda", generator=g) * 2 - 1).to(torch.bfloat16)
+    Bt = (torch.rand(n, n, device="cuda", generator=g) * 2 - 1).to(torch.bfloat16)
+    B = Bt.t()
+    C = torch.empty(n, n, device="cuda", dtype=torch.float32)
+
+    def launch():
+        torch.mm(A, B, out_dtype=torch.float32, out=C)
+
+    t_end = time.perf_counter() + SETTLE_S[0]
+    while time.perf_counter() < t_end:
+        launch()
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record()
+    for i in range(steps):
+        launch()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    TIMED_MEAN_MS[0] = sum(per) / steps
+    return 2.0 * n ** 3, statistics.median(per)
+
+
 # ---------------------------------------------------------------- CPU baseline
 def cpu_baseline_gemm(n=8192, budget_s=20.0):
     """The oracle's fp32-accumulate GEMM (a port of the tile loop, not the Lava
@@ -239,7 +274,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
-                             "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "copy"])
+                             "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "copy",
+                             "vendor_bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -252,15 +288,26 @@ def main():
               f"(asked for --gpus {args.gpus}, WORLD_SIZE={world}). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    import lava_hip as lh
-    lh.init()
-    s = lh.Stream()
-    stream = s.handle
     K, W = args.steps, args.warmup
     out = {"metric": METRIC, "n_gpus": 1, "steps": K, "warmup": W, "clock_settle_s": SETTLE_S[0],
            "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "data": "synthetic (seeded: uniform[-1,1] GEMM inputs, normal(0,1) Q/K/V), "
                                          "generated on the device before timing"}
+    if args.workload == "vendor_bf16":
+        # torch brings its own HIP runtime: it runs in a process that has not loaded liblava_hip.so
+        flop, kms = bench_vendor_bf16(K, W)
+        out.update({"value": round(flop / (kms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(kms, 4),
+                    "dtype": "bf16", "config": {"workload": "vendor reference: hipBLASLt (torch.mm, out_dtype fp32) on "
+                                                            "the headline product, bf16 8192^3, A row-major, B column-major"},
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+        print(json.dumps(out), flush=True)
+        return
+
+    import lava_hip as lh
+    lh.init()
+    s = lh.Stream()
+    stream = s.handle
 
     if args.workload in ("headline", "gemm_bf16"):
         flop, kms, wms = bench_gemm(lh, "bf16", 8192, K, W, stream, 1)

@@ -328,12 +328,13 @@ __global__ void __launch_bounds__(256, 1)
     }
 
     // ---- epilogue through LDS, so that global stores are whole 512-byte row runs.
-    // acc[i][j] register r of lane l is C[m][n] with m = 128 wm + 32 i + l % 32 and
-    // n = 128 wn + 32 j + 8 (r / 4) + 4 (l / 32) + r % 4 within the tile.  Each wave
-    // stages 32 rows x 128 columns at a time (one i) in its own 16.5 KB of the idle
-    // stage buffers (4 waves: 66 KB of the 128 KB), rows padded to 528 bytes so the
-    // 32 rows of one column group land on distinct banks; then reads whole rows back:
-    // lanes 0..31 and 32..63 each cover one 512-byte row per instruction.
+    // acc[I][j] register r of lane l is C[m][n] with m = 128 wm + 16 I + l % 16 and
+    // n = 128 wn + 16 j + 4 (l / 16) + r within the tile (the 16x16 MFMA accumulator
+    // map, I and j = 0..7).  Each wave stages 32 rows x 128 columns at a time (a row
+    // quarter i: I = 2 i, 2 i + 1) in its own 16.5 KB of the idle stage buffers (4 waves:
+    // 66 KB of the 128 KB), rows padded to 528 bytes so the 32 rows of one column group
+    // land on distinct banks; then reads whole rows back: lanes 0..31 and 32..63 each
+    // cover one 512-byte row per instruction.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     constexpr int EP_PITCH = 128 * 4 + 16;
