@@ -291,6 +291,32 @@ def test_flash_d128_scales(gpu, oracle, causal, scale, L):
 
 
 @pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("scale", [0.0, -0.0883883])
+@pytest.mark.parametrize("E", [128, 64])
+def test_flash_scale_zero_and_negative(gpu, oracle, causal, scale, E):
+    """A softmax scale of zero (every visible key weighs the same) or below zero (the
+    scores change sign, so the running maximum is taken over negated products): D = 128
+    runs on the score/output kernel (the scale folds into Q^T), D = 64 on the generic
+    kernel; both against the oracle."""
+    lh = gpu
+    L, H, B = 256, 2, 1
+    announce(f"flash D={E} scale={scale} S={L} causal={causal}")
+    Q, K, V = attn_inputs(lh, E, L, H, B, cfg=13)
+    O = lh.HIPDeviceArray("f16", (E, L, H, B))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, scale=scale, causal=causal)
+    rows = np.unique(np.concatenate([np.arange(0, L, 5), [L - 1]]))
+    check_heads(oracle, Q, K, V, O, scale, causal, [(0, 0), (0, 1)], rows)
+    o = O.to_numpy()
+    assert not np.isnan(o).any()
+    if scale == 0.0:
+        # uniform weights: the first query sees only key 0 (causal) or the mean of all keys
+        v = V.to_numpy().astype(np.float64)
+        want = v[:, 0, :, :] if causal else v.mean(axis=1)
+        np.testing.assert_allclose(o[:, 0, :, :].astype(np.float64), want, rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize("causal", [True, False])
 def test_flash_d128_maximum_beyond_fp16(gpu, oracle, causal):
     """Scores whose running maximum (in base-2 units) lies beyond +-60000, where the bias
     k-step cannot carry it in fp16: the wavefront switches to the fp32 path.  Scores are
