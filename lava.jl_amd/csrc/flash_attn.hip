@@ -54,6 +54,7 @@ struct FaParams {
     float scale_log2;        // softmax scale * log2(e)
     int causal;
     int o16;                 // O and its strides allow 16-byte row stores
+    int D;                   // head dimension (the score/output kernel zero-pads it to 128)
 };
 
 // Workgroup -> (batch * head, query block).  Workgroups are dispatched round-robin
@@ -564,13 +565,21 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
     // resource of a block starts at its first row and ends at the sequence's end, so rows
     // at or past S read zero.  Blocks past the end re-read the last one (every iteration
     // issues the same DMAs).
+    // A head dimension D < 128 (a multiple of 8) runs zero-padded to 128: a lane whose logical
+    // chunk lies at or past D / 8 takes an offset beyond every buffer resource's range, so its
+    // DMA writes zero into LDS -- zero Q and K columns add nothing to the scores, and the O
+    // columns that the zero V columns produce are not stored.
     const uint32_t row_bytes = (uint32_t)(p.sl * 2);
+    const int dch = p.D >> 3;                  // 16-byte chunks of a row that hold data
+    auto chunk_ofs = [&](int row, int c) -> uint32_t {
+        return c < dch ? (uint32_t)row * row_bytes + 16u * (uint32_t)c : 0x80000000u;
+    };
     uint32_t dv_k[DPT], dv_v[DPT];
 #pragma unroll
     for (int i = 0; i < DPT; ++i) {
         const int row = 16 * pr + 4 * i + lane / CH;
-        dv_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CH) ^ (row & 15));
-        dv_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CH) ^ (4 * (row & 3)));
+        dv_k[i] = chunk_ofs(row, (lane % CH) ^ (row & 15));
+        dv_v[i] = chunk_ofs(row, (lane % CH) ^ (4 * (row & 3)));
     }
     auto dma_tile = [&](bool is_k, int j) __attribute__((always_inline)) {
         const int src = j < nkb ? j : nkb - 1;
@@ -612,7 +621,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int row = 4 * i + lane / CH;
-                const uint32_t v = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CH) ^ (row & 15));
+                const uint32_t v = chunk_ofs(row, (lane % CH) ^ (row & 15));
                 f3_dma16(rs, v, 0u, __builtin_amdgcn_readfirstlane(qst[i / 8] + (uint32_t)((4 * i) % 32) * RB));
             }
         }
@@ -906,7 +915,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
             for (int i = 0; i < 16; ++i) {
                 const int row = 4 * i + lane / CH, c = lane % CH;
                 const f16x8 v = *(const lds_f16x8*)(uintptr_t)(ost[i / 8] + (uint32_t)((row % 32) * RB + ((c ^ (row & 15)) << 4)));
-                if (q0 + row < p.S) *reinterpret_cast<f16x8*>(Ob + (int64_t)(q0 + row) * p.osl + 8 * c) = v;
+                if (q0 + row < p.S && c < dch) *reinterpret_cast<f16x8*>(Ob + (int64_t)(q0 + row) * p.osl + 8 * c) = v;
             }
         } else {
 #pragma unroll
@@ -921,7 +930,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                         const int d = 32 * dt + 8 * g4 + 4 * h;
                         f16x4 v = {(f16)(o[dt][qh][4 * g4 + 0] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 1] * inv[qh]),
                                    (f16)(o[dt][qh][4 * g4 + 2] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 3] * inv[qh])};
-                        *reinterpret_cast<f16x4*>(orow + d) = v;
+                        if (d < p.D) *reinterpret_cast<f16x4*>(orow + d) = v;
                     }
             }
         }
@@ -1001,6 +1010,7 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     p.scale_log2 = scale * 1.4426950408889634f;
     p.causal = causal != 0;
     p.o16 = aligned(O, 16) && os[1] % 8 == 0 && os[2] % 8 == 0 && os[3] % 8 == 0;
+    p.D = (int)D;
     hipStream_t s = as_stream(stream);
 
     // D = 128 or 64 with 16-byte rows: the MFMA kernels.  D = 128 runs on flash_fwd5_kernel
@@ -1010,17 +1020,17 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     // zero-filled and masked).  LAVA_HIP_ATTN_KERNEL=3 in the environment runs D = 128 with a
     // positive scale on flash_fwd3_kernel as well (a comparison switch; both are
     // parity-tested).  Everything else runs on flash_generic_kernel.
-    bool lay_ok = D == FA_D || D == 64;
+    bool lay_ok = D >= 8 && D <= FA_D && D % 8 == 0 && strides[0] == 1 && os[0] == 1;
     for (int i = 1; i < 4; ++i) lay_ok = lay_ok && strides[i] % 8 == 0 && os[i] % 4 == 0;
     lay_ok = lay_ok && aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8) &&
              S * strides[1] * 2 < ((int64_t)1 << 31);
     const int64_t blocks3 = ((S + F3_BQ - 1) / F3_BQ) * H * B;
     const int64_t blocks5 = ((S + F5_BQ - 1) / F5_BQ) * H * B;
     const char* sel = getenv("LAVA_HIP_ATTN_KERNEL");
-    const bool want3 = sel && sel[0] == '3' && scale > 0.f;
-    const bool fast5 = lay_ok && D == FA_D && !want3 && blocks5 <= 0x7fffffff;
-    const bool fast3 = lay_ok && scale > 0.f && (D == 64 || want3) && blocks3 <= 0x7fffffff;
-    if (fast5) {
+    const bool want3 = sel && sel[0] == '3';
+    const bool fast3 = lay_ok && scale > 0.f && (D == 64 || (D == FA_D && want3)) && blocks3 <= 0x7fffffff;
+    const bool fast5 = lay_ok && !fast3 && blocks5 <= 0x7fffffff;
+    if (fast5) {   // any D <= 128, a multiple of 8 (zero-padded to 128)
         if (p.causal)
             hipLaunchKernelGGL((flash_fwd5_kernel<true>), dim3((unsigned)blocks5), dim3(128 * F5_PAIRS), 0, s, p);
         else

@@ -227,15 +227,32 @@ def test_flash_fast_d64(gpu, oracle, causal, L):
     assert not np.isnan(O.to_numpy()).any()
 
 
-@pytest.mark.parametrize("E,L,causal", [(32, 200, True), (16, 32, True), (96, 130, False), (48, 100, False)])
+@pytest.mark.parametrize("E,L,causal", [(20, 200, True), (100, 130, False), (160, 100, True), (256, 64, False)])
 def test_flash_generic_path(gpu, oracle, E, L, causal):
-    """Head dims and sequence lengths outside the fast kernel's tiling."""
+    """Head dims the MFMA kernels do not take (not a multiple of 8, or above 128)."""
     lh = gpu
     announce(f"flash generic D={E} S={L} causal={causal}")
     Q, K, V = attn_inputs(lh, E, L, 2, 1)
     O = lh.HIPDeviceArray("f16", (E, L, 2, 1))
     lh.flash_attn_fwd(O, Q, K, V, scale=0.2, causal=causal)
     check_heads(oracle, Q, K, V, O, 0.2, causal, [(0, 0), (0, 1)], np.arange(L))
+
+
+@pytest.mark.parametrize("E,L,causal", [(32, 200, True), (16, 32, True), (96, 130, False), (48, 100, False),
+                                         (8, 257, True), (120, 300, False), (80, 512, True), (96, 1000, True)])
+def test_flash_padded_head_dims(gpu, oracle, E, L, causal):
+    """Head dimensions below 128 (multiples of 8) on the score/output kernel, zero-padded to
+    128: the padding columns of Q and K read zero and add nothing to the scores; those of O
+    are not written."""
+    lh = gpu
+    announce(f"flash padded D={E} S={L} causal={causal}")
+    Q, K, V = attn_inputs(lh, E, L, 2, 1)
+    O = lh.HIPDeviceArray("f16", (E, L, 2, 1))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, scale=0.2, causal=causal)
+    rows = np.arange(L) if L <= 300 else np.unique(np.concatenate([np.arange(0, L, 7), [L - 1]]))
+    check_heads(oracle, Q, K, V, O, 0.2, causal, [(0, 0), (0, 1)], rows)
+    assert not np.isnan(O.to_numpy()).any()
 
 
 def test_flash_golden(gpu):
@@ -341,7 +358,7 @@ def test_flash_d128_maximum_beyond_fp16(gpu, oracle, causal):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("E,L", [(128, 300), (64, 512)])
+@pytest.mark.parametrize("E,L", [(128, 300), (64, 512), (96, 300)])
 def test_flash_strided_layouts(gpu, oracle, causal, E, L):
     """Q, K, V in (B, L, H, D) memory order (strides 1, D*H, D, D*H*L) and O with padded rows
     (row stride D + 8): the fast kernel addresses every tensor through its strides."""
