@@ -5,8 +5,9 @@
 // Compute-bound shapes take the 256 x 256 tile kernel (gemm_tn_kernel.hpp) in any
 // operand layout for 16-bit types (K-contiguous operands read directly, M/N-contiguous
 // ones through transposing LDS reads) and with both operands K-contiguous for int8 --
-// whole tiles, or ragged extents with zero-clamped loads; the rest (small products,
-// extents that split a 16-byte chunk, other int8 layouts) the staged kernel.
+// whole tiles, or ragged extents with zero-clamped loads.  Products of at most 16 such
+// tiles take the 64 x 64 small-product kernel; the rest (extents that split a 16-byte
+// chunk, other int8 layouts) the staged kernel.
 #include <hip/hip_runtime.h>
 
 #include "gemm_kernels.hpp"
@@ -58,9 +59,13 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     }
     hipStream_t s = as_stream(stream);
     Acc* c = static_cast<Acc*>(C);
+    if (small_gemm_eligible<T>(a, b, M, N, K, lda, ldb, arow, brow))
+        return launch_gemm_small<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
     const int fit = tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
     if (fit != TN_NO)
         return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, fit == TN_RAGGED, arow, !brow);
+    LAVA_REQUIRE((N + 63) / 64 <= 0x7fffffff && (M + 63) / 64 <= 65535, LAVA_HIP_ERR_UNSUPPORTED,
+                 "%s: too many 64-row tiles for the staged kernel (M=%lld N=%lld)", name, (long long)M, (long long)N);
     return launch_gemm_staged<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
 }
 

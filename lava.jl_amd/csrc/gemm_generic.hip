@@ -6,6 +6,10 @@
 //    multiples (the clamp-to-zero of a TENSOR_CLAMP_CONSTANT load,
 //    src/vocabulary/tensor.jl:46-51).  It is the fallback behind the fast TN
 //    kernel and the path for small problems.
+//  * gemm_small_kernel: the products too small to fill the chip with 256 x 256
+//    tiles (16 or fewer of them, e.g. BASELINE's 256^3 fp16 case): 64 x 64 tiles,
+//    K in chunks of 512 bytes loaded with 16-byte loads, all in flight at once, the
+//    next chunk arriving in registers while this one is multiplied.
 //  * coopmat_tiles_kernel: the 16x16x16 subgroup-tile GEMM written in the
 //    vocabulary exactly as docs/src/device.md:81-88 writes it -- one wavefront per
 //    tile of C, fragments loaded straight from global memory.
@@ -96,6 +100,157 @@ __global__ void __launch_bounds__(256) gemm_staged_kernel(const T* __restrict__ 
         }
 }
 
+// 64 x 64 C tile per workgroup of 4 wavefronts (32 x 32 each: 2 x 2 MFMA 16x16 tiles).  K runs
+// in chunks of 512 bytes.  A chunk of one operand is 64 rows (m or n) x 512 bytes = 2048 16-byte
+// loads, 8 per thread, all issued before any is waited for; the next chunk's loads are in flight
+// while this chunk is multiplied.  LDS layouts:
+//  * a K-contiguous operand (A row-major, B column-major) is copied as loaded, [row][k], rows
+//    padded to 528 bytes so that a fragment read (16 rows x one 16-byte chunk) is conflict-free;
+//  * an M/N-contiguous 16-bit operand is copied as loaded too, [k][row] (128-byte rows padded to
+//    144), and its fragments are read with two ds_read_b64_tr_b16 (4 k-values of one column per
+//    lane each);
+//  * an M/N-contiguous int8 operand is transposed by byte stores into the [row][k] layout.
+// Host conditions (small_gemm_eligible): 16-byte aligned operands and leading dimensions, K a
+// multiple of EV when an operand is K-contiguous, M (N) a multiple of EV when A (B) is M (N)-
+// contiguous -- so every 16-byte chunk is wholly inside or wholly outside the matrix, and the
+// outside ones read as zero.
+template <typename T, bool AROW, bool BROW, typename OutT, bool EPI>
+__global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A, const T* __restrict__ B,
+                                                         OutT* __restrict__ C, int64_t M, int64_t N, int64_t K,
+                                                         int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi) {
+    using Acc = typename Mfma16<T>::acc_elem;
+    using AccV = typename Mfma16<T>::acc_t;
+    constexpr int EV = 16 / (int)sizeof(T);   // elements per 16-byte chunk
+    constexpr int KC = 512 / (int)sizeof(T);  // elements of K per chunk
+    constexpr int KE = Mfma16<T>::k;          // elements per MFMA k-step (64 bytes)
+    constexpr int PITCH = 528;                // [row][k] layout: LDS bytes per row
+    constexpr int PTR = 144;                  // [k][row] layout (16-bit types): LDS bytes per k
+    constexpr int JR = 64 / EV;               // 16-byte chunks across the 64 rows of an M/N-contiguous chunk
+    constexpr bool A_TR = !AROW && sizeof(T) == 2;   // A read through transposing LDS reads
+    constexpr bool B_TR = BROW && sizeof(T) == 2;
+    constexpr int SBYTES = (64 * PITCH > KC * PTR) ? 64 * PITCH : KC * PTR;
+    __shared__ __attribute__((aligned(16))) uint8_t As[SBYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[SBYTES];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+    const int wm = w >> 1, wn = w & 1;
+
+    // 16-byte chunk i (of 8) of this thread for the K-chunk at k0 of operand X, whose rows r0 ..
+    // r0 + 63 (m or n) are K-contiguous (kcont) or M/N-contiguous
+    auto load = [&](const T* X, auto kcont, int64_t ld, int64_t r0, int64_t rows, int64_t k0, uint4* reg) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = tid + 256 * i;
+            int64_t rr, kk;
+            const T* p;
+            if constexpr (decltype(kcont)::value) {
+                rr = r0 + (e >> 5);
+                kk = k0 + (int64_t)EV * (e & 31);
+                p = X + rr * ld + kk;
+            } else {
+                kk = k0 + e / JR;
+                rr = r0 + (int64_t)EV * (e % JR);
+                p = X + kk * ld + rr;
+            }
+            reg[i] = make_uint4(0, 0, 0, 0);
+            if (rr < rows && kk < K) reg[i] = *reinterpret_cast<const uint4*>(p);
+        }
+    };
+    auto store = [&](uint8_t* S, auto kcont, auto tr, const uint4* reg) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int e = tid + 256 * i;
+            if constexpr (decltype(kcont)::value) {
+                *reinterpret_cast<uint4*>(S + (e >> 5) * PITCH + 16 * (e & 31)) = reg[i];
+            } else if constexpr (decltype(tr)::value) {
+                *reinterpret_cast<uint4*>(S + (e / JR) * PTR + 16 * (e % JR)) = reg[i];
+            } else {
+                const int k = e / JR, j = e % JR;
+                const T* v = reinterpret_cast<const T*>(&reg[i]);
+#pragma unroll
+                for (int t = 0; t < EV; ++t) *reinterpret_cast<T*>(S + (EV * j + t) * PITCH + k * (int)sizeof(T)) = v[t];
+            }
+        }
+    };
+    // fragment of rows rb .. rb + 15 at k-step ks: lane (r, g) = (lane % 16, lane / 16) holds
+    // row rb + r, k 8 g .. 8 g + 7 of the step
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    auto frag = [&](const uint8_t* S, auto tr, int rb, int ks) -> uint4 {
+        if constexpr (decltype(tr)::value) {
+            // source lane (jj, q) = ((lane % 16) / 4, lane % 4) of group g points at k row
+            // 8 g + jj (+ 4), rows rb + 4 q .. + 3: output lane r gets 4 k-values of row rb + r
+            const int g = lane >> 4, jj = (lane & 15) >> 2, q = lane & 3;
+            const uint8_t* p0 = S + (ks * KE + 8 * g + jj) * PTR + 2 * (rb + 4 * q);
+            const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(p0));
+            const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(p0 + 4 * PTR));
+            return __builtin_bit_cast(uint4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        } else {
+            return *reinterpret_cast<const uint4*>(S + (rb + (lane & 15)) * PITCH + ks * 64 + (lane >> 4) * 16);
+        }
+    };
+    typedef std::integral_constant<bool, AROW> AK;    // A row-major: K-contiguous
+    typedef std::integral_constant<bool, !BROW> BK;   // B column-major: K-contiguous
+    typedef std::integral_constant<bool, A_TR> ATR;
+    typedef std::integral_constant<bool, B_TR> BTR;
+
+    AccV acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = AccV{0, 0, 0, 0};
+    uint4 ra[8], rb[8];
+    load(A, AK{}, lda, m0, M, 0, ra);
+    load(B, BK{}, ldb, n0, N, 0, rb);
+    for (int64_t k0 = 0; k0 < K; k0 += KC) {
+        store(As, AK{}, ATR{}, ra);
+        store(Bs, BK{}, BTR{}, rb);
+        __syncthreads();
+        if (k0 + KC < K) {   // the next chunk, in flight during this one's MFMAs
+            load(A, AK{}, lda, m0, M, k0 + KC, ra);
+            load(B, BK{}, ldb, n0, N, k0 + KC, rb);
+        }
+        const int64_t nks = min((int64_t)(KC / KE), (K - k0 + KE - 1) / KE);
+#pragma unroll
+        for (int ks = 0; ks < KC / KE; ++ks) {
+            if (ks < nks) {
+                uint4 af[2], bf[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    af[t] = frag(As, ATR{}, wm * 32 + t * 16, ks);
+                    bf[t] = frag(Bs, BTR{}, wn * 32 + t * 16, ks);
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) acc[i][j] = Mfma16<T>::run(af[i], bf[j], acc[i][j]);
+            }
+        }
+        __syncthreads();
+    }
+    // lane holds column lane % 16 and rows 4 * (lane / 16) + q of each 16x16 tile
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t gn = n0 + wn * 32 + j * 16 + (lane & 15);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t gm = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q;
+                if (gm < M && gn < N) {
+                    if constexpr (!EPI && std::is_same<OutT, Acc>::value)
+                        C[gm * ldc + gn] = (Acc)acc[i][j][q];
+                    else
+                        C[gm * ldc + gn] =
+                            narrow<OutT>(EPI ? epi_apply(epi, gm, gn, (float)acc[i][j][q]) : (float)acc[i][j][q]);
+                }
+            }
+        }
+}
+
 __global__ void __launch_bounds__(256) coopmat_tiles_kernel(const f16* __restrict__ A, const f16* __restrict__ B,
                                                             float* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                             int64_t lda, int64_t ldb, int64_t ldc, uint32_t layout) {
@@ -133,9 +288,44 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
     return LAVA_HIP_OK;
 }
 
+template <typename T>
+bool small_gemm_eligible(const void* A, const void* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                         bool arow, bool brow) {
+    constexpr int64_t EV = 16 / (int64_t)sizeof(T);
+    const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
+    return tiles256 <= SMALL_GEMM_MAX_TILES && aligned(A, 16) && aligned(B, 16) && lda % EV == 0 && ldb % EV == 0 &&
+           ((arow || !brow) ? K % EV == 0 : true) && (arow || M % EV == 0) && (!brow || N % EV == 0);
+}
+template bool small_gemm_eligible<f16>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool, bool);
+template bool small_gemm_eligible<bf16>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool, bool);
+template bool small_gemm_eligible<int8_t>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool,
+                                          bool);
+
+template <typename T, typename OutT, bool EPI>
+int launch_gemm_small(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                      int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi) {
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+    if (arow && brow)
+        hipLaunchKernelGGL((gemm_small_kernel<T, true, true, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
+                           ldb, ldc, epi);
+    else if (arow)
+        hipLaunchKernelGGL((gemm_small_kernel<T, true, false, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
+                           ldb, ldc, epi);
+    else if (brow)
+        hipLaunchKernelGGL((gemm_small_kernel<T, false, true, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
+                           ldb, ldc, epi);
+    else
+        hipLaunchKernelGGL((gemm_small_kernel<T, false, false, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K,
+                           lda, ldb, ldc, epi);
+    LAVA_LAUNCH_CHECK("gemm_small_kernel");
+    return LAVA_HIP_OK;
+}
+
 #define LAVA_STAGED_INST(T, O, E)                                                                              \
     template int launch_gemm_staged<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t, \
-                                             int64_t, bool, bool, hipStream_t, const Epilogue&);
+                                             int64_t, bool, bool, hipStream_t, const Epilogue&);                  \
+    template int launch_gemm_small<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t,  \
+                                            int64_t, bool, bool, hipStream_t, const Epilogue&);
 LAVA_STAGED_INST(f16, float, false)
 LAVA_STAGED_INST(bf16, float, false)
 LAVA_STAGED_INST(int8_t, int32_t, false)

@@ -12,6 +12,17 @@ template <typename T, typename OutT, bool EPI>
 int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                        int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi);
 
+// Products of at most SMALL_GEMM_MAX_TILES 256 x 256 tiles, on 64 x 64 tiles (16 times the
+// workgroups).  small_gemm_eligible() says whether the product and its layout fit the
+// kernel's 16-byte chunks (C row-major; arow / brow: A / B row-major).
+constexpr int64_t SMALL_GEMM_MAX_TILES = 16;
+template <typename T>
+bool small_gemm_eligible(const void* A, const void* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                         bool arow, bool brow);
+template <typename T, typename OutT, bool EPI>
+int launch_gemm_small(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                      int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi);
+
 // The 16x16x16 vocabulary-tile GEMM (fp16 -> fp32); M, N, K multiples of 16.
 int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s);

@@ -3,7 +3,8 @@
   * fp16/bf16: relative Frobenius error <= 1e-3 against the fp64 product of the
     same rounded inputs (the tolerance BASELINE.json states);
   * int8 -> int32: bit-exact;
-  * every layout combination and ragged extents through the staged kernel;
+  * every layout combination and ragged extents through the staged kernel, and the
+    small-product kernel (at most 16 tiles of 256 x 256) in every layout;
   * the BASELINE configs at full size: 256^3 fp16 (A, B row-major), 4096^3 and
     8192^3 bf16 (A row-major, B column-major), 4096^3 int8.  At full size the
     oracle checks sampled rows exactly and a size-independent property checks
@@ -73,6 +74,26 @@ def test_gemm_all_layouts_ragged(gpu, oracle, layout, dt, shape):
         assert np.all(C.to_numpy() == 0)
         return
     check_rows(oracle, dt, A, B, C, np.arange(M), layout)
+
+
+@pytest.mark.parametrize("layout", range(8))
+@pytest.mark.parametrize("dt", ["f16", "bf16", "i8"])
+@pytest.mark.parametrize("shape", [(256, 256, 256), (192, 320, 1056), (16, 1024, 2048), (520, 136, 96)])
+def test_gemm_small_products(gpu, oracle, layout, dt, shape):
+    """Products of at most 16 tiles of 256 x 256 run on 64 x 64 tiles, K in 512-byte chunks
+    with the next chunk in flight (one chunk, several, a ragged last one, and extents that are
+    not tile multiples); K-contiguous operands staged as loaded, M/N-contiguous ones through
+    transposing LDS reads (16-bit) or byte stores (int8).  int8 bit-exact."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm small {dt} layout={layout} M={M} N={N} K={K}")
+    A, B = make_inputs(gpu, dt, M, N, K, layout, 300 + layout, 400 + layout)
+    acc = "i32" if dt == "i8" else "f32"
+    C = lh.HIPDeviceArray(acc, (M, N), order="C" if layout & 4 else "F")
+    C.fill_bytes(0xFF)
+    lh.gemm(C, A, B)
+    rows = np.unique(np.concatenate([np.arange(0, M, 7), [M - 1]]))
+    check_rows(oracle, dt, A, B, C, rows, layout)
 
 
 def test_gemm_fp16_256_config(gpu, oracle):
