@@ -10,7 +10,7 @@ before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
-                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|attn_d96|copy]
+                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|attn_d96|w8a16_wcol|copy]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -180,14 +180,15 @@ def bench_attn(lh, steps, warmup, stream, B=4, H=32, S=4096, D=128):
     return flop, kern_ms, wall_ms
 
 
-def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6):
+def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6, w_order="C"):
     """Rotates `copies` weight/scale sets (> the 256 MB Infinity Cache) so that
-    every launch streams its weights from HBM."""
+    every launch streams its weights from HBM.  w_order "F": W column-major (K contiguous
+    per output column)."""
     X = lh.HIPDeviceArray("f16", (M, K), order="C")
     lh.fill_normal(X, lh.seed(3, 0))
     Ws, Ss = [], []
     for c in range(copies):
-        W = lh.HIPDeviceArray("i8", (K, N), order="C")
+        W = lh.HIPDeviceArray("i8", (K, N), order=w_order)
         s = lh.HIPDeviceArray("f16", (N,))
         lh.fill_i8(W, lh.seed(3, 1) + 1000 * c, symmetric=True)
         lh.fill_uniform(s, lh.seed(3, 2) + 1000 * c, 0.001, 0.02)
@@ -275,7 +276,7 @@ def main():
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96",
-                             "copy", "vendor_bf16"])
+                             "copy", "vendor_bf16", "w8a16_wcol"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -403,6 +404,14 @@ def main():
                     "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
                     "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s",
                                          load_traffic("w8a16"))})
+    elif args.workload == "w8a16_wcol":
+        nbytes, kms, wms = bench_w8a16(lh, K, W, stream, w_order="F")
+        out.update({"value": round(nbytes / (wms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 5),
+                    "dtype": "f16", "launches_per_step": SHORT_GROUP,
+                    "config": {"workload": "W8A16 16x4096 . 4096x14336 with W column-major (K contiguous per output "
+                                           "column), per-column fp16 scale, 6 rotating weight copies"},
+                    "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
+                    "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s", None)})
     elif args.workload == "gemm_f16_256":
         flop, kms, wms = bench_gemm_layout(lh, "f16", 256, 3 | 4, K, W, stream, 0, group=SHORT_GROUP)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),

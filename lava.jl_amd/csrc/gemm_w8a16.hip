@@ -207,6 +207,117 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
     }
 }
 
+// W column-major (K contiguous per output column: the usual layout of a linear layer's weight,
+// W^T row-major), X and Y row-major.  Each column's dot product streams contiguous memory, so a
+// workgroup takes whole columns over all of K -- no split across workgroups, no exchange:
+//  * a workgroup owns KM_GROUPS x KM_COLS = 64 columns of one 16-row block of X; its 8
+//    wavefronts are 2 column groups of 32 columns (two 16 x 16 MFMA tiles) x KM_KSPLIT = 4
+//    K ranges, reduced through LDS at the end (two wavefronts per SIMD);
+//  * per 64 k, lane (n, g) = (lane % 16, lane / 16) loads 16 bytes of column n0 + 16 t + n at
+//    k + 16 g .. k + 16 g + 15 for tile t: the first 8 bytes are its B operand for the k-step
+//    {16 g + j}, the last 8 for {16 g + 8 + j} (any assignment of k to the MFMA's k-slots works
+//    when A uses the same one), and the 32 bytes of X at [m = lane % 16][k + 16 g ...] are the
+//    two A operands;
+//  * int8 -> fp16 exactly: the byte (w ^ 0x80) under the high byte 0x64 is the fp16 value
+//    1152 + w (v_perm_b32 against a register of 0x64 bytes), then subtract 1152;
+//  * KM_DEPTH 64-k chunks in flight per wavefront; the scale is the per-element callback.
+constexpr int KM_COLS = 32;
+constexpr int KM_GROUPS = 2;
+constexpr int KM_KSPLIT = 4;
+constexpr int KM_WAVES = KM_GROUPS * KM_KSPLIT;
+constexpr int KM_DEPTH = 8;
+
+// 8 int8 weights (two dwords, k ascending) -> the 8 fp16 values of a B operand
+__device__ __forceinline__ f16x8 km_dequant(uint32_t lo, uint32_t hi) {
+    const uint32_t x0 = lo ^ 0x80808080u, x1 = hi ^ 0x80808080u;
+    // bytes 0-3 of the selector's source pair are the 0x64 register, 4-7 the weights
+    uint4 v;
+    v.x = __builtin_amdgcn_perm(x0, 0x64646464u, 0x00050004u);
+    v.y = __builtin_amdgcn_perm(x0, 0x64646464u, 0x00070006u);
+    v.z = __builtin_amdgcn_perm(x1, 0x64646464u, 0x00050004u);
+    v.w = __builtin_amdgcn_perm(x1, 0x64646464u, 0x00070006u);
+    const f16x8 bias = {(f16)-1152.f, (f16)-1152.f, (f16)-1152.f, (f16)-1152.f,
+                        (f16)-1152.f, (f16)-1152.f, (f16)-1152.f, (f16)-1152.f};
+    return __builtin_bit_cast(f16x8, v) + bias;   // exact: w = (1152 + w) - 1152
+}
+
+__global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* __restrict__ X,
+                                                                     const int8_t* __restrict__ W,
+                                                                     const f16* __restrict__ scale,
+                                                                     float* __restrict__ Y, int M, int N, int K,
+                                                                     int64_t ldx, int64_t ldw, int64_t ldy) {
+    __shared__ __attribute__((aligned(16))) f32x4 red[KM_KSPLIT][KM_GROUPS][2][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int cg = w % KM_GROUPS, ks = w / KM_GROUPS;   // column group, K range
+    const int q = lane & 15, g = lane >> 4;
+    const int n0 = (blockIdx.x * KM_GROUPS + cg) * KM_COLS;
+    const bool cols_ok = n0 < N;                        // the host keeps N a multiple of KM_COLS
+    const int m0 = blockIdx.y * 16;
+    const bool xrow_ok = m0 + q < M;
+    const int chunks = K / 64;
+    const int per = (chunks + KM_KSPLIT - 1) / KM_KSPLIT;
+    const int c_begin = min(chunks, ks * per), c_end = min(chunks, c_begin + per);
+    const int nch = cols_ok ? c_end - c_begin : 0;
+    const f16* xp = X + (int64_t)(m0 + q) * ldx + 64 * (int64_t)c_begin + 16 * g;
+    const int8_t* wp0 = W + (int64_t)(cols_ok ? n0 + q : 0) * ldw + 64 * (int64_t)c_begin + 16 * g;
+    const int8_t* wp1 = wp0 + 16 * ldw;
+
+    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    typedef uint32_t km_u4 __attribute__((ext_vector_type(4)));
+    km_u4 rw[KM_DEPTH][2];
+    uint4 rx[KM_DEPTH][2];
+    auto load = [&](int c, km_u4 (&ww)[2], uint4 (&xx)[2]) {
+        ww[0] = __builtin_nontemporal_load(reinterpret_cast<const km_u4*>(wp0 + 64 * (int64_t)c));
+        ww[1] = __builtin_nontemporal_load(reinterpret_cast<const km_u4*>(wp1 + 64 * (int64_t)c));
+        xx[0] = make_uint4(0, 0, 0, 0);
+        xx[1] = make_uint4(0, 0, 0, 0);
+        if (xrow_ok) {
+            xx[0] = *reinterpret_cast<const uint4*>(xp + 64 * c);
+            xx[1] = *reinterpret_cast<const uint4*>(xp + 64 * c + 8);
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < KM_DEPTH; ++u)
+        if (u < nch) load(u, rw[u], rx[u]);
+    for (int c0 = 0; c0 < nch; c0 += KM_DEPTH) {
+#pragma unroll
+        for (int u = 0; u < KM_DEPTH; ++u) {
+            if (c0 + u < nch) {
+                const km_u4 w0 = rw[u][0], w1 = rw[u][1];
+                const f16x8 xa = __builtin_bit_cast(f16x8, rx[u][0]), xb = __builtin_bit_cast(f16x8, rx[u][1]);
+                if (c0 + u + KM_DEPTH < nch) load(c0 + u + KM_DEPTH, rw[u], rx[u]);
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, km_dequant(w0.x, w0.y), acc[0], 0, 0, 0);
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, km_dequant(w0.z, w0.w), acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, km_dequant(w1.x, w1.y), acc[1], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, km_dequant(w1.z, w1.w), acc[1], 0, 0, 0);
+            }
+        }
+    }
+    // the K ranges of a column group added in order through LDS; the first finishes
+    red[ks][cg][0][lane] = acc[0];
+    red[ks][cg][1][lane] = acc[1];
+    __syncthreads();
+    if (ks != 0 || !cols_ok) return;
+    // acc[t] lane holds column n0 + 16 t + q and rows m0 + 4 g + j: the dequant scale by the
+    // per-element callback with the scale pointer in `extras`
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        f32x4 sum = red[0][cg][t][lane];
+#pragma unroll
+        for (int r = 1; r < KM_KSPLIT; ++r) sum += red[r][cg][t][lane];
+        Frag<float, 16, 16, Accumulator> f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f.v[j] = sum[j];
+        f = perelement(ScaleStrided<1>{}, f, scale, (uint32_t)(n0 + 16 * t));
+        const int col = n0 + 16 * t + q;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = m0 + 4 * g + j;
+            if (row < M) Y[(int64_t)row * ldy + col] = f.v[j];
+        }
+    }
+}
+
 // Any layout, any shape: one thread per output element, fp32 sums.
 __global__ void w8a16_generic_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
                                      const f16* __restrict__ scale, float* __restrict__ Y, int64_t M, int64_t N,
@@ -225,7 +336,7 @@ __global__ void w8a16_generic_kernel(const f16* __restrict__ X, const int8_t* __
 }
 
 // ---- launch planning ----------------------------------------------------------------------
-enum W8Path { W8_GENERIC = 0, W8_SPLIT = 1 };
+enum W8Path { W8_GENERIC = 0, W8_SPLIT = 1, W8_KMAJOR = 2 };
 
 // Arrival counters at the front of a split-K workspace: the split rule keeps splits * column
 // blocks * row blocks <= 256 with splits >= 2, so at most 128 counters are ever in use.
@@ -246,6 +357,15 @@ struct W8Plan {
 static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
                          uint32_t layout) {
     W8Plan p;
+    // W column-major, X and Y row-major
+    if (layout == 5u && N % KM_COLS == 0 && K > 0 && K % 64 == 0 && K <= 0x7fffffff && ldw % 16 == 0 &&
+        ldx % 8 == 0 && aligned(W, 16) && aligned(X, 16) && N <= 0x7fffffff && M <= 0x7fffffff &&
+        (M + 15) / 16 <= 65535) {
+        p.path = W8_KMAJOR;
+        p.mblocks = (M + 15) / 16;
+        p.cblocks = (N / KM_COLS + KM_GROUPS - 1) / KM_GROUPS;
+        return p;
+    }
     const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 && K / W8_KSTEP <= 0x7fffffff &&
                       ldw % 8 == 0 && ldx % 8 == 0 && aligned(W, 8) && aligned(X, 16) && N <= 0x7fffffff &&
                       M <= 0x7fffffff && (M + 15) / 16 <= 65535;
@@ -299,6 +419,13 @@ static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const voi
         default: launch_split_ks<0>(p, X, W, scale, Y, partial, counters, M, N, ldx, ldw, ldy, s); break;
         }
         LAVA_LAUNCH_CHECK("w8a16_kernel");
+        return LAVA_HIP_OK;
+    }
+    if (p.path == W8_KMAJOR) {
+        hipLaunchKernelGGL(w8a16_kmajor_kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_WAVES), 0,
+                           s, (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, (int)M, (int)N, (int)K,
+                           ldx, ldw, ldy);
+        LAVA_LAUNCH_CHECK("w8a16_kmajor_kernel");
         return LAVA_HIP_OK;
     }
     // any layout, any shape

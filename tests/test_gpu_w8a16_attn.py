@@ -107,6 +107,32 @@ def test_w8a16_stream_destroy_releases_workspace(gpu, oracle):
     assert oracle.rel_frobenius(outs[0], ref) <= 1e-3
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 14336, 4096), (1, 4096, 4096), (5, 11008, 4096), (16, 96, 64), (40, 256, 1024),
+                                   (16, 4096, 11008 // 64 * 64)])
+def test_w8a16_weights_column_major(gpu, oracle, M, N, K):
+    """W column-major (K contiguous per output column, the layout of a linear layer's weight),
+    X and Y row-major: the whole-column kernel (no split-K); rows past M read as zero and
+    more than one 16-row block of X; repeat calls identical."""
+    lh = gpu
+    announce(f"w8a16 W column-major M={M} N={N} K={K}")
+    X = lh.HIPDeviceArray("f16", (M, K), order="C")
+    W = lh.HIPDeviceArray("i8", (K, N), order="F")
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(X, lh_mod.seed(5, 0))
+    lh.fill_i8(W, lh_mod.seed(5, 1), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(5, 2), 0.001, 0.02)
+    Y = lh.HIPDeviceArray("f32", (M, N), order="C")
+    Y.fill_bytes(0xFF)
+    lh.w8a16(Y, X, W, s)
+    y1 = Y.to_numpy()
+    lh.w8a16(Y, X, W, s)
+    np.testing.assert_array_equal(Y.to_numpy(), y1)
+    Wh = np.ascontiguousarray(W.to_numpy())          # K x N, row-major for the oracle
+    rows = np.arange(M)
+    ref = oracle.w8a16_rows(X.to_numpy(), Wh, s.to_numpy(), N, K, K, N, rows)
+    assert oracle.rel_frobenius(y1, ref) <= 1e-3
+
+
 def test_w8a16_column_major_generic(gpu, oracle):
     lh = gpu
     announce("w8a16 column-major operands (generic kernel)")
