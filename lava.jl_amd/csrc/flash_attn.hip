@@ -38,6 +38,7 @@
 
 #include "lava_coopmat.hpp"
 #include "lava_hip_internal.hpp"
+#include "lds_dma.hpp"
 
 namespace lava {
 
@@ -133,34 +134,8 @@ struct f3_tag {
     static constexpr bool value = B;
 };
 
-typedef int f3_v4i __attribute__((ext_vector_type(4)));
 typedef short f3_s16x4 __attribute__((ext_vector_type(4)));
 typedef short f3_s16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ f3_v4i f3_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    f3_v4i r;
-    r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-    r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffffu));
-    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
-    r[3] = 0x00020000;
-    return r;
-}
-
-// 16 bytes per lane from rsrc + voffset + soffset into LDS at lds + 16 * lane.
-// Inline asm so that the compiler does not wait for it before unrelated LDS
-// reads; completion is waited for explicitly (s_waitcnt vmcnt) before the barrier
-// that publishes a stage.  m0 is reserved and set here.
-__device__ __forceinline__ void f3_dma16(const f3_v4i& rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :
-                 : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
-                 : "memory");
-}
-
-__device__ __forceinline__ uint32_t f3_lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
 
 __device__ __forceinline__ f3_s16x4 f3_read_tr(const uint8_t* p) {
     return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -245,8 +220,8 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // ---- LDS-DMA: wave w moves rows [8 w, 8 w + 8) of a K or V tile in DPT
     // instructions: instruction i covers rows 8 w + RPI i + lane / CH, physical chunk lane % CH.
     const uint32_t row_bytes = (uint32_t)(p.sl * 2);
-    const f3_v4i rk = f3_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
-    const f3_v4i rv = f3_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
+    const v4i rk = make_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
+    const v4i rv = make_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
     uint32_t voff_k[DPT], voff_v[DPT];
     int dma_row[DPT];
 #pragma unroll
@@ -257,8 +232,8 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
         voff_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ kswz(row));
         voff_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ vswz(row));
     }
-    const uint32_t lds_k = f3_lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * RB;
-    const uint32_t lds_v = f3_lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * RB;
+    const uint32_t lds_k = lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * RB;
+    const uint32_t lds_v = lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * RB;
     const int nkb_s = (p.S + F3_BK - 1) / F3_BK;   // key blocks holding keys < S
     const int nkb = CAUSAL ? min((qb * F3_BQ + F3_BQ) / F3_BK, nkb_s) : nkb_s;
     // block j -> stage j % F3_STAGES; blocks past the end re-read the last one so
@@ -266,7 +241,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // A row at or past S gets an offset beyond the resource (2^31 > S * row bytes,
     // no wrap with soffset), so it reads zero whether or not the range check counts
     // soffset; its scores are masked.
-    auto issue = [&](const f3_v4i& rsrc, const uint32_t* voff, uint32_t lds, int j) {
+    auto issue = [&](const v4i& rsrc, const uint32_t* voff, uint32_t lds, int j) {
         const int src = j < nkb ? j : nkb - 1;
         const uint32_t soff = (uint32_t)src * F3_BK * row_bytes;
         const uint32_t dst = lds + (uint32_t)(j % F3_STAGES) * TILE;
@@ -278,7 +253,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
             for (int i = 0; i < DPT; ++i) v[i] = src * F3_BK + dma_row[i] < p.S ? v[i] : 0x80000000u;
         }
 #pragma unroll
-        for (int i = 0; i < DPT; ++i) f3_dma16(rsrc, v[i], soff, dst + 1024 * i);
+        for (int i = 0; i < DPT; ++i) dma16(rsrc, v[i], soff, dst + 1024 * i);
     };
 
     // K fragment (kt, ks): row 32 kt + r32, logical chunk 2 ks + h, stored at chunk ^ kswz(row)
@@ -585,17 +560,17 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
         const int src = j < nkb ? j : nkb - 1;
         const f16* base = (is_k ? p.K : p.V) + head + (int64_t)src * F5_BK * p.sl;
         const uint32_t rows = (uint32_t)min(F5_BK, p.S - src * F5_BK);
-        const f3_v4i rs = f3_rsrc(base, rows * row_bytes);
-        const uint32_t dst = f3_lds_addr(is_k ? &kbuf[0][0] : &vbuf[0][0]) + (uint32_t)pr * 16 * RB +
+        const v4i rs = make_rsrc(base, rows * row_bytes);
+        const uint32_t dst = lds_addr(is_k ? &kbuf[0][0] : &vbuf[0][0]) + (uint32_t)pr * 16 * RB +
                              (uint32_t)(j % (is_k ? F5_KST : F5_VST)) * TILE;
 #pragma unroll
         for (int i = 0; i < DPT; ++i)
-            f3_dma16(rs, is_k ? dv_k[i] : dv_v[i], 0u, __builtin_amdgcn_readfirstlane(dst + 1024u * i));
+            dma16(rs, is_k ? dv_k[i] : dv_v[i], 0u, __builtin_amdgcn_readfirstlane(dst + 1024u * i));
     };
     typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
     typedef __attribute__((address_space(3))) f3_s16x4 lds_s16x4;
     // P^T fragment (kt, ks, qh) of pair pr in buffer b: 1 KB, lane l at 16 l
-    const uint32_t p_lane = f3_lds_addr(&pbuf[0][0][0]) + (uint32_t)pr * PBUF + 16u * lane;
+    const uint32_t p_lane = lds_addr(&pbuf[0][0][0]) + (uint32_t)pr * PBUF + 16u * lane;
     auto paddr = [&](int b, int kt, int ks, int qh) __attribute__((always_inline)) -> uint32_t {
         return p_lane + (uint32_t)(b * F5_PAIRS * PBUF + ((kt * 2 + ks) * 2 + qh) * 1024);
     };
@@ -614,15 +589,15 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
         // instruction, chunk ^ row % 16, rows at or past S read zero -- and the Q^T
         // fragments are read from there: whole-row reads instead of 32 rows x 32 bytes per
         // load instruction.
-        const uint32_t qst[2] = {f3_lds_addr(&pbuf[0][pr][0]), f3_lds_addr(&pbuf[1][pr][0])};
+        const uint32_t qst[2] = {lds_addr(&pbuf[0][pr][0]), lds_addr(&pbuf[1][pr][0])};
         {
             const uint32_t rows = (uint32_t)max(0, min(64, p.S - q0));
-            const f3_v4i rs = f3_rsrc(p.Q + head + (int64_t)q0 * p.sl, rows * row_bytes);
+            const v4i rs = make_rsrc(p.Q + head + (int64_t)q0 * p.sl, rows * row_bytes);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int row = 4 * i + lane / CH;
                 const uint32_t v = chunk_ofs(row, (lane % CH) ^ (row & 15));
-                f3_dma16(rs, v, 0u, __builtin_amdgcn_readfirstlane(qst[i / 8] + (uint32_t)((4 * i) % 32) * RB));
+                dma16(rs, v, 0u, __builtin_amdgcn_readfirstlane(qst[i / 8] + (uint32_t)((4 * i) % 32) * RB));
             }
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -664,7 +639,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
         uint32_t kb0[NKS];
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks)
-            kb0[ks] = f3_lds_addr(&kbuf[0][0]) + (uint32_t)(r32 * RB + (((2 * ks + h) ^ (r32 & 15)) << 4));
+            kb0[ks] = lds_addr(&kbuf[0][0]) + (uint32_t)(r32 * RB + (((2 * ks + h) ^ (r32 & 15)) << 4));
         f32x16 st[2][2];           // st[kt][qh] register r: key 32 kt + 8 (r / 4) + 4 h + r % 4
         float m_run[2] = {0.f, 0.f};
 
@@ -804,7 +779,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
             const int jj = (lane & 15) >> 2, q = lane & 3, dh = (lane >> 4) & 1;
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt)
-                vb0[dt] = f3_lds_addr(&vbuf[0][0]) +
+                vb0[dt] = lds_addr(&vbuf[0][0]) +
                           (uint32_t)((4 * h + jj) * RB + (((4 * dt + 2 * dh + (q >> 1)) ^ (4 * jj)) << 4) + ((q & 1) << 3));
         }
         f32x16 o[NDT][2];
@@ -899,7 +874,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
             // Staged through this pair's P buffers (no wavefront reads them after the last
             // barrier) as 64 rows of 256 bytes, chunk ^ row % 16, then stored 4 whole rows per
             // instruction (16 bytes per lane) instead of 32 rows x 16 bytes.
-            const uint32_t ost[2] = {f3_lds_addr(&pbuf[0][pr][0]), f3_lds_addr(&pbuf[1][pr][0])};
+            const uint32_t ost[2] = {lds_addr(&pbuf[0][pr][0]), lds_addr(&pbuf[1][pr][0])};
             typedef __attribute__((address_space(3))) f16x4 lds_f16x4;
 #pragma unroll
             for (int qh = 0; qh < 2; ++qh)

@@ -32,6 +32,7 @@
 
 #include "lava_coopmat.hpp"
 #include "lava_hip_internal.hpp"
+#include "lds_dma.hpp"
 
 namespace lava {
 
@@ -210,22 +211,30 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
 // W column-major (K contiguous per output column: the usual layout of a linear layer's weight,
 // W^T row-major), X and Y row-major.  Each column's dot product streams contiguous memory, so a
 // workgroup takes whole columns over all of K -- no split across workgroups, no exchange:
-//  * a workgroup owns KM_GROUPS x KM_COLS = 64 columns of one 16-row block of X; its 8
-//    wavefronts are 2 column groups of 32 columns (two 16 x 16 MFMA tiles) x KM_KSPLIT = 4
-//    K ranges, reduced through LDS at the end (two wavefronts per SIMD);
-//  * per 64 k, lane (n, g) = (lane % 16, lane / 16) loads 16 bytes of column n0 + 16 t + n at
-//    k + 16 g .. k + 16 g + 15 for tile t: the first 8 bytes are its B operand for the k-step
-//    {16 g + j}, the last 8 for {16 g + 8 + j} (any assignment of k to the MFMA's k-slots works
-//    when A uses the same one), and the 32 bytes of X at [m = lane % 16][k + 16 g ...] are the
-//    two A operands;
+//  * a workgroup owns KM_COLS = 32 columns (two 16 x 16 MFMA tiles) of one 16-row block of X;
+//    its KM_KSPLIT = 4 wavefronts take a quarter of K each and are added through LDS at the end;
+//  * a wavefront streams its 32 columns in stages of KM_SEG = 128 k: W (32 columns x 128 bytes)
+//    and X (16 rows x 256 bytes) go straight into the wavefront's own LDS buffers (LDS DMA,
+//    one 128-byte run of a column per 8 lanes -- HBM serves 128-byte runs of a column at ~4.8
+//    TB/s against ~3.4 for the 64-byte runs a direct MFMA-layout load would make), two stages
+//    in flight, waited for with vmcnt: no barriers between wavefronts;
+//  * LDS rows are XOR-swizzled (16-byte slot = chunk ^ row) so the fragment reads of 16 rows hit
+//    distinct banks;
+//  * per 64 k, lane (n, g) = (lane % 16, lane / 16) reads 16 bytes of column n0 + 16 t + n at
+//    k + 16 g for tile t: the first 8 bytes are its B operand for the k-step {16 g + j}, the last
+//    8 for {16 g + 8 + j} (any assignment of k to the MFMA's k-slots works when A uses the same
+//    one), and the 32 bytes of X at [m = lane % 16][k + 16 g ...] are the two A operands;
 //  * int8 -> fp16 exactly: the byte (w ^ 0x80) under the high byte 0x64 is the fp16 value
 //    1152 + w (v_perm_b32 against a register of 0x64 bytes), then subtract 1152;
-//  * KM_DEPTH 64-k chunks in flight per wavefront; the scale is the per-element callback.
-constexpr int KM_COLS = 32;
-constexpr int KM_GROUPS = 2;
+//  * K's tail: 16-byte chunks at or past K take the out-of-range offset and read zero (in W and
+//    in X); rows of X at or past M likewise.  The scale is the per-element callback.
+constexpr int KM_TILES = 2;
+constexpr int KM_COLS = 16 * KM_TILES;
 constexpr int KM_KSPLIT = 4;
-constexpr int KM_WAVES = KM_GROUPS * KM_KSPLIT;
-constexpr int KM_DEPTH = 8;
+constexpr int KM_SEG = 128;                       // k per stage
+constexpr int KM_W_INSTR = KM_COLS / 8;           // W DMA instructions per stage (8 columns each)
+constexpr int KM_X_INSTR = 16 / 4;                // X DMA instructions per stage (4 rows each)
+constexpr int KM_STAGE_BYTES = KM_COLS * KM_SEG + 16 * KM_SEG * 2;
 
 // 8 int8 weights (two dwords, k ascending) -> the 8 fp16 values of a B operand
 __device__ __forceinline__ f16x8 km_dequant(uint32_t lo, uint32_t hi) {
@@ -241,70 +250,95 @@ __device__ __forceinline__ f16x8 km_dequant(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(f16x8, v) + bias;   // exact: w = (1152 + w) - 1152
 }
 
-__global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* __restrict__ X,
-                                                                     const int8_t* __restrict__ W,
-                                                                     const f16* __restrict__ scale,
-                                                                     float* __restrict__ Y, int M, int N, int K,
-                                                                     int64_t ldx, int64_t ldw, int64_t ldy) {
-    __shared__ __attribute__((aligned(16))) f32x4 red[KM_KSPLIT][KM_GROUPS][2][64];
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int cg = w % KM_GROUPS, ks = w / KM_GROUPS;   // column group, K range
+__global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16* __restrict__ X,
+                                                                      const int8_t* __restrict__ W,
+                                                                      const f16* __restrict__ scale,
+                                                                      float* __restrict__ Y, int M, int N, int K,
+                                                                      int64_t ldx, int64_t ldw, int64_t ldy) {
+    // per wavefront: two stage buffers, each W [32 columns][128 bytes] then X [16 rows][256 bytes]
+    __shared__ __attribute__((aligned(16))) uint8_t stage_buf[KM_KSPLIT][2][KM_STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) f32x4 red[KM_KSPLIT][KM_TILES][64];
+    const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane & 15, g = lane >> 4;
-    const int n0 = (blockIdx.x * KM_GROUPS + cg) * KM_COLS;
-    const bool cols_ok = n0 < N;                        // the host keeps N a multiple of KM_COLS
+    const int n0 = blockIdx.x * KM_COLS;              // the host keeps N a multiple of KM_COLS
     const int m0 = blockIdx.y * 16;
-    const bool xrow_ok = m0 + q < M;
-    const int chunks = K / 64;
-    const int per = (chunks + KM_KSPLIT - 1) / KM_KSPLIT;
-    const int c_begin = min(chunks, ks * per), c_end = min(chunks, c_begin + per);
-    const int nch = cols_ok ? c_end - c_begin : 0;
-    const f16* xp = X + (int64_t)(m0 + q) * ldx + 64 * (int64_t)c_begin + 16 * g;
-    const int8_t* wp0 = W + (int64_t)(cols_ok ? n0 + q : 0) * ldw + 64 * (int64_t)c_begin + 16 * g;
-    const int8_t* wp1 = wp0 + 16 * ldw;
+    const int stages = (K + KM_SEG - 1) / KM_SEG;
+    const int per = (stages + KM_KSPLIT - 1) / KM_KSPLIT;
+    const int s_begin = min(stages, ks * per), s_end = min(stages, s_begin + per);
+    const int nst = s_end - s_begin;
 
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
-    typedef uint32_t km_u4 __attribute__((ext_vector_type(4)));
-    km_u4 rw[KM_DEPTH][2];
-    uint4 rx[KM_DEPTH][2];
-    auto load = [&](int c, km_u4 (&ww)[2], uint4 (&xx)[2]) {
-        ww[0] = __builtin_nontemporal_load(reinterpret_cast<const km_u4*>(wp0 + 64 * (int64_t)c));
-        ww[1] = __builtin_nontemporal_load(reinterpret_cast<const km_u4*>(wp1 + 64 * (int64_t)c));
-        xx[0] = make_uint4(0, 0, 0, 0);
-        xx[1] = make_uint4(0, 0, 0, 0);
-        if (xrow_ok) {
-            xx[0] = *reinterpret_cast<const uint4*>(xp + 64 * c);
-            xx[1] = *reinterpret_cast<const uint4*>(xp + 64 * c + 8);
+    // buffer resources over this workgroup's 32 columns of W and 16 rows of X
+    const v4i w_rs = make_rsrc(W + (int64_t)n0 * ldw, (uint32_t)(KM_COLS * ldw));
+    const v4i x_rs = make_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(16 * ldx * 2));
+    // W instruction i, lane l: column 8 i + l / 8, slot l % 8 holding chunk slot ^ (column % 8)
+    // X instruction j, lane l: row 4 j + l / 16, slot l % 16 holding chunk slot ^ (row % 16)
+    const int wc_lo = lane >> 3, w_slot = lane & 7;
+    const int xr_lo = lane >> 4, x_slot = lane & 15;
+    const int rows_ok = min(16, M - m0);
+    auto issue = [&](int st, int buf) {
+        const int k0 = st * KM_SEG;                   // first k of the stage
+        const uint32_t lds0 = lds_addr(&stage_buf[ks][buf][0]);
+#pragma unroll
+        for (int i = 0; i < KM_W_INSTR; ++i) {
+            const int col = 8 * i + wc_lo;
+            const int kb = k0 + 16 * (w_slot ^ (col & 7));
+            const uint32_t off = kb < K ? (uint32_t)(col * ldw + kb) : OOB_OFS;
+            dma16(w_rs, off, 0, lds0 + 1024 * i);
+        }
+#pragma unroll
+        for (int j = 0; j < KM_X_INSTR; ++j) {
+            const int row = 4 * j + xr_lo;
+            const int kx = k0 + 8 * (x_slot ^ (row & 15));
+            const uint32_t off = (kx < K && row < rows_ok) ? (uint32_t)(row * ldx * 2 + 2 * kx) : OOB_OFS;
+            dma16(x_rs, off, 0, lds0 + KM_COLS * KM_SEG + 1024 * j);
         }
     };
+
+    f32x4 acc[KM_TILES];
 #pragma unroll
-    for (int u = 0; u < KM_DEPTH; ++u)
-        if (u < nch) load(u, rw[u], rx[u]);
-    for (int c0 = 0; c0 < nch; c0 += KM_DEPTH) {
+    for (int t = 0; t < KM_TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nst > 0) issue(s_begin, 0);
+    if (nst > 1) issue(s_begin + 1, 1);
+    for (int s = 0; s < nst; ++s) {
+        // this stage's DMA done; the next stage's (if issued) may still be in flight
+        if (s + 1 < nst)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KM_W_INSTR + KM_X_INSTR) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const uint8_t* wb = &stage_buf[ks][s & 1][0];
+        const uint8_t* xb = wb + KM_COLS * KM_SEG;
 #pragma unroll
-        for (int u = 0; u < KM_DEPTH; ++u) {
-            if (c0 + u < nch) {
-                const km_u4 w0 = rw[u][0], w1 = rw[u][1];
-                const f16x8 xa = __builtin_bit_cast(f16x8, rx[u][0]), xb = __builtin_bit_cast(f16x8, rx[u][1]);
-                if (c0 + u + KM_DEPTH < nch) load(c0 + u + KM_DEPTH, rw[u], rx[u]);
-                acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, km_dequant(w0.x, w0.y), acc[0], 0, 0, 0);
-                acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, km_dequant(w0.z, w0.w), acc[0], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, km_dequant(w1.x, w1.y), acc[1], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xb, km_dequant(w1.z, w1.w), acc[1], 0, 0, 0);
+        for (int h = 0; h < 2; ++h) {
+            // X row q, k 64 h + 16 g .. + 15: fp16 chunks 8 h + 2 g and + 1
+            const int c0 = 8 * h + 2 * g;
+            const f16x8 xa = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * (c0 ^ q));
+            const f16x8 xv = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * ((c0 + 1) ^ q));
+#pragma unroll
+            for (int t = 0; t < KM_TILES; ++t) {
+                const int col = 16 * t + q;
+                const uint4 wv = *reinterpret_cast<const uint4*>(wb + KM_SEG * col + 16 * ((4 * h + g) ^ (col & 7)));
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, km_dequant(wv.x, wv.y), acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, km_dequant(wv.z, wv.w), acc[t], 0, 0, 0);
             }
         }
+        if (s + 2 < nst) {
+            // the buffer is refilled: its LDS reads must have returned first
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(s_begin + s + 2, s & 1);
+        }
     }
-    // the K ranges of a column group added in order through LDS; the first finishes
-    red[ks][cg][0][lane] = acc[0];
-    red[ks][cg][1][lane] = acc[1];
+    // the K quarters added in order through LDS; the first wavefront finishes
+#pragma unroll
+    for (int t = 0; t < KM_TILES; ++t) red[ks][t][lane] = acc[t];
     __syncthreads();
-    if (ks != 0 || !cols_ok) return;
+    if (ks != 0) return;
     // acc[t] lane holds column n0 + 16 t + q and rows m0 + 4 g + j: the dequant scale by the
     // per-element callback with the scale pointer in `extras`
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        f32x4 sum = red[0][cg][t][lane];
+    for (int t = 0; t < KM_TILES; ++t) {
+        f32x4 sum = red[0][t][lane];
 #pragma unroll
-        for (int r = 1; r < KM_KSPLIT; ++r) sum += red[r][cg][t][lane];
+        for (int r = 1; r < KM_KSPLIT; ++r) sum += red[r][t][lane];
         Frag<float, 16, 16, Accumulator> f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) f.v[j] = sum[j];
@@ -358,12 +392,13 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
                          uint32_t layout) {
     W8Plan p;
     // W column-major, X and Y row-major
-    if (layout == 5u && N % KM_COLS == 0 && K > 0 && K % 64 == 0 && K <= 0x7fffffff && ldw % 16 == 0 &&
-        ldx % 8 == 0 && aligned(W, 16) && aligned(X, 16) && N <= 0x7fffffff && M <= 0x7fffffff &&
-        (M + 15) / 16 <= 65535) {
+    // (the kernel's 32-bit buffer offsets span 32 columns of W and 16 rows of X)
+    if (layout == 5u && N % KM_COLS == 0 && K > 0 && K % 16 == 0 && ldw % 16 == 0 && ldw >= K &&
+        ldw <= (int64_t(1) << 31) / KM_COLS && ldx % 8 == 0 && ldx >= K && ldx <= (int64_t(1) << 26) &&
+        aligned(W, 16) && aligned(X, 16) && N <= 0x7fffffff && M <= 0x7fffffff && (M + 15) / 16 <= 65535) {
         p.path = W8_KMAJOR;
         p.mblocks = (M + 15) / 16;
-        p.cblocks = (N / KM_COLS + KM_GROUPS - 1) / KM_GROUPS;
+        p.cblocks = N / KM_COLS;
         return p;
     }
     const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 && K / W8_KSTEP <= 0x7fffffff &&
@@ -422,7 +457,7 @@ static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const voi
         return LAVA_HIP_OK;
     }
     if (p.path == W8_KMAJOR) {
-        hipLaunchKernelGGL(w8a16_kmajor_kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_WAVES), 0,
+        hipLaunchKernelGGL(w8a16_kmajor_kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_KSPLIT), 0,
                            s, (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, (int)M, (int)N, (int)K,
                            ldx, ldw, ldy);
         LAVA_LAUNCH_CHECK("w8a16_kmajor_kernel");

@@ -108,7 +108,12 @@ def test_w8a16_stream_destroy_releases_workspace(gpu, oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 14336, 4096), (1, 4096, 4096), (5, 11008, 4096), (16, 96, 64), (40, 256, 1024),
-                                   (16, 4096, 11008 // 64 * 64)])
+                                   (16, 4096, 11008 // 64 * 64),
+                                   # K not a multiple of the 128-k stage: a partial last stage, and
+                                   # K quarters of unequal length (some empty when K < 4 stages)
+                                   (16, 4096, 1040), (3, 256, 48), (17, 64, 4112), (16, 32, 400),
+                                   # K not a multiple of 16: the generic kernel
+                                   (4, 64, 40)])
 def test_w8a16_weights_column_major(gpu, oracle, M, N, K):
     """W column-major (K contiguous per output column, the layout of a linear layer's weight),
     X and Y row-major: the whole-column kernel (no split-K); rows past M read as zero and
@@ -131,6 +136,26 @@ def test_w8a16_weights_column_major(gpu, oracle, M, N, K):
     rows = np.arange(M)
     ref = oracle.w8a16_rows(X.to_numpy(), Wh, s.to_numpy(), N, K, K, N, rows)
     assert oracle.rel_frobenius(y1, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("M,N,K,padx,padw", [(16, 4096, 4096, 8, 16), (5, 256, 1040, 24, 48)])
+def test_w8a16_weights_column_major_strided(gpu, oracle, M, N, K, padx, padw):
+    """Column-major W and row-major X with leading dimensions past K (padding never read)."""
+    lh = gpu
+    announce(f"w8a16 W column-major strided M={M} N={N} K={K} ldx=K+{padx} ldw=K+{padw}")
+    ldx, ldw = K + padx, K + padw
+    Xp = lh.HIPDeviceArray("f16", (M, ldx), order="C")
+    Wp = lh.HIPDeviceArray("i8", (ldw, N), order="F")
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(Xp, lh_mod.seed(6, 0))
+    lh.fill_i8(Wp, lh_mod.seed(6, 1), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(6, 2), 0.001, 0.02)
+    Y = lh.HIPDeviceArray("f32", (M, N), order="C")
+    lh.w8a16_raw(Xp.ptr, Wp.ptr, s.ptr, Y.ptr, M, N, K, ldx, ldw, N, layout=5)
+    Xh = np.ascontiguousarray(Xp.to_numpy()[:, :K])
+    Wh = np.ascontiguousarray(Wp.to_numpy()[:K, :])
+    ref = oracle.w8a16_rows(Xh, Wh, s.to_numpy(), N, K, K, N, np.arange(M))
+    assert oracle.rel_frobenius(Y.to_numpy(), ref) <= 1e-3
 
 
 def test_w8a16_column_major_generic(gpu, oracle):
