@@ -212,12 +212,15 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
 // W^T row-major), X and Y row-major.  Each column's dot product streams contiguous memory, so a
 // workgroup takes whole columns over all of K -- no split across workgroups, no exchange:
 //  * a workgroup owns KM_COLS = 32 columns (two 16 x 16 MFMA tiles) of one 16-row block of X;
-//    its KM_KSPLIT = 4 wavefronts take a quarter of K each and are added through LDS at the end;
+//    its KM_KSPLIT = 2 wavefronts take half of K each and are added through LDS at the end;
 //  * a wavefront streams its 32 columns in stages of KM_SEG = 128 k: W (32 columns x 128 bytes)
-//    and X (16 rows x 256 bytes) go straight into the wavefront's own LDS buffers (LDS DMA,
-//    one 128-byte run of a column per 8 lanes -- HBM serves 128-byte runs of a column at ~4.8
-//    TB/s against ~3.4 for the 64-byte runs a direct MFMA-layout load would make), two stages
-//    in flight, waited for with vmcnt: no barriers between wavefronts;
+//    and X (16 rows x 256 bytes) go straight into the wavefront's own LDS ring of KM_BUFS = 4
+//    stages (LDS DMA, one 128-byte run of a column per 8 lanes -- HBM serves 128-byte runs of a
+//    column at ~4.8 TB/s against ~3.4 for the 64-byte runs a direct MFMA-layout load would
+//    make), waited for with vmcnt: no barriers between wavefronts.  A stage's buffer is refilled
+//    as soon as its fragments are in registers, before its MFMAs;
+//  * 68 KB of LDS per workgroup holds the chip to two workgroups per CU, which spreads a grid
+//    of a few hundred workgroups evenly (a third per CU, from a shallower ring, measured slower);
 //  * LDS rows are XOR-swizzled (16-byte slot = chunk ^ row) so the fragment reads of 16 rows hit
 //    distinct banks;
 //  * per 64 k, lane (n, g) = (lane % 16, lane / 16) reads 16 bytes of column n0 + 16 t + n at
@@ -230,7 +233,9 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
 //    in X); rows of X at or past M likewise.  The scale is the per-element callback.
 constexpr int KM_TILES = 2;
 constexpr int KM_COLS = 16 * KM_TILES;
-constexpr int KM_KSPLIT = 4;
+constexpr int KM_KSPLIT = 2;
+constexpr int KM_BUFS = 4;                        // stage ring per wavefront
+static_assert(KM_BUFS >= 1 && KM_BUFS <= 4, "the vmcnt waits cover up to 3 later stages");
 constexpr int KM_SEG = 128;                       // k per stage
 constexpr int KM_W_INSTR = KM_COLS / 8;           // W DMA instructions per stage (8 columns each)
 constexpr int KM_X_INSTR = 16 / 4;                // X DMA instructions per stage (4 rows each)
@@ -256,7 +261,7 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
                                                                       float* __restrict__ Y, int M, int N, int K,
                                                                       int64_t ldx, int64_t ldw, int64_t ldy) {
     // per wavefront: two stage buffers, each W [32 columns][128 bytes] then X [16 rows][256 bytes]
-    __shared__ __attribute__((aligned(16))) uint8_t stage_buf[KM_KSPLIT][2][KM_STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) uint8_t stage_buf[KM_KSPLIT][KM_BUFS][KM_STAGE_BYTES];
     __shared__ __attribute__((aligned(16))) f32x4 red[KM_KSPLIT][KM_TILES][64];
     const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = lane & 15, g = lane >> 4;
@@ -297,35 +302,53 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
     f32x4 acc[KM_TILES];
 #pragma unroll
     for (int t = 0; t < KM_TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (nst > 0) issue(s_begin, 0);
-    if (nst > 1) issue(s_begin + 1, 1);
+#pragma unroll
+    for (int b = 0; b < KM_BUFS; ++b)
+        if (b < nst) issue(s_begin + b, b);
+    constexpr int PER_STAGE = KM_W_INSTR + KM_X_INSTR;   // DMA instructions
     for (int s = 0; s < nst; ++s) {
-        // this stage's DMA done; the next stage's (if issued) may still be in flight
-        if (s + 1 < nst)
-            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KM_W_INSTR + KM_X_INSTR) : "memory");
+        // this stage's DMA done; the later stages issued (up to KM_BUFS - 1) may be in flight
+        const int later = min(KM_BUFS - 1, nst - 1 - s);
+        if (later >= 3)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PER_STAGE) : "memory");
+        else if (later == 2)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PER_STAGE) : "memory");
+        else if (later == 1)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PER_STAGE) : "memory");
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        const uint8_t* wb = &stage_buf[ks][s & 1][0];
+        const int buf = s % KM_BUFS;
+        const uint8_t* wb = &stage_buf[ks][buf][0];
         const uint8_t* xb = wb + KM_COLS * KM_SEG;
+        // the stage's fragments into registers; X row q, k 64 h + 16 g .. + 15 is fp16 chunks
+        // 8 h + 2 g and + 1, W column 16 t + q at k 64 h + 16 g is chunk 4 h + g
+        f16x8 xf[2][2];
+        uint4 wf[2][KM_TILES];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            // X row q, k 64 h + 16 g .. + 15: fp16 chunks 8 h + 2 g and + 1
             const int c0 = 8 * h + 2 * g;
-            const f16x8 xa = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * (c0 ^ q));
-            const f16x8 xv = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * ((c0 + 1) ^ q));
+            xf[h][0] = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * (c0 ^ q));
+            xf[h][1] = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * ((c0 + 1) ^ q));
 #pragma unroll
             for (int t = 0; t < KM_TILES; ++t) {
                 const int col = 16 * t + q;
-                const uint4 wv = *reinterpret_cast<const uint4*>(wb + KM_SEG * col + 16 * ((4 * h + g) ^ (col & 7)));
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, km_dequant(wv.x, wv.y), acc[t], 0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xv, km_dequant(wv.z, wv.w), acc[t], 0, 0, 0);
+                wf[h][t] = *reinterpret_cast<const uint4*>(wb + KM_SEG * col + 16 * ((4 * h + g) ^ (col & 7)));
             }
         }
-        if (s + 2 < nst) {
-            // the buffer is refilled: its LDS reads must have returned first
+        if (s + KM_BUFS < nst) {
+            // the buffer is refilled as soon as its LDS reads have returned
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            issue(s_begin + s + 2, s & 1);
+            issue(s_begin + s + KM_BUFS, buf);
         }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int t = 0; t < KM_TILES; ++t) {
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[h][0], km_dequant(wf[h][t].x, wf[h][t].y), acc[t],
+                                                                0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[h][1], km_dequant(wf[h][t].z, wf[h][t].w), acc[t],
+                                                                0, 0, 0);
+            }
     }
     // the K quarters added in order through LDS; the first wavefront finishes
 #pragma unroll
