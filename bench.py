@@ -10,7 +10,7 @@ before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
-                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|attn_d96|w8a16_wcol|copy]
+                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|attn_d96|w8a16_wrow|w8a16_julia|copy]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -180,11 +180,12 @@ def bench_attn(lh, steps, warmup, stream, B=4, H=32, S=4096, D=128):
     return flop, kern_ms, wall_ms
 
 
-def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6, w_order="C"):
+def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6, x_order="C", w_order="F",
+                y_order="C"):
     """Rotates `copies` weight/scale sets (> the 256 MB Infinity Cache) so that
-    every launch streams its weights from HBM.  w_order "F": W column-major (K contiguous
-    per output column)."""
-    X = lh.HIPDeviceArray("f16", (M, K), order="C")
+    every launch streams its weights from HBM.  Orders: "C" row-major, "F" column-major
+    (W "F": K contiguous per output column)."""
+    X = lh.HIPDeviceArray("f16", (M, K), order=x_order)
     lh.fill_normal(X, lh.seed(3, 0))
     Ws, Ss = [], []
     for c in range(copies):
@@ -194,7 +195,7 @@ def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6, w_or
         lh.fill_uniform(s, lh.seed(3, 2) + 1000 * c, 0.001, 0.02)
         Ws.append(W)
         Ss.append(s)
-    Y = lh.HIPDeviceArray("f32", (M, N), order="C")
+    Y = lh.HIPDeviceArray("f32", (M, N), order=y_order)
     lh.synchronize()
     state = {"i": 0}
 
@@ -206,6 +207,15 @@ def bench_w8a16(lh, steps, warmup, stream, M=16, N=14336, K=4096, copies=6, w_or
     kern_ms, wall_ms = timed(lh, launch, steps, warmup, stream, group=SHORT_GROUP)
     nbytes = K * N + 2 * N + 2 * M * K + 4 * M * N
     return nbytes, kern_ms, wall_ms
+
+
+# W8A16 workloads: (X, W, Y orders, description, traffic.json key).  The headline follows the
+# GEMM configs' operand convention (A row-major, B column-major: both K-contiguous).
+W8A16_WORKLOADS = {
+    "w8a16": ("C", "F", "C", "X row-major, W column-major (K-contiguous operands), Y row-major", "w8a16"),
+    "w8a16_wrow": ("C", "C", "C", "X, W and Y row-major (N-contiguous weights)", "w8a16_wrow"),
+    "w8a16_julia": ("F", "F", "F", "X, W and Y column-major (Julia's default layout)", None),
+}
 
 
 def bench_vendor_bf16(steps, warmup, n=8192):
@@ -276,7 +286,7 @@ def main():
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96",
-                             "copy", "vendor_bf16", "w8a16_wcol"])
+                             "copy", "vendor_bf16", "w8a16_wrow", "w8a16_julia"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -395,23 +405,16 @@ def main():
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_INT8_TOPS, "TOP/s",
                                          load_traffic("gemm_i8_4096"))})
-    elif args.workload == "w8a16":
-        nbytes, kms, wms = bench_w8a16(lh, K, W, stream)
+    elif args.workload in W8A16_WORKLOADS:
+        xo, wo, yo, what, traffic_key = W8A16_WORKLOADS[args.workload]
+        nbytes, kms, wms = bench_w8a16(lh, K, W, stream, x_order=xo, w_order=wo, y_order=yo)
         out.update({"value": round(nbytes / (wms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 5),
                     "dtype": "f16", "launches_per_step": SHORT_GROUP,
                     "config": {"workload": "W8A16 16x4096 . 4096x14336, per-column fp16 scale, "
-                                           "6 rotating weight copies (BASELINE configs[3])"},
+                                           "6 rotating weight copies (BASELINE configs[3]); " + what},
                     "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
                     "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s",
-                                         load_traffic("w8a16"))})
-    elif args.workload == "w8a16_wcol":
-        nbytes, kms, wms = bench_w8a16(lh, K, W, stream, w_order="F")
-        out.update({"value": round(nbytes / (wms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 5),
-                    "dtype": "f16", "launches_per_step": SHORT_GROUP,
-                    "config": {"workload": "W8A16 16x4096 . 4096x14336 with W column-major (K contiguous per output "
-                                           "column), per-column fp16 scale, 6 rotating weight copies"},
-                    "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
-                    "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s", None)})
+                                         load_traffic(traffic_key) if traffic_key else None)})
     elif args.workload == "gemm_f16_256":
         flop, kms, wms = bench_gemm_layout(lh, "f16", 256, 3 | 4, K, W, stream, 0, group=SHORT_GROUP)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),

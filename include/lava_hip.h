@@ -376,14 +376,19 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
 /* W8A16 (coopmat2 per-element dequant callback, src/device/coopmat_intrinsics.jl:535-628
  * with the scale pointer in `extras`, :569-572):
  *   Y (M x N, fp32) = (X (M x K, fp16) * float(W (K x N, int8))) .* s[col] (fp16).
- * layout: bit0 X row-major, bit1 W row-major, bit2 Y row-major.  The weight-streaming
- * kernels take layout 7 with K a multiple of 32 and N a multiple of 128; any other layout
- * or shape runs on a generic kernel.  Every call is one launch.  Narrower N splits K across
- * workgroups through a split-K workspace the library owns, one per (device, stream), whose
- * last-arriving workgroup per column block adds the partial blocks: a call that grows it
- * allocates (hipMalloc) and so is not capturable -- make one call of the largest shape
- * outside capture first.  Calls on one stream from several threads are serialised around
- * the workspace; lava_hip_stream_destroy frees it.  Results are deterministic (fixed
+ * layout: bit0 X row-major, bit1 W row-major, bit2 Y row-major.  Two weight-streaming
+ * kernels, every call one launch:
+ *  - W column-major (K contiguous per output column), X and Y either way: N a multiple of
+ *    32, K of 16, 16-byte aligned X and W with leading dimensions multiples of 8 (X) and 16
+ *    (W); a column-major X needs M a multiple of 8 (or M == 1 with ldx == 1).  Whole
+ *    columns per workgroup, no workspace.
+ *  - W row-major, X and Y row-major (layout 7): K a multiple of 32, N of 128.  Narrower N
+ *    splits K across workgroups through a split-K workspace the library owns, one per
+ *    (device, stream), whose last-arriving workgroup per column block adds the partial
+ *    blocks: a call that grows it allocates (hipMalloc) and so is not capturable -- make one
+ *    call of the largest shape outside capture first.  Calls on one stream from several
+ *    threads are serialised around the workspace; lava_hip_stream_destroy frees it.
+ * Any other layout or shape runs on a generic kernel.  Results are deterministic (fixed
  * summation order). */
 int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N, int64_t K,
                         int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream);

@@ -255,12 +255,22 @@ __device__ __forceinline__ f16x8 km_dequant(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(f16x8, v) + bias;   // exact: w = (1152 + w) - 1152
 }
 
+// X column-major: the stage's X is [128 k-lines][16 rows] (32-byte lines), line L stored at
+// km_xline(L) -- lines 16 apart would share banks in a fragment read, the permutation moves every
+// other group of 16 to the other half of the banks -- and read with ds_read_b64_tr_b16: source
+// lane (jj, r4) = ((lane % 16) / 4, lane % 4) of group g points at a line and rows 4 r4 .. + 3, and
+// output lane r gets the 4 lines' values of row r.
+__device__ __forceinline__ int km_xline(int L) { return L ^ ((L >> 2) & 4); }
+typedef short km_s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) km_s16x4 km_lds_s16x4;
+
+template <bool XROW, bool YROW>
 __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16* __restrict__ X,
                                                                       const int8_t* __restrict__ W,
                                                                       const f16* __restrict__ scale,
                                                                       float* __restrict__ Y, int M, int N, int K,
                                                                       int64_t ldx, int64_t ldw, int64_t ldy) {
-    // per wavefront: two stage buffers, each W [32 columns][128 bytes] then X [16 rows][256 bytes]
+    // per wavefront: a ring of stage buffers, each W [32 columns][128 bytes] then X (4 KB)
     __shared__ __attribute__((aligned(16))) uint8_t stage_buf[KM_KSPLIT][KM_BUFS][KM_STAGE_BYTES];
     __shared__ __attribute__((aligned(16))) f32x4 red[KM_KSPLIT][KM_TILES][64];
     const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -274,9 +284,14 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
 
     // buffer resources over this workgroup's 32 columns of W and 16 rows of X
     const v4i w_rs = make_rsrc(W + (int64_t)n0 * ldw, (uint32_t)(KM_COLS * ldw));
-    const v4i x_rs = make_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(16 * ldx * 2));
+    // (X column-major: the host keeps M a multiple of 8, so a 16-byte chunk of 8 rows is wholly
+    // inside or wholly past M)
+    const v4i x_rs = XROW ? make_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(16 * ldx * 2))
+                          : make_rsrc(X + m0, (uint32_t)(K * ldx * 2));
     // W instruction i, lane l: column 8 i + l / 8, slot l % 8 holding chunk slot ^ (column % 8)
-    // X instruction j, lane l: row 4 j + l / 16, slot l % 16 holding chunk slot ^ (row % 16)
+    // X row-major, instruction j, lane l: row 4 j + l / 16, slot l % 16 holding chunk slot ^ (row % 16)
+    // X column-major, instruction j, lane l: LDS line 32 j + l / 2 (holding k-line km_xline of it),
+    // rows 8 (l % 2) .. + 7
     const int wc_lo = lane >> 3, w_slot = lane & 7;
     const int xr_lo = lane >> 4, x_slot = lane & 15;
     const int rows_ok = min(16, M - m0);
@@ -292,9 +307,16 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
         }
 #pragma unroll
         for (int j = 0; j < KM_X_INSTR; ++j) {
-            const int row = 4 * j + xr_lo;
-            const int kx = k0 + 8 * (x_slot ^ (row & 15));
-            const uint32_t off = (kx < K && row < rows_ok) ? (uint32_t)(row * ldx * 2 + 2 * kx) : OOB_OFS;
+            uint32_t off;
+            if constexpr (XROW) {
+                const int row = 4 * j + xr_lo;
+                const int kx = k0 + 8 * (x_slot ^ (row & 15));
+                off = (kx < K && row < rows_ok) ? (uint32_t)(row * ldx * 2 + 2 * kx) : OOB_OFS;
+            } else {
+                const int kx = k0 + km_xline(32 * j + (lane >> 1));
+                const int row = 8 * (lane & 1);
+                off = (kx < K && row < rows_ok) ? (uint32_t)((kx * ldx + row) * 2) : OOB_OFS;
+            }
             dma16(x_rs, off, 0, lds0 + KM_COLS * KM_SEG + 1024 * j);
         }
     };
@@ -326,9 +348,22 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
         uint4 wf[2][KM_TILES];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const int c0 = 8 * h + 2 * g;
-            xf[h][0] = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * (c0 ^ q));
-            xf[h][1] = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * ((c0 + 1) ^ q));
+            if constexpr (XROW) {
+                const int c0 = 8 * h + 2 * g;
+                xf[h][0] = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * (c0 ^ q));
+                xf[h][1] = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * ((c0 + 1) ^ q));
+            } else {
+                // lines 64 h + 16 g + 4 p + jj for the p-th group of 4 k-values
+                const int jj = (lane & 15) >> 2, r4 = lane & 3;
+                km_s16x4 v[4];
+#pragma unroll
+                for (int pp = 0; pp < 4; ++pp)
+                    v[pp] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (km_lds_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(
+                            xb + 32 * km_xline(64 * h + 16 * g + 4 * pp + jj) + 8 * r4));
+                xf[h][0] = __builtin_bit_cast(f16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+                xf[h][1] = __builtin_bit_cast(f16x8, __builtin_shufflevector(v[2], v[3], 0, 1, 2, 3, 4, 5, 6, 7));
+            }
 #pragma unroll
             for (int t = 0; t < KM_TILES; ++t) {
                 const int col = 16 * t + q;
@@ -370,7 +405,7 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = m0 + 4 * g + j;
-            if (row < M) Y[(int64_t)row * ldy + col] = f.v[j];
+            if (row < M) Y[YROW ? (int64_t)row * ldy + col : row + (int64_t)col * ldy] = f.v[j];
         }
     }
 }
@@ -403,6 +438,9 @@ static_assert(W8_COUNTER_BYTES >= 128 * sizeof(unsigned), "counter region");
 struct W8Plan {
     W8Path path = W8_GENERIC;
     int64_t cblocks = 0, mblocks = 0, total_steps = 0, ks = 0;
+    // W8_KMAJOR: X and Y orientation, and X's leading dimension as the kernel reads it
+    bool xrow = true, yrow = true;
+    int64_t kldx = 0;
     int splits = 1;
     int ksteps = 0;              // the per-wavefront step count of an unrolled instance, or 0
     // split-K workspace (W8_SPLIT with splits > 1): the arrival counters (one per column and
@@ -414,14 +452,27 @@ struct W8Plan {
 static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
                          uint32_t layout) {
     W8Plan p;
-    // W column-major, X and Y row-major
-    // (the kernel's 32-bit buffer offsets span 32 columns of W and 16 rows of X)
-    if (layout == 5u && N % KM_COLS == 0 && K > 0 && K % 16 == 0 && ldw % 16 == 0 && ldw >= K &&
-        ldw <= (int64_t(1) << 31) / KM_COLS && ldx % 8 == 0 && ldx >= K && ldx <= (int64_t(1) << 26) &&
-        aligned(W, 16) && aligned(X, 16) && N <= 0x7fffffff && M <= 0x7fffffff && (M + 15) / 16 <= 65535) {
+    // W column-major, X and Y either way (the kernel's 32-bit buffer offsets span 32 columns of
+    // W and 16 rows of X).  A column-major X of one row with unit stride is the same bytes as a
+    // row-major one; otherwise a column-major X needs M a multiple of 8 (whole 16-byte chunks of
+    // rows).
+    bool xrow = layout & 1u;
+    int64_t kldx = ldx;
+    if (!xrow && M == 1 && ldx == 1) {
+        xrow = true;
+        kldx = K;
+    }
+    const bool x_ok = xrow ? (kldx % 8 == 0 && kldx >= K && kldx <= (int64_t(1) << 26))
+                           : (M % 8 == 0 && ldx % 8 == 0 && ldx >= M && K * ldx <= (int64_t(1) << 30));
+    if ((layout & 2u) == 0 && x_ok && N % KM_COLS == 0 && K > 0 && K % 16 == 0 && ldw % 16 == 0 && ldw >= K &&
+        ldw <= (int64_t(1) << 31) / KM_COLS && aligned(W, 16) && aligned(X, 16) && N <= 0x7fffffff &&
+        M <= 0x7fffffff && (M + 15) / 16 <= 65535) {
         p.path = W8_KMAJOR;
         p.mblocks = (M + 15) / 16;
         p.cblocks = N / KM_COLS;
+        p.xrow = xrow;
+        p.yrow = layout & 4u;
+        p.kldx = kldx;
         return p;
     }
     const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 && K / W8_KSTEP <= 0x7fffffff &&
@@ -480,9 +531,15 @@ static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const voi
         return LAVA_HIP_OK;
     }
     if (p.path == W8_KMAJOR) {
-        hipLaunchKernelGGL(w8a16_kmajor_kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_KSPLIT), 0,
-                           s, (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, (int)M, (int)N, (int)K,
-                           ldx, ldw, ldy);
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_KSPLIT), 0, s,
+                               (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, (int)M, (int)N, (int)K,
+                               p.kldx, ldw, ldy);
+        };
+        if (p.xrow)
+            p.yrow ? go(w8a16_kmajor_kernel<true, true>) : go(w8a16_kmajor_kernel<true, false>);
+        else
+            p.yrow ? go(w8a16_kmajor_kernel<false, true>) : go(w8a16_kmajor_kernel<false, false>);
         LAVA_LAUNCH_CHECK("w8a16_kmajor_kernel");
         return LAVA_HIP_OK;
     }

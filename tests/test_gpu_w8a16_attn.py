@@ -118,23 +118,39 @@ def test_w8a16_weights_column_major(gpu, oracle, M, N, K):
     """W column-major (K contiguous per output column, the layout of a linear layer's weight),
     X and Y row-major: the whole-column kernel (no split-K); rows past M read as zero and
     more than one 16-row block of X; repeat calls identical."""
-    lh = gpu
-    announce(f"w8a16 W column-major M={M} N={N} K={K}")
-    X = lh.HIPDeviceArray("f16", (M, K), order="C")
+    w8a16_column_major_case(gpu, oracle, M, N, K, "C", "C")
+
+
+@pytest.mark.parametrize("M,N,K,xo,yo", [
+    # all column-major (the Julia default), X column-major only, Y column-major only
+    (16, 14336, 4096, "F", "F"), (16, 4096, 4096, "F", "C"), (16, 4096, 4096, "C", "F"),
+    # two row blocks, the second of 8 rows; a partial last stage
+    (24, 96, 400, "F", "C"), (8, 4096, 1040, "F", "F"), (40, 256, 1024, "F", "F"),
+    # one row with unit stride (read as row-major); M not a multiple of 8 (the generic kernel)
+    (1, 4096, 4096, "F", "F"), (5, 256, 128, "F", "F")])
+def test_w8a16_weights_column_major_orders(gpu, oracle, M, N, K, xo, yo):
+    """Column-major W with X and Y in either orientation."""
+    w8a16_column_major_case(gpu, oracle, M, N, K, xo, yo)
+
+
+def w8a16_column_major_case(lh, oracle, M, N, K, xo, yo):
+    announce(f"w8a16 W column-major M={M} N={N} K={K} X {xo} Y {yo}")
+    X = lh.HIPDeviceArray("f16", (M, K), order=xo)
     W = lh.HIPDeviceArray("i8", (K, N), order="F")
     s = lh.HIPDeviceArray("f16", (N,))
     lh.fill_normal(X, lh_mod.seed(5, 0))
     lh.fill_i8(W, lh_mod.seed(5, 1), symmetric=True)
     lh.fill_uniform(s, lh_mod.seed(5, 2), 0.001, 0.02)
-    Y = lh.HIPDeviceArray("f32", (M, N), order="C")
+    Y = lh.HIPDeviceArray("f32", (M, N), order=yo)
     Y.fill_bytes(0xFF)
     lh.w8a16(Y, X, W, s)
     y1 = Y.to_numpy()
     lh.w8a16(Y, X, W, s)
     np.testing.assert_array_equal(Y.to_numpy(), y1)
-    Wh = np.ascontiguousarray(W.to_numpy())          # K x N, row-major for the oracle
+    Xh = np.ascontiguousarray(X.to_numpy())          # row-major copies for the oracle
+    Wh = np.ascontiguousarray(W.to_numpy())
     rows = np.arange(M)
-    ref = oracle.w8a16_rows(X.to_numpy(), Wh, s.to_numpy(), N, K, K, N, rows)
+    ref = oracle.w8a16_rows(Xh, Wh, s.to_numpy(), N, K, K, N, rows)
     assert oracle.rel_frobenius(y1, ref) <= 1e-3
 
 
