@@ -457,7 +457,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
             const int d = 32 * dt + 8 * g4 + 4 * h;
             f16x4 v = {(f16)(o[dt][4 * g4 + 0] * inv), (f16)(o[dt][4 * g4 + 1] * inv),
                        (f16)(o[dt][4 * g4 + 2] * inv), (f16)(o[dt][4 * g4 + 3] * inv)};
-            *reinterpret_cast<f16x4*>(orow + d) = v;
+            __builtin_nontemporal_store(v, reinterpret_cast<f16x4*>(orow + d));
         }
 }
 
@@ -890,7 +890,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
             for (int i = 0; i < 16; ++i) {
                 const int row = 4 * i + lane / CH, c = lane % CH;
                 const f16x8 v = *(const lds_f16x8*)(uintptr_t)(ost[i / 8] + (uint32_t)((row % 32) * RB + ((c ^ (row & 15)) << 4)));
-                if (q0 + row < p.S && c < dch) *reinterpret_cast<f16x8*>(Ob + (int64_t)(q0 + row) * p.osl + 8 * c) = v;
+                if (q0 + row < p.S && c < dch) __builtin_nontemporal_store(v, reinterpret_cast<f16x8*>(Ob + (int64_t)(q0 + row) * p.osl + 8 * c));
             }
         } else {
 #pragma unroll
@@ -905,7 +905,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                         const int d = 32 * dt + 8 * g4 + 4 * h;
                         f16x4 v = {(f16)(o[dt][qh][4 * g4 + 0] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 1] * inv[qh]),
                                    (f16)(o[dt][qh][4 * g4 + 2] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 3] * inv[qh])};
-                        if (d < p.D) *reinterpret_cast<f16x4*>(orow + d) = v;
+                        if (d < p.D) __builtin_nontemporal_store(v, reinterpret_cast<f16x4*>(orow + d));
                     }
             }
         }
