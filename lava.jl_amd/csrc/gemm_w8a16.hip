@@ -303,7 +303,7 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
             const int col = 8 * i + wc_lo;
             const int kb = k0 + 16 * (w_slot ^ (col & 7));
             const uint32_t off = kb < K ? (uint32_t)(col * ldw + kb) : OOB_OFS;
-            dma16(w_rs, off, 0, lds0 + 1024 * i);
+            dma16_stream(w_rs, off, 0, lds0 + 1024 * i);   // W is read once
         }
 #pragma unroll
         for (int j = 0; j < KM_X_INSTR; ++j) {

@@ -42,6 +42,16 @@ __device__ __forceinline__ void dma16(const v4i& rsrc, uint32_t voffset, uint32_
                  : "memory");
 }
 
+// dma16 for data read once: the nontemporal hint lets L2 and the Infinity Cache evict the
+// lines early instead of displacing data that is read again (W8A16's weight stream: ~7 %
+// faster at the decode shape).
+__device__ __forceinline__ void dma16_stream(const v4i& rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+                 :
+                 : "s"(lds), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory");
+}
+
 // A masked lane's offset: past every range here (byte counts < 2^31), and
 // OOB_OFS + soffset (< 2^31) does not wrap, whether or not the range check counts soffset.
 constexpr uint32_t OOB_OFS = 0x80000000u;
