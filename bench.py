@@ -10,7 +10,7 @@ before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
-                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|attn_d96|w8a16_wrow|w8a16_julia|copy]
+                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -285,7 +285,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
-                             "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96",
+                             "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96", "attn_d256",
                              "copy", "vendor_bf16", "w8a16_wrow", "w8a16_julia"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
@@ -365,6 +365,13 @@ def main():
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "f16", "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=96 "
                                                            "(zero-padded to 128 on the score/output kernel; FLOP at D=96)"},
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "attn_d256":
+        flop, kms, wms = bench_attn(lh, K, W, stream, D=256)
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "f16", "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=256 "
+                                                           "(two launches per call, one per half of V and O; FLOP at D=256)"},
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_bf16_nn":

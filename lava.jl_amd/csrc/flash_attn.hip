@@ -104,9 +104,10 @@ __device__ __forceinline__ void fa_order(int nqb, int nbh, bool causal, int& bh,
 // matrix core and the VALU work at the same time instead of taking turns.
 //
 // K and V have three LDS stages each.  The MFMA phase of iteration kb issues the
-// DMA of K block kb + 2 and V block kb + 1 (4 instructions per wavefront) and each
-// phase ends with s_waitcnt vmcnt(4), so a wavefront's DMAs have landed by the end
-// of its next MFMA phase; the barrier after it publishes them.  The stage a DMA
+// DMA of K block kb + 2 and V block kb + 1 (4 instructions per wavefront at D = 128,
+// 6 with 512-byte K rows) and each phase ends with s_waitcnt vmcnt(that count), so a
+// wavefront's DMAs have landed by the end of its next MFMA phase; the barrier after
+// it publishes them.  The stage a DMA
 // overwrites was last read by the late wavefronts one phase before it is issued.
 //
 // LDS layout: K [64 keys][256 B] and V [64 keys][256 B] per stage, 16-byte chunks
@@ -158,36 +159,43 @@ __device__ __forceinline__ void f3_pin(const f32x16& v) {
 // phase issues), then the workgroup barrier.
 template <int N>
 __device__ __forceinline__ void f3_phase_end() {
-    static_assert(N == 4 || N == 2, "K and V tiles of 2 or 1 instructions per wavefront");
-    if constexpr (N == 4)
+    static_assert(N == 6 || N == 4 || N == 2, "K + V DMA instructions per wavefront and phase");
+    if constexpr (N == 6)
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else if constexpr (N == 4)
         asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else
         asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
     __syncthreads();
 }
 
-// DH = 128 or 64: the head dimension sets the row size (DH * 2 bytes = CH chunks of
-// 16 bytes), the number of S^T k-steps (DH / 16) and of O^T row tiles (DH / 32), and
-// the swizzles: K chunk ^ (key % 16) for 16-chunk rows, ^ ((key % 8) ^ (key / 8 % 2))
-// for 8-chunk rows (a fragment read, 32 keys x one chunk, spread over the banks);
-// V chunk ^ 4 (key % 4), resp. ^ 2 (key % 4) (a transposing read, 4 keys x 2 chunks per
-// 16-lane group).
-template <bool CAUSAL, int DH>
+// DQK (the Q / K head dimension: 64, 128 or 256) and DV (the V / O one: 64 or 128; DQK = 256
+// runs with DV = 128, once per half of V's columns) set the row sizes (D * 2 bytes = CH chunks
+// of 16 bytes), the number of S^T k-steps (DQK / 16) and of O^T row tiles (DV / 32), and the
+// swizzles: K chunk ^ (key % 16) for rows of 16 or more chunks, ^ ((key % 8) ^ (key / 8 % 2))
+// for 8-chunk rows (a fragment read, 32 keys x one chunk, spread over the banks); V chunk
+// ^ 4 (key % 4), resp. ^ 2 (key % 4) (a transposing read, 4 keys x 2 chunks per 16-lane group).
+template <bool CAUSAL, int DQK, int DV>
 __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p) {
-    static_assert(DH == 128 || DH == 64, "head dimension 128 or 64");
-    constexpr int RB = DH * 2;                             // bytes per K / V row
-    constexpr int CH = RB / 16;                            // 16-byte chunks per row
-    constexpr int TILE = F3_BK * RB;                       // one K or V block
-    constexpr int NKS = DH / 16;                           // S^T MFMAs per key tile
-    constexpr int NDT = DH / 32;                           // O^T row tiles
+    static_assert((DQK == DV && (DV == 128 || DV == 64)) || (DQK == 256 && DV == 128),
+                  "head dimensions 64, 128, or 256 for Q/K with 128 for V/O");
+    constexpr int RBK = DQK * 2, RBV = DV * 2;             // bytes per K / V row
+    constexpr int CHK = RBK / 16, CHV = RBV / 16;          // 16-byte chunks per row
+    constexpr int TILEK = F3_BK * RBK, TILEV = F3_BK * RBV;   // one K / V block
+    constexpr int NKS = DQK / 16;                          // S^T MFMAs per key tile
+    constexpr int NDT = DV / 32;                           // O^T row tiles
     constexpr int NPV = 4 * NDT;                           // O^T MFMAs per block
     constexpr int NOPS = NPV + 2 * NKS;                    // MFMAs of a full phase
-    constexpr int DPT = TILE / (1024 * F3_WAVES);          // DMA instructions per wavefront per tile
-    constexpr int RPI = 64 / CH;                           // rows per DMA instruction
-    __shared__ __attribute__((aligned(1024))) uint8_t kbuf[F3_STAGES][TILE];   // [stage][key][RB]
-    __shared__ __attribute__((aligned(1024))) uint8_t vbuf[F3_STAGES][TILE];
-    auto kswz = [](int row) { return CH == 16 ? (row & 15) : ((row & 7) ^ ((row >> 3) & 1)); };
-    auto vswz = [](int row) { return CH == 16 ? 4 * (row & 3) : 2 * (row & 3); };
+    constexpr int DPTK = TILEK / (1024 * F3_WAVES);        // DMA instructions per wavefront per tile
+    constexpr int DPTV = TILEV / (1024 * F3_WAVES);
+    constexpr int RPIK = 64 / CHK, RPIV = 64 / CHV;        // rows per DMA instruction
+    // LDS operand reads ahead of their MFMA (3 at DQK = 256, where the 16 Q^T fragments fill the
+    // registers)
+    constexpr int PREF = DQK == 256 ? 3 : F3_PREFETCH;
+    __shared__ __attribute__((aligned(1024))) uint8_t kbuf[F3_STAGES][TILEK];   // [stage][key][RBK]
+    __shared__ __attribute__((aligned(1024))) uint8_t vbuf[F3_STAGES][TILEV];
+    auto kswz = [](int row) { return CHK >= 16 ? (row & 15) : ((row & 7) ^ ((row >> 3) & 1)); };
+    auto vswz = [](int row) { return CHV == 16 ? 4 * (row & 3) : 2 * (row & 3); };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -217,23 +225,24 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
         }
     }
 
-    // ---- LDS-DMA: wave w moves rows [8 w, 8 w + 8) of a K or V tile in DPT
+    // ---- LDS-DMA: wave w moves rows [8 w, 8 w + 8) of a K (V) tile in DPTK (DPTV)
     // instructions: instruction i covers rows 8 w + RPI i + lane / CH, physical chunk lane % CH.
     const uint32_t row_bytes = (uint32_t)(p.sl * 2);
     const v4i rk = make_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
     const v4i rv = make_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
-    uint32_t voff_k[DPT], voff_v[DPT];
-    int dma_row[DPT];
+    uint32_t voff_k[DPTK], voff_v[DPTV];
 #pragma unroll
-    for (int i = 0; i < DPT; ++i) {
-        const int row = 8 * w + RPI * i + lane / CH;
-        dma_row[i] = row;
-        const int pc = lane % CH;
-        voff_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ kswz(row));
-        voff_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)(pc ^ vswz(row));
+    for (int i = 0; i < DPTK; ++i) {
+        const int row = 8 * w + RPIK * i + lane / CHK;
+        voff_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CHK) ^ kswz(row));
     }
-    const uint32_t lds_k = lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * RB;
-    const uint32_t lds_v = lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * RB;
+#pragma unroll
+    for (int i = 0; i < DPTV; ++i) {
+        const int row = 8 * w + RPIV * i + lane / CHV;
+        voff_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CHV) ^ vswz(row));
+    }
+    const uint32_t lds_k = lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * RBK;
+    const uint32_t lds_v = lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * RBV;
     const int nkb_s = (p.S + F3_BK - 1) / F3_BK;   // key blocks holding keys < S
     const int nkb = CAUSAL ? min((qb * F3_BQ + F3_BQ) / F3_BK, nkb_s) : nkb_s;
     // block j -> stage j % F3_STAGES; blocks past the end re-read the last one so
@@ -241,26 +250,41 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // A row at or past S gets an offset beyond the resource (2^31 > S * row bytes,
     // no wrap with soffset), so it reads zero whether or not the range check counts
     // soffset; its scores are masked.
-    auto issue = [&](const v4i& rsrc, const uint32_t* voff, uint32_t lds, int j) {
+    // (ntag: DMA instructions per tile; ctag: chunks per row, so 64 / CH rows per instruction)
+    auto issue = [&](auto ntag, auto ctag, const v4i& rsrc, const uint32_t* voff, uint32_t lds, int tile, int j) {
+        constexpr int DPT = decltype(ntag)::value, CH = decltype(ctag)::value;
         const int src = j < nkb ? j : nkb - 1;
         const uint32_t soff = (uint32_t)src * F3_BK * row_bytes;
-        const uint32_t dst = lds + (uint32_t)(j % F3_STAGES) * TILE;
+        const uint32_t dst = lds + (uint32_t)(j % F3_STAGES) * tile;
         uint32_t v[DPT];
 #pragma unroll
         for (int i = 0; i < DPT; ++i) v[i] = voff[i];
         if ((src + 1) * F3_BK > p.S) {   // uniform: only the ragged last block checks rows
 #pragma unroll
-            for (int i = 0; i < DPT; ++i) v[i] = src * F3_BK + dma_row[i] < p.S ? v[i] : 0x80000000u;
+            for (int i = 0; i < DPT; ++i)
+                v[i] = src * F3_BK + 8 * w + (64 / CH) * i + lane / CH < p.S ? v[i] : 0x80000000u;
         }
 #pragma unroll
         for (int i = 0; i < DPT; ++i) dma16(rsrc, v[i], soff, dst + 1024 * i);
     };
+    auto issue_k = [&](int j) {
+        issue(std::integral_constant<int, DPTK>{}, std::integral_constant<int, CHK>{}, rk, voff_k, lds_k, TILEK, j);
+    };
+    auto issue_v = [&](int j) {
+        issue(std::integral_constant<int, DPTV>{}, std::integral_constant<int, CHV>{}, rv, voff_v, lds_v, TILEV, j);
+    };
+    constexpr int DPP = DPTK + DPTV;   // DMA instructions per wavefront and MFMA phase
 
     // K fragment (kt, ks): row 32 kt + r32, logical chunk 2 ks + h, stored at chunk ^ kswz(row)
     // (kswz depends on row % 16 = r32 % 16 only)
-    int k_off[NKS];
+    // (2 ks + h) ^ kswz = 2 ks ^ (h ^ kswz) with kswz < 16 and the row's byte offset a multiple of
+    // 32 chunks, so k_off[ks] = k_off[0] ^ 32 ks; at DQK = 256 that XOR is done per read instead of
+    // holding 16 offsets in registers
+    constexpr bool K_XOR = NKS > 8;
+    int k_off[K_XOR ? 1 : NKS];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ++ks) k_off[ks] = r32 * RB + (((2 * ks + h) ^ kswz(r32)) << 4);
+    for (int ks = 0; ks < (K_XOR ? 1 : NKS); ++ks) k_off[ks] = r32 * RBK + (((2 * ks + h) ^ kswz(r32)) << 4);
+    auto k_ofs = [&](int ks) { return K_XOR ? (k_off[0] ^ (32 * ks)) : k_off[ks]; };
     // V^T fragment (dt, kk = 32 kt + 16 ks, read t = 0/1): source lane jj = (lane % 16) / 4,
     // q = lane % 4, dh = (lane / 16) % 2 addresses V[kk + 8 t + 4 h + jj][32 dt + 16 dh + 4 q],
     // logical chunk 4 dt + 2 dh + q / 2 stored at chunk ^ vswz(jj) (jj = key % 4 as kk % 8 == 0).
@@ -269,7 +293,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
         const int jj = (lane & 15) >> 2, q = lane & 3, dh = (lane >> 4) & 1;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
-            v_off[dt] = (4 * h + jj) * RB + (((4 * dt + 2 * dh + (q >> 1)) ^ vswz(jj)) << 4) + ((q & 1) << 3);
+            v_off[dt] = (4 * h + jj) * RBV + (((4 * dt + 2 * dh + (q >> 1)) ^ vswz(jj)) << 4) + ((q & 1) << 3);
     }
 
     f32x16 o[NDT];
@@ -286,17 +310,17 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // The MFMA phase as one list of NOPS operations -- ops [0, NPV): O^T += V^T P^T
     // for the previous block (kt = i / (2 NDT), ks = i / NDT % 2, dt = i % NDT); ops
     // [NPV, NOPS): S^T = K Q^T (ks = (i - NPV) / 2, kt = i % 2) -- whose LDS operand
-    // reads run F3_PREFETCH operations ahead of the MFMAs (the partner wavefront is in
+    // reads run PREF operations ahead of the MFMAs (the partner wavefront is in
     // its softmax phase, so nothing else hides the LDS latency).
     auto read_op = [&](int i, const uint8_t* vbase, const uint8_t* kbase) -> f16x8 {
         if (i < NPV) {
             const int kk = 32 * (i / (2 * NDT)) + 16 * ((i / NDT) & 1), dt = i % NDT;
-            const f3_s16x4 lo = f3_read_tr(vbase + v_off[dt] + kk * RB);
-            const f3_s16x4 hi = f3_read_tr(vbase + v_off[dt] + (kk + 8) * RB);
+            const f3_s16x4 lo = f3_read_tr(vbase + v_off[dt] + kk * RBV);
+            const f3_s16x4 hi = f3_read_tr(vbase + v_off[dt] + (kk + 8) * RBV);
             return __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
         const int j = i - NPV;
-        return *reinterpret_cast<const f16x8*>(kbase + k_off[j >> 1] + (j & 1) * 32 * RB);
+        return *reinterpret_cast<const f16x8*>(kbase + k_ofs(j >> 1) + (j & 1) * 32 * RBK);
     };
     auto mma_op = [&](int i, f16x8 a) {
         if (i < NPV) {
@@ -310,14 +334,14 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     auto mfma_phase = [&](auto pv_tag, auto s_tag, const uint8_t* vbase, const uint8_t* kbase) {
         constexpr int first = decltype(pv_tag)::value ? 0 : NPV;
         constexpr int last = decltype(s_tag)::value ? NOPS : NPV;
-        f16x8 buf[F3_PREFETCH];
+        f16x8 buf[PREF];
 #pragma unroll
-        for (int t = 0; t < F3_PREFETCH; ++t)
+        for (int t = 0; t < PREF; ++t)
             if (first + t < last) buf[t] = read_op(first + t, vbase, kbase);
 #pragma unroll
         for (int i = first; i < last; ++i) {
-            const f16x8 a = buf[(i - first) % F3_PREFETCH];
-            if (i + F3_PREFETCH < last) buf[(i - first) % F3_PREFETCH] = read_op(i + F3_PREFETCH, vbase, kbase);
+            const f16x8 a = buf[(i - first) % PREF];
+            if (i + PREF < last) buf[(i - first) % PREF] = read_op(i + PREF, vbase, kbase);
             mma_op(i, a);
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -327,7 +351,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
         }
     };
 
-    issue(rk, voff_k, lds_k, 0);
+    issue_k(0);
     // Consume Q here so the compiler's own wait for its loads happens once, before
     // the loop, instead of as vmcnt waits inside it (which would also cover the
     // DMAs issued in the loop, since it does not count those).
@@ -336,8 +360,8 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
         const uint4 u = __builtin_bit_cast(uint4, qf[ks]);
         asm volatile("" ::"v"(u.x), "v"(u.y), "v"(u.z), "v"(u.w));
     }
-    issue(rk, voff_k, lds_k, 1);
-    issue(rv, voff_v, lds_v, 0);
+    issue_k(1);
+    issue_v(0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (late) __builtin_amdgcn_s_barrier();
@@ -409,8 +433,8 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // tiles are loaded cooperatively, so each wavefront issues its share of every
     // one, active or not, and passes the same barriers.
     auto dma = [&](int kb) {
-        issue(rk, voff_k, lds_k, kb + 2);
-        issue(rv, voff_v, lds_v, kb + 1);
+        issue_k(kb + 2);
+        issue_v(kb + 1);
     };
     auto vb = [&](int kb) { return &vbuf[(kb + F3_STAGES - 1) % F3_STAGES][0]; };   // V of block kb - 1
     auto kbuf_of = [&](int kb) { return &kbuf[kb % F3_STAGES][0]; };
@@ -420,27 +444,27 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     // iteration 0: S only
     dma(0);
     mfma_phase(f3_tag<false>{}, f3_tag<true>{}, vb(0), kbuf_of(0));
-    f3_phase_end<2 * DPT>();
+    f3_phase_end<DPP>();
     softmax(0);
-    f3_phase_end<2 * DPT>();
+    f3_phase_end<DPP>();
     // iterations 1 .. last: O += V^T P^T for block kb - 1, then S for block kb
     for (int kb = 1; kb <= last; ++kb) {
         dma(kb);
         mfma_phase(f3_tag<true>{}, f3_tag<true>{}, vb(kb), kbuf_of(kb));
-        f3_phase_end<2 * DPT>();
+        f3_phase_end<DPP>();
         softmax(kb);
-        f3_phase_end<2 * DPT>();
+        f3_phase_end<DPP>();
     }
     // iteration last + 1: the final O update
     dma(last + 1);
     mfma_phase(f3_tag<true>{}, f3_tag<false>{}, vb(last + 1), kbuf_of(last + 1));
-    f3_phase_end<2 * DPT>();
-    f3_phase_end<2 * DPT>();
+    f3_phase_end<DPP>();
+    f3_phase_end<DPP>();
     // remaining iterations (causal: blocks past this wavefront's queries)
     for (int kb = last + 2; kb <= nkb; ++kb) {
         dma(kb);
-        f3_phase_end<2 * DPT>();
-        f3_phase_end<2 * DPT>();
+        f3_phase_end<DPP>();
+        f3_phase_end<DPP>();
     }
     if (!late) __builtin_amdgcn_s_barrier();
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -988,11 +1012,11 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     p.D = (int)D;
     hipStream_t s = as_stream(stream);
 
-    // D = 128 or 64 with 16-byte rows: the MFMA kernels.  D = 128 runs on flash_fwd5_kernel
-    // (score/output wavefront pairs; the scale folds into Q^T, so any sign), D = 64 with a
-    // positive scale on flash_fwd3_kernel (ping-pong wavefront pairs; its base-2 running
-    // maximum assumes one); both take any S (a ragged last block of queries or keys is
-    // zero-filled and masked).  LAVA_HIP_ATTN_KERNEL=3 in the environment runs D = 128 with a
+    // D <= 128 (a multiple of 8) with 16-byte rows, and D = 256: the MFMA kernels.  D <= 128 runs
+    // on flash_fwd5_kernel (score/output wavefront pairs, zero-padded to 128; the scale folds into
+    // Q^T, so any sign), D = 64 and D = 256 with a positive scale on flash_fwd3_kernel (ping-pong
+    // wavefront pairs; its base-2 running maximum assumes one); all take any S (a ragged last
+    // block of queries or keys is zero-filled and masked).  LAVA_HIP_ATTN_KERNEL=3 in the environment runs D = 128 with a
     // positive scale on flash_fwd3_kernel as well (a comparison switch; both are
     // parity-tested).  Everything else runs on flash_generic_kernel.
     bool lay_ok = D >= 8 && D <= FA_D && D % 8 == 0 && strides[0] == 1 && os[0] == 1;
@@ -1005,6 +1029,12 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     const bool want3 = sel && sel[0] == '3';
     const bool fast3 = lay_ok && scale > 0.f && (D == 64 || (D == FA_D && want3)) && blocks3 <= 0x7fffffff;
     const bool fast5 = lay_ok && !fast3 && blocks5 <= 0x7fffffff;
+    // D = 256 with a positive scale: the ping-pong kernel over Q/K rows of 512 bytes, once per
+    // 128-column half of V and O (the scores are computed twice)
+    bool fast256 = D == 256 && scale > 0.f && strides[0] == 1 && os[0] == 1 && blocks3 <= 0x7fffffff &&
+                   aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8) &&
+                   S * strides[1] * 2 < ((int64_t)1 << 31);
+    for (int i = 1; i < 4; ++i) fast256 = fast256 && strides[i] % 8 == 0 && os[i] % 4 == 0;
     if (fast5) {   // any D <= 128, a multiple of 8 (zero-padded to 128)
         if (p.causal)
             hipLaunchKernelGGL((flash_fwd5_kernel<true>), dim3((unsigned)blocks5), dim3(128 * F5_PAIRS), 0, s, p);
@@ -1017,15 +1047,30 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
         const dim3 grid((unsigned)blocks3);
         if (D == 64) {
             if (p.causal)
-                hipLaunchKernelGGL((flash_fwd3_kernel<true, 64>), grid, dim3(64 * F3_WAVES), 0, s, p);
+                hipLaunchKernelGGL((flash_fwd3_kernel<true, 64, 64>), grid, dim3(64 * F3_WAVES), 0, s, p);
             else
-                hipLaunchKernelGGL((flash_fwd3_kernel<false, 64>), grid, dim3(64 * F3_WAVES), 0, s, p);
+                hipLaunchKernelGGL((flash_fwd3_kernel<false, 64, 64>), grid, dim3(64 * F3_WAVES), 0, s, p);
         } else if (p.causal) {
-            hipLaunchKernelGGL((flash_fwd3_kernel<true, 128>), grid, dim3(64 * F3_WAVES), 0, s, p);
+            hipLaunchKernelGGL((flash_fwd3_kernel<true, 128, 128>), grid, dim3(64 * F3_WAVES), 0, s, p);
         } else {
-            hipLaunchKernelGGL((flash_fwd3_kernel<false, 128>), grid, dim3(64 * F3_WAVES), 0, s, p);
+            hipLaunchKernelGGL((flash_fwd3_kernel<false, 128, 128>), grid, dim3(64 * F3_WAVES), 0, s, p);
         }
         LAVA_LAUNCH_CHECK("flash_fwd3_kernel");
+        return LAVA_HIP_OK;
+    }
+    if (fast256) {
+        // two launches, each over the full 256-wide scores and one 128-column half of V and O
+        const dim3 grid((unsigned)blocks3);
+        for (int half = 0; half < 2; ++half) {
+            FaParams ph = p;
+            ph.V = p.V + 128 * half;
+            ph.O = p.O + 128 * half;
+            if (p.causal)
+                hipLaunchKernelGGL((flash_fwd3_kernel<true, 256, 128>), grid, dim3(64 * F3_WAVES), 0, s, ph);
+            else
+                hipLaunchKernelGGL((flash_fwd3_kernel<false, 256, 128>), grid, dim3(64 * F3_WAVES), 0, s, ph);
+            LAVA_LAUNCH_CHECK("flash_fwd3_kernel");
+        }
         return LAVA_HIP_OK;
     }
     const int64_t rows = S * H * B;

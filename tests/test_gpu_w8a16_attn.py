@@ -294,15 +294,43 @@ def test_flash_fast_d64(gpu, oracle, causal, L):
     assert not np.isnan(O.to_numpy()).any()
 
 
-@pytest.mark.parametrize("E,L,causal", [(20, 200, True), (100, 130, False), (160, 100, True), (256, 64, False)])
+@pytest.mark.parametrize("E,L,causal", [(20, 200, True), (100, 130, False), (160, 100, True), (200, 64, False)])
 def test_flash_generic_path(gpu, oracle, E, L, causal):
-    """Head dims the MFMA kernels do not take (not a multiple of 8, or above 128)."""
+    """Head dims the MFMA kernels do not take (not a multiple of 8, or above 128 other than 256)."""
     lh = gpu
     announce(f"flash generic D={E} S={L} causal={causal}")
     Q, K, V = attn_inputs(lh, E, L, 2, 1)
     O = lh.HIPDeviceArray("f16", (E, L, 2, 1))
     lh.flash_attn_fwd(O, Q, K, V, scale=0.2, causal=causal)
     check_heads(oracle, Q, K, V, O, 0.2, causal, [(0, 0), (0, 1)], np.arange(L))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("L,H,B", [(64, 2, 1), (300, 2, 1), (1000, 1, 2), (2048, 2, 1)])
+def test_flash_d256(gpu, oracle, causal, L, H, B):
+    """D = 256: the ping-pong kernel over 512-byte Q/K rows, launched once per 128-column half
+    of V and O (scores computed in each); ragged S, several heads and batches."""
+    lh = gpu
+    announce(f"flash D=256 S={L} H={H} B={B} causal={causal}")
+    Q, K, V = attn_inputs(lh, 256, L, H, B)
+    O = lh.HIPDeviceArray("f16", (256, L, H, B))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, causal=causal)
+    rows = np.arange(L) if L <= 300 else np.unique(np.concatenate([np.arange(0, L, 13), [L - 1]]))
+    check_heads(oracle, Q, K, V, O, 1 / math.sqrt(256), causal, [(b, h) for b in range(B) for h in range(H)], rows)
+    assert not np.isnan(O.to_numpy()).any()
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_d256_nonpositive_scale(gpu, oracle, causal):
+    """D = 256 with a negative scale runs on the generic kernel (the ping-pong kernel's running
+    maximum assumes a positive scale)."""
+    lh = gpu
+    announce(f"flash D=256 scale<0 causal={causal}")
+    Q, K, V = attn_inputs(lh, 256, 100, 1, 1)
+    O = lh.HIPDeviceArray("f16", (256, 100, 1, 1))
+    lh.flash_attn_fwd(O, Q, K, V, scale=-0.0625, causal=causal)
+    check_heads(oracle, Q, K, V, O, -0.0625, causal, [(0, 0)], np.arange(100))
 
 
 @pytest.mark.parametrize("E,L,causal", [(32, 200, True), (16, 32, True), (96, 130, False), (48, 100, False),
