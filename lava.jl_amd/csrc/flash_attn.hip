@@ -56,6 +56,7 @@ struct FaParams {
     int causal;
     int o16;                 // O and its strides allow 16-byte row stores
     int D;                   // head dimension (the score/output kernel zero-pads it to 128)
+    int dv;                  // the ping-pong kernel at DQK = 256: V / O columns of this launch's half
 };
 
 // Workgroup -> (batch * head, query block).  Workgroups are dispatched round-robin
@@ -221,7 +222,8 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
         for (int ks = 0; ks < NKS; ++ks) qf[ks] = f16x8{};
         if (my_q < p.S) {
 #pragma unroll
-            for (int ks = 0; ks < NKS; ++ks) qf[ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
+            for (int ks = 0; ks < NKS; ++ks)
+                if (DQK != 256 || 16 * ks + 8 * h < p.D) qf[ks] = *reinterpret_cast<const f16x8*>(qrow + 16 * ks);
         }
     }
 
@@ -231,15 +233,21 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
     const v4i rk = make_rsrc(p.K + head, (uint32_t)p.S * row_bytes);
     const v4i rv = make_rsrc(p.V + head, (uint32_t)p.S * row_bytes);
     uint32_t voff_k[DPTK], voff_v[DPTV];
+    // At DQK = 256 a head dimension D < 256 is zero-padded: a lane whose logical chunk lies at or
+    // past D (K) or past this launch's dv columns (V) takes an offset beyond the resource, so the
+    // DMA writes zeros (zero K columns add nothing to the scores; zero V columns give O columns
+    // that are not stored).
 #pragma unroll
     for (int i = 0; i < DPTK; ++i) {
         const int row = 8 * w + RPIK * i + lane / CHK;
-        voff_k[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CHK) ^ kswz(row));
+        const int c = (lane % CHK) ^ kswz(row);
+        voff_k[i] = (DQK != 256 || 8 * c < p.D) ? (uint32_t)row * row_bytes + 16u * (uint32_t)c : 0x80000000u;
     }
 #pragma unroll
     for (int i = 0; i < DPTV; ++i) {
         const int row = 8 * w + RPIV * i + lane / CHV;
-        voff_v[i] = (uint32_t)row * row_bytes + 16u * (uint32_t)((lane % CHV) ^ vswz(row));
+        const int c = (lane % CHV) ^ vswz(row);
+        voff_v[i] = (DQK != 256 || 8 * c < p.dv) ? (uint32_t)row * row_bytes + 16u * (uint32_t)c : 0x80000000u;
     }
     const uint32_t lds_k = lds_addr(&kbuf[0][0]) + (uint32_t)w * 8 * RBK;
     const uint32_t lds_v = lds_addr(&vbuf[0][0]) + (uint32_t)w * 8 * RBV;
@@ -481,7 +489,7 @@ __global__ void __launch_bounds__(64 * F3_WAVES, 1) flash_fwd3_kernel(FaParams p
             const int d = 32 * dt + 8 * g4 + 4 * h;
             f16x4 v = {(f16)(o[dt][4 * g4 + 0] * inv), (f16)(o[dt][4 * g4 + 1] * inv),
                        (f16)(o[dt][4 * g4 + 2] * inv), (f16)(o[dt][4 * g4 + 3] * inv)};
-            __builtin_nontemporal_store(v, reinterpret_cast<f16x4*>(orow + d));
+            if (DQK != 256 || d < p.dv) __builtin_nontemporal_store(v, reinterpret_cast<f16x4*>(orow + d));
         }
 }
 
@@ -1010,6 +1018,7 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     p.causal = causal != 0;
     p.o16 = aligned(O, 16) && os[1] % 8 == 0 && os[2] % 8 == 0 && os[3] % 8 == 0;
     p.D = (int)D;
+    p.dv = (int)D;
     hipStream_t s = as_stream(stream);
 
     // D <= 128 (a multiple of 8) with 16-byte rows, and D = 256: the MFMA kernels.  D <= 128 runs
@@ -1029,9 +1038,10 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     const bool want3 = sel && sel[0] == '3';
     const bool fast3 = lay_ok && scale > 0.f && (D == 64 || (D == FA_D && want3)) && blocks3 <= 0x7fffffff;
     const bool fast5 = lay_ok && !fast3 && blocks5 <= 0x7fffffff;
-    // D = 256 with a positive scale: the ping-pong kernel over Q/K rows of 512 bytes, once per
-    // 128-column half of V and O (the scores are computed twice)
-    bool fast256 = D == 256 && scale > 0.f && strides[0] == 1 && os[0] == 1 && blocks3 <= 0x7fffffff &&
+    // 128 < D <= 256 (a multiple of 8) with a positive scale: the ping-pong kernel over Q/K rows
+    // zero-padded to 256, once per 128-column half of V and O (the scores are computed twice)
+    bool fast256 = D > FA_D && D <= 256 && D % 8 == 0 && scale > 0.f && strides[0] == 1 && os[0] == 1 &&
+                   blocks3 <= 0x7fffffff &&
                    aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8) &&
                    S * strides[1] * 2 < ((int64_t)1 << 31);
     for (int i = 1; i < 4; ++i) fast256 = fast256 && strides[i] % 8 == 0 && os[i] % 4 == 0;
@@ -1065,6 +1075,7 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
             FaParams ph = p;
             ph.V = p.V + 128 * half;
             ph.O = p.O + 128 * half;
+            ph.dv = (int)(D - 128 * half < 128 ? D - 128 * half : 128);
             if (p.causal)
                 hipLaunchKernelGGL((flash_fwd3_kernel<true, 256, 128>), grid, dim3(64 * F3_WAVES), 0, s, ph);
             else

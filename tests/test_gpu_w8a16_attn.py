@@ -294,9 +294,9 @@ def test_flash_fast_d64(gpu, oracle, causal, L):
     assert not np.isnan(O.to_numpy()).any()
 
 
-@pytest.mark.parametrize("E,L,causal", [(20, 200, True), (100, 130, False), (160, 100, True), (200, 64, False)])
+@pytest.mark.parametrize("E,L,causal", [(20, 200, True), (100, 130, False), (164, 100, True), (250, 64, False)])
 def test_flash_generic_path(gpu, oracle, E, L, causal):
-    """Head dims the MFMA kernels do not take (not a multiple of 8, or above 128 other than 256)."""
+    """Head dims the MFMA kernels do not take (not a multiple of 8)."""
     lh = gpu
     announce(f"flash generic D={E} S={L} causal={causal}")
     Q, K, V = attn_inputs(lh, E, L, 2, 1)
@@ -318,6 +318,23 @@ def test_flash_d256(gpu, oracle, causal, L, H, B):
     lh.flash_attn_fwd(O, Q, K, V, causal=causal)
     rows = np.arange(L) if L <= 300 else np.unique(np.concatenate([np.arange(0, L, 13), [L - 1]]))
     check_heads(oracle, Q, K, V, O, 1 / math.sqrt(256), causal, [(b, h) for b in range(B) for h in range(H)], rows)
+    assert not np.isnan(O.to_numpy()).any()
+
+
+@pytest.mark.parametrize("E,L,causal", [(136, 200, True), (160, 100, False), (192, 300, True), (200, 64, False),
+                                         (248, 777, True), (192, 1000, False)])
+def test_flash_padded_head_dims_above_128(gpu, oracle, E, L, causal):
+    """128 < D < 256 (multiples of 8) on the ping-pong kernel zero-padded to 256: the padding
+    columns of Q and K read zero; the second launch covers V and O columns 128 .. D - 1 and
+    writes no others."""
+    lh = gpu
+    announce(f"flash padded D={E} S={L} causal={causal}")
+    Q, K, V = attn_inputs(lh, E, L, 2, 1)
+    O = lh.HIPDeviceArray("f16", (E, L, 2, 1))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, scale=0.1, causal=causal)
+    rows = np.arange(L) if L <= 300 else np.unique(np.concatenate([np.arange(0, L, 7), [L - 1]]))
+    check_heads(oracle, Q, K, V, O, 0.1, causal, [(0, 0), (0, 1)], rows)
     assert not np.isnan(O.to_numpy()).any()
 
 
