@@ -382,7 +382,8 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
  *    32, K of 16, 16-byte aligned X and W with leading dimensions multiples of 8 (X) and 16
  *    (W); a column-major X needs M a multiple of 8 (or M == 1 with ldx == 1).  Whole
  *    columns per workgroup, no workspace.
- *  - W row-major, X and Y row-major (layout 7): K a multiple of 32, N of 128.  Narrower N
+ *  - W row-major, X and Y either way: K a multiple of 32, N of 128 (a row-major X 16-byte
+ *    aligned with ldx a multiple of 8).  Narrower N
  *    splits K across workgroups through a split-K workspace the library owns, one per
  *    (device, stream), whose last-arriving workgroup per column block adds the partial
  *    blocks: a call that grows it allocates (hipMalloc) and so is not capturable -- make one

@@ -59,11 +59,14 @@ struct ScaleStrided {
 // Wavefront gw = split * W8_WAVES + w takes the 32-row steps [gw ks, min((gw + 1) ks,
 // total_steps)) of K.  KSTEPS > 0: the host guarantees exactly KSTEPS each, fully
 // unrolled; KSTEPS == 0: any count (zero included), in unrolled groups of W8_DEPTH.
+// xrow / yrow (wave-uniform): X and Y row-major, else column-major (a lane then gathers its 8
+// k-values of X with 2-byte loads, ldx apart; Y is stored column by column).
 template <int KSTEPS>
 __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
                                                     const f16* __restrict__ scale, float* __restrict__ Y,
                                                     float* partial, unsigned* counters, int M, int N, int64_t ldx,
-                                                    int64_t ldw, int64_t ldy, int splits, int ks, int total_steps) {
+                                                    int64_t ldw, int64_t ldy, int splits, int ks, int total_steps,
+                                                    int xrow, int yrow) {
     __shared__ __attribute__((aligned(16))) float red[W8_WAVES][16][W8_COLS];
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -79,7 +82,7 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
 
     // A operand rows: X[m0 + q][k .. k + 8) for this lane's group; rows >= M read as 0
     const bool xrow_ok = (m0 + q) < M;
-    const f16* xp = X + (int64_t)(m0 + q) * ldx + k_wave + 8 * g;
+    const f16* xp = xrow ? X + (int64_t)(m0 + q) * ldx + k_wave + 8 * g : X + (k_wave + 8 * g) * ldx + (m0 + q);
     const int8_t* wp = W + (k_wave + 8 * g) * ldw + n0 + 8 * q;
 
     f32x4 acc[8];
@@ -100,7 +103,16 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
         for (int r = 0; r < 8; ++r)
             rows[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(wp + ((int64_t)s * W8_KSTEP + r) * ldw));
         xa = make_uint4(0, 0, 0, 0);
-        if (xrow_ok) xa = *reinterpret_cast<const uint4*>(xp + s * W8_KSTEP);
+        if (xrow_ok) {
+            if (xrow) {
+                xa = *reinterpret_cast<const uint4*>(xp + s * W8_KSTEP);
+            } else {
+                f16x8 xv;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xv[j] = xp[((int64_t)s * W8_KSTEP + j) * ldx];
+                xa = __builtin_bit_cast(uint4, xv);
+            }
+        }
     };
     // step s from ring slot u (a compile-time constant at every call), refilling it with step s + DEPTH
     auto step = [&](int u, int s) {
@@ -202,9 +214,14 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
         v = y;
     }
     if (grow < M) {
-        float* yp = Y + (int64_t)grow * ldy + n0 + c4;
+        if (yrow) {
+            float* yp = Y + (int64_t)grow * ldy + n0 + c4;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) yp[i] = v[i];
+            for (int i = 0; i < 4; ++i) yp[i] = v[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Y[grow + (int64_t)(n0 + c4 + i) * ldy] = v[i];
+        }
     }
 }
 
@@ -438,7 +455,7 @@ static_assert(W8_COUNTER_BYTES >= 128 * sizeof(unsigned), "counter region");
 struct W8Plan {
     W8Path path = W8_GENERIC;
     int64_t cblocks = 0, mblocks = 0, total_steps = 0, ks = 0;
-    // W8_KMAJOR: X and Y orientation, and X's leading dimension as the kernel reads it
+    // X and Y orientation; W8_KMAJOR: X's leading dimension as the kernel reads it
     bool xrow = true, yrow = true;
     int64_t kldx = 0;
     int splits = 1;
@@ -475,11 +492,16 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
         p.kldx = kldx;
         return p;
     }
-    const bool fast = layout == 7u && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 && K / W8_KSTEP <= 0x7fffffff &&
-                      ldw % 8 == 0 && ldx % 8 == 0 && aligned(W, 8) && aligned(X, 16) && N <= 0x7fffffff &&
-                      M <= 0x7fffffff && (M + 15) / 16 <= 65535;
+    // W row-major, X and Y either way (a row-major X in 16-byte loads)
+    const bool x_row = layout & 1u;
+    const bool fast = (layout & 2u) && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 &&
+                      K / W8_KSTEP <= 0x7fffffff && ldw % 8 == 0 && aligned(W, 8) &&
+                      (x_row ? ldx % 8 == 0 && aligned(X, 16) : true) && N <= 0x7fffffff && M <= 0x7fffffff &&
+                      (M + 15) / 16 <= 65535;
     if (!fast) return p;
     p.path = W8_SPLIT;
+    p.xrow = x_row;
+    p.yrow = layout & 4u;
     p.mblocks = (M + 15) / 16;
     p.total_steps = K / W8_KSTEP;
     p.cblocks = N / W8_COLS;
@@ -507,7 +529,8 @@ static void launch_split_ks(const W8Plan& p, const void* X, const void* W, const
                             hipStream_t s) {
     hipLaunchKernelGGL(w8a16_kernel<KS>, dim3((unsigned)p.cblocks, (unsigned)p.splits, (unsigned)p.mblocks),
                        dim3(64 * W8_WAVES), 0, s, (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, partial,
-                       counters, (int)M, (int)N, ldx, ldw, ldy, p.splits, (int)p.ks, (int)p.total_steps);
+                       counters, (int)M, (int)N, ldx, ldw, ldy, p.splits, (int)p.ks, (int)p.total_steps, (int)p.xrow,
+                       (int)p.yrow);
 }
 
 // Enqueues the plan's kernel on `s`.  `ws` holds p.scratch_bytes when p.splits > 1, its

@@ -50,6 +50,29 @@ def test_w8a16(gpu, oracle, M, N, K):
     np.testing.assert_array_equal(Y.to_numpy(), Y2.to_numpy())
 
 
+@pytest.mark.parametrize("M,N,K,xo,yo", [(16, 4096, 4096, "F", "C"), (16, 4096, 4096, "C", "F"), (16, 14336, 4096, "F", "F"),
+                                         (5, 256, 1024, "F", "F"), (33, 6144, 1120, "F", "C"), (1, 1024, 384, "C", "F")])
+def test_w8a16_row_major_w_orders(gpu, oracle, M, N, K, xo, yo):
+    """Row-major W with X and/or Y column-major: the split-K stream kernel (column-major X
+    gathered with 2-byte loads, column-major Y stored column by column); repeat calls identical."""
+    lh = gpu
+    announce(f"w8a16 W row-major M={M} N={N} K={K} X {xo} Y {yo}")
+    X = lh.HIPDeviceArray("f16", (M, K), order=xo)
+    W = lh.HIPDeviceArray("i8", (K, N), order="C")
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(X, lh_mod.seed(7, 0))
+    lh.fill_i8(W, lh_mod.seed(7, 1), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(7, 2), 0.001, 0.02)
+    Y = lh.HIPDeviceArray("f32", (M, N), order=yo)
+    Y.fill_bytes(0xFF)
+    lh.w8a16(Y, X, W, s)
+    y1 = Y.to_numpy()
+    lh.w8a16(Y, X, W, s)
+    np.testing.assert_array_equal(Y.to_numpy(), y1)
+    ref = oracle.w8a16_rows(np.ascontiguousarray(X.to_numpy()), W.to_numpy(), s.to_numpy(), N, K, K, N, np.arange(M))
+    assert oracle.rel_frobenius(y1, ref) <= 1e-3
+
+
 def test_w8a16_two_threads_one_stream(gpu, oracle):
     """Split-K calls from two host threads on the NULL stream: each call's kernel pair is
     enqueued whole, so neither thread's partial sums are overwritten by the other's."""
@@ -176,8 +199,8 @@ def test_w8a16_weights_column_major_strided(gpu, oracle, M, N, K, padx, padw):
 
 def test_w8a16_column_major_generic(gpu, oracle):
     lh = gpu
-    announce("w8a16 column-major operands (generic kernel)")
-    M, N, K = 8, 96, 64
+    announce("w8a16 column-major operands, N not a multiple of 32 (generic kernel)")
+    M, N, K = 8, 100, 64
     X, W, s = w8_inputs(lh, M, N, K, order="F")
     Y = lh.HIPDeviceArray("f32", (M, N), order="F")
     lh.w8a16(Y, X, W, s)
