@@ -28,9 +28,8 @@
 //    epilogue stages them through LDS and stores whole 512-byte row runs;
 //  * workgroups are renumbered XCD by XCD (xcd_tile) so that the tiles one XCD
 //    runs together share rows of A and columns of B in its L2;
-//  * C is written with nontemporal stores: the output stream does not displace the A
-//    and B lines the other tiles re-read from L2 and the Infinity Cache (8192^3 bf16:
-//    ~4 % faster than plain stores);
+//  * C is written with nontemporal stores (8192^3 bf16: ~4 % faster than plain stores;
+//    the HBM fetch of A and B is unchanged, so the gain is on the write side);
 //  * ragged extents (the RAGGED instances; Lava's TENSOR_CLAMP_CONSTANT layout with
 //    the default zero, src/vocabulary/tensor.jl:44-51): a lane whose row or chunk lies
 //    past M, N or K gets a lane offset beyond the buffer resource's range, so its

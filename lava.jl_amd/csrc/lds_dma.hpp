@@ -42,9 +42,8 @@ __device__ __forceinline__ void dma16(const v4i& rsrc, uint32_t voffset, uint32_
                  : "memory");
 }
 
-// dma16 for data read once: the nontemporal hint lets L2 and the Infinity Cache evict the
-// lines early instead of displacing data that is read again (W8A16's weight stream: ~7 %
-// faster at the decode shape).
+// dma16 with the nontemporal hint, for data read once (W8A16's weight stream: ~7 % faster at
+// the decode shape, with the same HBM fetch as without the hint).
 __device__ __forceinline__ void dma16_stream(const v4i& rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
     asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
                  :
