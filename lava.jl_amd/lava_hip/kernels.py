@@ -105,14 +105,25 @@ def coopmat_gemm_tiles(C_: HIPDeviceArray, A: HIPDeviceArray, B: HIPDeviceArray,
     return C_
 
 
-def w8a16(Y: HIPDeviceArray, X: HIPDeviceArray, W: HIPDeviceArray, scale: HIPDeviceArray,
-          stream: Optional[int] = None) -> HIPDeviceArray:
-    """Y = (X * float(W)) .* scale[col]: the per-element dequant epilogue
-    (src/device/coopmat_intrinsics.jl:535-628)."""
+def _check_w8a16(Y: HIPDeviceArray, X: HIPDeviceArray, W: HIPDeviceArray, scale: HIPDeviceArray) -> None:
+    if (X.dtype, W.dtype, scale.dtype, Y.dtype) != ("f16", "i8", "f16", "f32"):
+        raise ValueError(f"W8A16 is f16 X, i8 W, f16 scale -> f32 Y (got {X.dtype}, {W.dtype}, {scale.dtype}, "
+                         f"{Y.dtype})")
+    if len(X.dims) != 2 or len(W.dims) != 2 or len(Y.dims) != 2:
+        raise ValueError("X, W and Y must be 2-D")
     M, K = X.dims
     K2, N = W.dims
     if K2 != K or Y.dims != (M, N) or scale.size != N:
         raise ValueError(f"shape mismatch: X {X.dims}, W {W.dims}, scale {scale.dims}, Y {Y.dims}")
+
+
+def w8a16(Y: HIPDeviceArray, X: HIPDeviceArray, W: HIPDeviceArray, scale: HIPDeviceArray,
+          stream: Optional[int] = None) -> HIPDeviceArray:
+    """Y = (X * float(W)) .* scale[col]: the per-element dequant epilogue
+    (src/device/coopmat_intrinsics.jl:535-628)."""
+    _check_w8a16(Y, X, W, scale)
+    M, K = X.dims
+    N = W.dims[1]
     layout = (1 if X.order == "C" else 0) | (2 if W.order == "C" else 0) | (4 if Y.order == "C" else 0)
     _lib.call("lava_hip_gemm_w8a16", X.ptr, W.ptr, scale.ptr, Y.ptr, M, N, K, _ld(X), _ld(W), _ld(Y), layout,
               stream)
@@ -123,10 +134,9 @@ def w8a16_noalloc(Y: HIPDeviceArray, X: HIPDeviceArray, W: HIPDeviceArray, scale
                   stream: Optional[int] = None) -> HIPDeviceArray:
     """`w8a16` through the entry point that allocates nothing: the split-K partials live in a
     fixed per-GPU device array (shared by every call on that GPU: overlapping calls race)."""
+    _check_w8a16(Y, X, W, scale)
     M, K = X.dims
-    K2, N = W.dims
-    if K2 != K or Y.dims != (M, N) or scale.size != N:
-        raise ValueError(f"shape mismatch: X {X.dims}, W {W.dims}, scale {scale.dims}, Y {Y.dims}")
+    N = W.dims[1]
     layout = (1 if X.order == "C" else 0) | (2 if W.order == "C" else 0) | (4 if Y.order == "C" else 0)
     _lib.call("lava_hip_gemm_w8a16_noalloc", X.ptr, W.ptr, scale.ptr, Y.ptr, M, N, K, _ld(X), _ld(W), _ld(Y), layout,
               stream)
