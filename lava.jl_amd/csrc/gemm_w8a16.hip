@@ -248,15 +248,18 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
 //    1152 + w (v_perm_b32 against a register of 0x64 bytes), then subtract 1152;
 //  * K's tail: 16-byte chunks at or past K take the out-of-range offset and read zero (in W and
 //    in X); rows of X at or past M likewise.  The scale is the per-element callback.
-constexpr int KM_TILES = 2;
-constexpr int KM_COLS = 16 * KM_TILES;
-constexpr int KM_KSPLIT = 2;
+constexpr int KM_TILES = 2;                       // 16-column MFMA tiles per wavefront
+constexpr int KM_CG = 1;                          // column groups (wavefronts side by side in N)
+constexpr int KM_KSPLIT = 2;                      // wavefronts side by side in K
+constexpr int KM_WAVES = KM_CG * KM_KSPLIT;
+constexpr int KM_WCOLS = 16 * KM_TILES;           // columns per wavefront
+constexpr int KM_COLS = KM_WCOLS * KM_CG;         // columns per workgroup
 constexpr int KM_BUFS = 4;                        // stage ring per wavefront
-static_assert(KM_BUFS >= 1 && KM_BUFS <= 4, "the vmcnt waits cover up to 3 later stages");
+static_assert(KM_BUFS >= 1 && KM_BUFS <= 6, "the vmcnt waits cover up to 5 later stages");
 constexpr int KM_SEG = 128;                       // k per stage
-constexpr int KM_W_INSTR = KM_COLS / 8;           // W DMA instructions per stage (8 columns each)
+constexpr int KM_W_INSTR = KM_WCOLS / 8;          // W DMA instructions per stage (8 columns each)
 constexpr int KM_X_INSTR = 16 / 4;                // X DMA instructions per stage (4 rows each)
-constexpr int KM_STAGE_BYTES = KM_COLS * KM_SEG + 16 * KM_SEG * 2;
+constexpr int KM_STAGE_BYTES = KM_WCOLS * KM_SEG + 16 * KM_SEG * 2;
 
 // 8 int8 weights (two dwords, k ascending) -> the 8 fp16 values of a B operand
 __device__ __forceinline__ f16x8 km_dequant(uint32_t lo, uint32_t hi) {
@@ -282,17 +285,19 @@ typedef short km_s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) km_s16x4 km_lds_s16x4;
 
 template <bool XROW, bool YROW>
-__global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16* __restrict__ X,
+__global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* __restrict__ X,
                                                                       const int8_t* __restrict__ W,
                                                                       const f16* __restrict__ scale,
                                                                       float* __restrict__ Y, int M, int N, int K,
                                                                       int64_t ldx, int64_t ldw, int64_t ldy) {
     // per wavefront: a ring of stage buffers, each W [32 columns][128 bytes] then X (4 KB)
-    __shared__ __attribute__((aligned(16))) uint8_t stage_buf[KM_KSPLIT][KM_BUFS][KM_STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) f32x4 red[KM_KSPLIT][KM_TILES][64];
-    const int lane = threadIdx.x & 63, ks = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    __shared__ __attribute__((aligned(16))) uint8_t stage_buf[KM_WAVES][KM_BUFS][KM_STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) f32x4 red[KM_KSPLIT][KM_CG * KM_TILES][64];
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cg = w % KM_CG, ks = w / KM_CG;         // column group, K range
     const int q = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * KM_COLS;              // the host keeps N a multiple of KM_COLS
+    // the host keeps N a multiple of KM_COLS; this wavefront's columns start at n0
+    const int n0 = blockIdx.x * KM_COLS + cg * KM_WCOLS;
     const int m0 = blockIdx.y * 16;
     const int stages = (K + KM_SEG - 1) / KM_SEG;
     const int per = (stages + KM_KSPLIT - 1) / KM_KSPLIT;
@@ -300,7 +305,7 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
     const int nst = s_end - s_begin;
 
     // buffer resources over this workgroup's 32 columns of W and 16 rows of X
-    const v4i w_rs = make_rsrc(W + (int64_t)n0 * ldw, (uint32_t)(KM_COLS * ldw));
+    const v4i w_rs = make_rsrc(W + (int64_t)n0 * ldw, (uint32_t)(KM_WCOLS * ldw));
     // (X column-major: the host keeps M a multiple of 8, so a 16-byte chunk of 8 rows is wholly
     // inside or wholly past M)
     const v4i x_rs = XROW ? make_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(16 * ldx * 2))
@@ -314,7 +319,7 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
     const int rows_ok = min(16, M - m0);
     auto issue = [&](int st, int buf) {
         const int k0 = st * KM_SEG;                   // first k of the stage
-        const uint32_t lds0 = lds_addr(&stage_buf[ks][buf][0]);
+        const uint32_t lds0 = lds_addr(&stage_buf[w][buf][0]);
 #pragma unroll
         for (int i = 0; i < KM_W_INSTR; ++i) {
             const int col = 8 * i + wc_lo;
@@ -334,7 +339,7 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
                 const int row = 8 * (lane & 1);
                 off = (kx < K && row < rows_ok) ? (uint32_t)((kx * ldx + row) * 2) : OOB_OFS;
             }
-            dma16(x_rs, off, 0, lds0 + KM_COLS * KM_SEG + 1024 * j);
+            dma16(x_rs, off, 0, lds0 + KM_WCOLS * KM_SEG + 1024 * j);
         }
     };
 
@@ -348,7 +353,11 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
     for (int s = 0; s < nst; ++s) {
         // this stage's DMA done; the later stages issued (up to KM_BUFS - 1) may be in flight
         const int later = min(KM_BUFS - 1, nst - 1 - s);
-        if (later >= 3)
+        if (later >= 5)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(5 * PER_STAGE) : "memory");
+        else if (later == 4)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * PER_STAGE) : "memory");
+        else if (later == 3)
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PER_STAGE) : "memory");
         else if (later == 2)
             asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PER_STAGE) : "memory");
@@ -357,8 +366,8 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
         else
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         const int buf = s % KM_BUFS;
-        const uint8_t* wb = &stage_buf[ks][buf][0];
-        const uint8_t* xb = wb + KM_COLS * KM_SEG;
+        const uint8_t* wb = &stage_buf[w][buf][0];
+        const uint8_t* xb = wb + KM_WCOLS * KM_SEG;
         // the stage's fragments into registers; X row q, k 64 h + 16 g .. + 15 is fp16 chunks
         // 8 h + 2 g and + 1, W column 16 t + q at k 64 h + 16 g is chunk 4 h + g
         f16x8 xf[2][2];
@@ -404,16 +413,16 @@ __global__ void __launch_bounds__(64 * KM_KSPLIT) w8a16_kmajor_kernel(const f16*
     }
     // the K quarters added in order through LDS; the first wavefront finishes
 #pragma unroll
-    for (int t = 0; t < KM_TILES; ++t) red[ks][t][lane] = acc[t];
+    for (int t = 0; t < KM_TILES; ++t) red[ks][cg * KM_TILES + t][lane] = acc[t];
     __syncthreads();
     if (ks != 0) return;
     // acc[t] lane holds column n0 + 16 t + q and rows m0 + 4 g + j: the dequant scale by the
     // per-element callback with the scale pointer in `extras`
 #pragma unroll
     for (int t = 0; t < KM_TILES; ++t) {
-        f32x4 sum = red[0][t][lane];
+        f32x4 sum = red[0][cg * KM_TILES + t][lane];
 #pragma unroll
-        for (int r = 1; r < KM_KSPLIT; ++r) sum += red[r][t][lane];
+        for (int r = 1; r < KM_KSPLIT; ++r) sum += red[r][cg * KM_TILES + t][lane];
         Frag<float, 16, 16, Accumulator> f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) f.v[j] = sum[j];
@@ -482,7 +491,7 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
     const bool x_ok = xrow ? (kldx % 8 == 0 && kldx >= K && kldx <= (int64_t(1) << 26))
                            : (M % 8 == 0 && ldx % 8 == 0 && ldx >= M && K * ldx <= (int64_t(1) << 30));
     if ((layout & 2u) == 0 && x_ok && N % KM_COLS == 0 && K > 0 && K % 16 == 0 && ldw % 16 == 0 && ldw >= K &&
-        ldw <= (int64_t(1) << 31) / KM_COLS && aligned(W, 16) && aligned(X, 16) && N <= 0x7fffffff &&
+        ldw <= (int64_t(1) << 31) / KM_WCOLS && aligned(W, 16) && aligned(X, 16) && N <= 0x7fffffff &&
         M <= 0x7fffffff && (M + 15) / 16 <= 65535) {
         p.path = W8_KMAJOR;
         p.mblocks = (M + 15) / 16;
@@ -555,7 +564,7 @@ static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const voi
     }
     if (p.path == W8_KMAJOR) {
         auto go = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_KSPLIT), 0, s,
+            hipLaunchKernelGGL(kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_WAVES), 0, s,
                                (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, (int)M, (int)N, (int)K,
                                p.kldx, ldw, ldy);
         };
