@@ -1,6 +1,7 @@
 """The W8A16 entry point that allocates nothing, through the C ABI: the same results as
 lava_hip_gemm_w8a16 (bit for bit: the same kernels and summation order) on two calls in a
-row, the second smaller, and on a shape that needs no split-K scratch at all."""
+row, the second smaller, and on shapes that need no split-K scratch at all (column-major
+weights run one kernel over whole columns)."""
 from __future__ import annotations
 
 import numpy as np
@@ -53,3 +54,28 @@ def test_noalloc_without_split_and_argument_errors(gpu, oracle):
         np.testing.assert_array_equal(got, ref_entry)
     with pytest.raises(lh.InvalidArgument):
         lh._lib.call("lava_hip_gemm_w8a16_noalloc", 16, 16, 16, 16, 16, 128, 256, 256, 100, 128, 7, None)
+
+
+@pytest.mark.parametrize("xo,yo", [("C", "C"), ("F", "F")])
+def test_noalloc_column_major_weights(gpu, oracle, xo, yo):
+    """W column-major (K contiguous per column): the whole-column kernel, no scratch; the
+    no-allocation entry gives the same bits as the allocating one."""
+    lh = gpu
+    M, N, K = 16, 4096, 4096
+    announce(f"w8a16_noalloc: W column-major, X {xo}, Y {yo}")
+    X = lh.HIPDeviceArray("f16", (M, K), order=xo)
+    W = lh.HIPDeviceArray("i8", (K, N), order="F")
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(X, lh_mod.seed(44, 0))
+    lh.fill_i8(W, lh_mod.seed(44, 1), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(44, 2), 0.001, 0.02)
+    Y_ref = lh.HIPDeviceArray("f32", (M, N), order=yo)
+    Y_na = lh.HIPDeviceArray("f32", (M, N), order=yo)
+    Y_na.fill_bytes(0xFF)
+    lh.w8a16(Y_ref, X, W, s)
+    lh.w8a16_noalloc(Y_na, X, W, s)
+    lh.synchronize()
+    np.testing.assert_array_equal(Y_na.to_numpy(), Y_ref.to_numpy())
+    ref = oracle.w8a16_rows(np.ascontiguousarray(X.to_numpy()), np.ascontiguousarray(W.to_numpy()), s.to_numpy(),
+                            N, K, K, N, np.arange(M))
+    assert oracle.rel_frobenius(Y_na.to_numpy(), ref) <= 1e-3
