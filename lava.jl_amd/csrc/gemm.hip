@@ -3,11 +3,10 @@
 // A column-major C is handled as its row-major transpose, C^T = B^T A^T, which
 // swaps the operands and flips their layouts; so every kernel writes row-major C.
 // Compute-bound shapes take the 256 x 256 tile kernel (gemm_tn_kernel.hpp) in any
-// operand layout for 16-bit types (K-contiguous operands read directly, M/N-contiguous
-// ones through transposing LDS reads) and with both operands K-contiguous for int8 --
-// whole tiles, or ragged extents with zero-clamped loads.  Products of at most 16 such
-// tiles take the 64 x 64 small-product kernel; the rest (extents that split a 16-byte
-// chunk, other int8 layouts) the staged kernel.
+// operand layout (K-contiguous operands read directly, M/N-contiguous ones through
+// transposing LDS reads, 16- or 8-bit) -- whole tiles, or ragged extents with
+// zero-clamped loads.  Products of at most 16 such tiles take the 64 x 64 small-product
+// kernel; the rest (extents that split a 16-byte chunk) the staged kernel.
 #include <hip/hip_runtime.h>
 
 #include "gemm_kernels.hpp"

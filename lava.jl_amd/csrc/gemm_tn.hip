@@ -1,6 +1,6 @@
 // gemm_tn.hip -- the compute-bound GEMM: eligibility, the layout dispatcher and the
-// instances with both operands K-contiguous (A row-major, B column-major: the bf16
-// configuration, and every int8 product).  The kernel (gemm_tn16_kernel) is
+// instances with both operands K-contiguous (A row-major, B column-major: the bf16 and
+// int8 configurations).  The kernel (gemm_tn16_kernel) is
 // gemm_tn_kernel.hpp; the other operand forms are instantiated in gemm_tn_{nk,kn,nn}.hip.
 #include "gemm_tn_kernel.hpp"
 
@@ -9,6 +9,9 @@ namespace lava {
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_EXTERN, false, true)
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_EXTERN, true, false)
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_EXTERN, false, false)
+LAVA_TN_LAYOUT_EXTERN(int8_t, int32_t, false, false, true)
+LAVA_TN_LAYOUT_EXTERN(int8_t, int32_t, false, true, false)
+LAVA_TN_LAYOUT_EXTERN(int8_t, int32_t, false, false, false)
 
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_INST, true, true)
 LAVA_TN_LAYOUT_INST(int8_t, int32_t, false, true, true)
@@ -17,14 +20,11 @@ template <typename T, typename OutT, bool EPI>
 int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                    int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged, bool ak, bool bk) {
     if (ak && bk) return launch_gemm_tn_layout<T, OutT, EPI, true, true>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
-    if constexpr (sizeof(T) == 2) {
-        if (!ak && bk)
-            return launch_gemm_tn_layout<T, OutT, EPI, false, true>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
-        if (ak && !bk)
-            return launch_gemm_tn_layout<T, OutT, EPI, true, false>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
-        return launch_gemm_tn_layout<T, OutT, EPI, false, false>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
-    }
-    LAVA_REQUIRE(false, LAVA_HIP_ERR_UNSUPPORTED, "gemm_tn: 8-bit operands must both be K-contiguous");
+    if (!ak && bk)
+        return launch_gemm_tn_layout<T, OutT, EPI, false, true>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
+    if (ak && !bk)
+        return launch_gemm_tn_layout<T, OutT, EPI, true, false>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
+    return launch_gemm_tn_layout<T, OutT, EPI, false, false>(A, B, C, M, N, K, lda, ldb, ldc, s, epi, ragged);
 }
 
 template int tn_gemm_eligible<f16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t,

@@ -54,6 +54,7 @@ constexpr int TN_KB = 128;      // bytes of K per stage
 constexpr int TN_SLICE = TN_TILE * TN_KB;  // 32 KB
 
 typedef short tn_s16x4 __attribute__((ext_vector_type(4)));
+typedef int tn_v2i __attribute__((ext_vector_type(2)));
 typedef short tn_s16x8 __attribute__((ext_vector_type(8)));
 
 // The M/N-contiguous swizzle F(r % 4) = {0, 6, 10, 12}, as nibbles.
@@ -170,8 +171,70 @@ struct TnSide<T, false> {
     }
 };
 
+// M/N-contiguous int8: the slice is 128 rows of K x 256 bytes (256 m or n).  Row r's logical
+// 16-byte chunk c is stored at slot c ^ F8(r), F8(r) = (r % 8) | 8 (r / 16 % 2).  A fragment is
+// two transposing reads (ds_read_b64_tr_b8: in a 16-lane group, output lane i byte j is the
+// byte at source lane 2 j + i / 8's address + i % 8; measured on the box).  Source lane s of
+// 16-lane group g points at k row 64 u + 16 g + 8 h + s / 2 of k-step u (h = 0, 1 for the two
+// reads), byte 8 (s % 2) of the block's chunk, so output lane i receives the k-values
+// 64 u + 16 g + 8 h + [0, 8) of column 16 t + i: together the 16 k-slots a K-contiguous
+// fragment gives lane group g (bytes 16 g .. 16 g + 15 of the k-step), so the two forms mix.
+// F8 puts the 8 rows one group reads, and the two groups of a 32-lane half, on distinct banks.
+template <>
+struct TnSide<int8_t, false> {
+    v4i rs;
+    uint32_t off[4];   // per instruction variant (i % 2, i / 4): the row's swizzle depends on them
+    uint32_t step;     // soffset per instruction: 4 rows of K
+    uint32_t ld;       // bytes per row of K
+    int klim;          // instruction i's row is inside iff k0 + 4 i < klim
+    bool cin[4];       // the lane's chunk lies inside M (N), per variant
+    int rd;            // fragment reads: the lane's k row and byte offset
+    int c16[8];        // fragment reads: the stored chunk of column block t, times 16
+
+    // mn_total: M (N); K: the depth in elements; w: the wavefront; wx: its 128-column half.
+    __device__ __forceinline__ void init(const int8_t* X, int64_t ld_b, int tile, int, int64_t mn_total, int K, int w,
+                                         int wx, int lane) {
+        const int64_t col0 = (int64_t)tile * TN_TILE;
+        rs = make_rsrc(reinterpret_cast<const char*>(X) + col0, (uint32_t)((int64_t)K * ld_b - col0));
+        // DMA: instruction i covers rows 32 w + 4 i + lane / 16, slot lane % 16; that row's
+        // r % 8 is 4 (i % 2) + lane / 16 and r / 16 % 2 is i / 4
+        const int rr = lane >> 4, p = lane & 15;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int c = p ^ ((4 * (v & 1) + rr) | ((v >> 1) << 3));
+            off[v] = (uint32_t)((32 * w + rr) * ld_b + 16 * c);
+            cin[v] = col0 + 16 * c < mn_total;
+        }
+        step = (uint32_t)(4 * ld_b);
+        ld = (uint32_t)ld_b;
+        klim = K - 32 * w - rr;
+        // fragments: every row a lane reads has F8 = (s / 2) | 8 (g % 2)
+        const int s = lane & 15, g = lane >> 4;
+        const int f = (s >> 1) | ((g & 1) << 3);
+        rd = (16 * g + (s >> 1)) * 256 + 8 * (s & 1);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) c16[t] = ((8 * wx + t) ^ f) * 16;
+    }
+    __device__ __forceinline__ static int variant(int i) { return (i & 1) | ((i >> 2) << 1); }
+    __device__ __forceinline__ bool valid(int i, uint32_t kofs, int) const {
+        return (int)kofs + 4 * i < klim && cin[variant(i)];
+    }
+    __device__ __forceinline__ uint32_t voff(int i) const { return off[variant(i)]; }
+    __device__ __forceinline__ uint32_t soff(int i, uint32_t kofs) const { return kofs * ld + i * step; }
+    // fragment t (columns 16 t of the half) of k-step u (64 rows of K): two transposing reads,
+    // k rows 16 g + [0, 8) and 16 g + [8, 16) of the k-step
+    __device__ __forceinline__ uint4 read16(const uint8_t* slice, int u, int t) const {
+        const uint8_t* b = slice + u * 64 * 256 + rd + c16[t];
+        const tn_v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) tn_v2i*)(const __attribute__((address_space(3))) uint8_t*)b);
+        const tn_v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) tn_v2i*)(const __attribute__((address_space(3))) uint8_t*)(b + 8 * 256));
+        return make_uint4((uint32_t)lo.x, (uint32_t)lo.y, (uint32_t)hi.x, (uint32_t)hi.y);
+    }
+};
+
 // The tile kernel.  AK / BK: A / B K-contiguous (row-major A, column-major B) or
-// M/N-contiguous; int8 needs both K-contiguous.  16x16 MFMAs (16x16x32 for 16-bit
+// M/N-contiguous (transposing LDS reads, 16- or 8-bit).  16x16 MFMAs (16x16x32 for 16-bit
 // types, 16x16x64 for int8), 8 x 8 accumulators of 16 x 16 per wavefront: at the chip's
 // power limit the 16x16 shape sustains ~11 % more than 32x32 (it moves ~20 % fewer
 // register-file bytes per flop), and its fragments (16 rows x 64 bytes of K per k-step)
@@ -422,7 +485,6 @@ int tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int
                      int64_t ldb, int64_t ldc, size_t c_elem, bool ak, bool bk) {
     const int64_t sz = (int64_t)sizeof(T), ke = TN_KB / sz, chunk = 16 / sz;
     if (M <= 0 || N <= 0 || K <= 0) return TN_NO;
-    if ((!ak || !bk) && sz != 2) return TN_NO;            // transposing reads are 16-bit
     if ((ak || bk) && K % chunk) return TN_NO;           // a K-contiguous chunk wholly in or out
     if ((!ak && M % chunk) || (!bk && N % chunk)) return TN_NO;
     const int64_t tiles_m = (M + TN_TILE - 1) / TN_TILE, tiles_n = (N + TN_TILE - 1) / TN_TILE;

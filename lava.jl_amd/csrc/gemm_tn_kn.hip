@@ -4,5 +4,6 @@
 namespace lava {
 
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_INST, true, false)
+LAVA_TN_LAYOUT_INST(int8_t, int32_t, false, true, false)
 
 }  // namespace lava

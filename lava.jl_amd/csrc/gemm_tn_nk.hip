@@ -4,5 +4,6 @@
 namespace lava {
 
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_INST, false, true)
+LAVA_TN_LAYOUT_INST(int8_t, int32_t, false, false, true)
 
 }  // namespace lava

@@ -157,6 +157,41 @@ def test_gemm_tn_full_size(gpu, oracle, dt, n):
         assert abs(lhs - rhs) <= 1e-3 * (abs(rhs) + n * np.sqrt(n))
 
 
+@pytest.mark.parametrize("layout", range(8))
+@pytest.mark.parametrize("shape", [(2048, 1536, 1024), (1280, 1024, 640), (1296, 1040, 528)])
+def test_gemm_i8_tile_kernel_layouts(gpu, oracle, layout, shape):
+    """int8 on the tile kernel in every operand layout: M/N-contiguous operands staged as
+    [k][m] and read through ds_read_b64_tr_b8 (whole tiles; ragged M and N; ragged K).
+    Bit-exact on sampled rows."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm i8 tile kernel layout={layout} M={M} N={N} K={K}")
+    A, B = make_inputs(gpu, "i8", M, N, K, layout, 500 + layout, 600 + layout)
+    C = lh.HIPDeviceArray("i32", (M, N), order="C" if layout & 4 else "F")
+    C.fill_bytes(0xFF)
+    lh.gemm(C, A, B)
+    rows = np.unique(np.concatenate([np.arange(0, M, 37), [1, 15, 16, 255, 256, M - 1]]))
+    check_rows(oracle, "i8", A, B, C, rows, layout)
+
+
+@pytest.mark.parametrize("layout", [0, 4])
+def test_gemm_i8_full_size_column_major(gpu, oracle, layout):
+    """int8 4096^3 with A column-major (Julia's layout), B column-major: every element of C
+    through the exact checksum, sampled rows against the oracle."""
+    lh = gpu
+    n = 4096
+    announce(f"gemm i8 {n}^3 layout={layout}")
+    A, B = make_inputs(gpu, "i8", n, n, n, layout, lh_mod.seed(2, 0), lh_mod.seed(2, 1))
+    C = lh.HIPDeviceArray("i32", (n, n), order="C" if layout & 4 else "F")
+    lh.gemm(C, A, B)
+    lh.synchronize()
+    rng = np.random.default_rng(n + layout)
+    rows = np.unique(np.concatenate([[0, 1, 255, 256, n - 1], rng.integers(0, n, 11)]))
+    check_rows(oracle, "i8", A, B, C, rows, layout)
+    lhs, rhs = full_checksum(C, A, B, "i8")
+    assert lhs == rhs
+
+
 def test_gemm_tn_column_major_c_swaps_operands(gpu, oracle):
     """Column-major C with A column-major and B row-major is the TN kernel on the
     transposed problem."""
