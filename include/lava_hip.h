@@ -379,16 +379,17 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
  * layout: bit0 X row-major, bit1 W row-major, bit2 Y row-major.  Two weight-streaming
  * kernels, every call one launch:
  *  - W column-major (K contiguous per output column), X and Y either way: N a multiple of
- *    32, K of 16, 16-byte aligned X and W with leading dimensions multiples of 8 (X) and 16
- *    (W); a column-major X needs M a multiple of 8 (or M == 1 with ldx == 1).  Whole
- *    columns per workgroup, no workspace.
+ *    32, K of 16, 16-byte aligned W with a leading dimension a multiple of 16.  Whole columns
+ *    per workgroup.  X is read in place when row-major (16-byte aligned, ldx a multiple of 8),
+ *    or column-major with M a multiple of 8 (or M == 1 with ldx == 1); any other column-major X
+ *    is first copied row-major into the workspace (M x K fp16).
  *  - W row-major, X and Y either way: K a multiple of 32, N of 128 (a row-major X 16-byte
- *    aligned with ldx a multiple of 8).  Narrower N
- *    splits K across workgroups through a split-K workspace the library owns, one per
- *    (device, stream), whose last-arriving workgroup per column block adds the partial
- *    blocks: a call that grows it allocates (hipMalloc) and so is not capturable -- make one
- *    call of the largest shape outside capture first.  Calls on one stream from several
- *    threads are serialised around the workspace; lava_hip_stream_destroy frees it.
+ *    aligned with ldx a multiple of 8).  Narrower N splits K across workgroups, whose
+ *    last-arriving workgroup per column block adds the partial blocks from the workspace.
+ * The workspace (split-K partials, or the copy of X) is owned by the library, one per
+ * (device, stream): a call that grows it allocates (hipMalloc) and so is not capturable --
+ * make one call of the largest shape outside capture first.  Calls on one stream from
+ * several threads are serialised around the workspace; lava_hip_stream_destroy frees it.
  * Any other layout or shape runs on a generic kernel.  Results are deterministic (fixed
  * summation order). */
 int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N, int64_t K,

@@ -436,6 +436,16 @@ __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* 
     }
 }
 
+// A column-major X (element (m, k) at k ldx + m) copied row-major with leading dimension K,
+// for the column-major-W kernel when it cannot stage X in place (M not a multiple of 8).
+__global__ void w8a16_x_rows_kernel(const f16* __restrict__ X, f16* __restrict__ Xr, int64_t M, int64_t K,
+                                    int64_t ldx) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= M * K) return;
+    const int64_t m = e % M, k = e / M;   // consecutive threads read consecutive m of one k
+    Xr[m * K + k] = X[k * ldx + m];
+}
+
 // Any layout, any shape: one thread per output element, fp32 sums.
 __global__ void w8a16_generic_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
                                      const f16* __restrict__ scale, float* __restrict__ Y, int64_t M, int64_t N,
@@ -467,6 +477,9 @@ struct W8Plan {
     // X and Y orientation; W8_KMAJOR: X's leading dimension as the kernel reads it
     bool xrow = true, yrow = true;
     int64_t kldx = 0;
+    // W8_KMAJOR with a column-major X the kernel cannot stage (M not a multiple of 8): X is first
+    // copied row-major into the workspace, after the counter region
+    bool x_copy = false;
     int splits = 1;
     int ksteps = 0;              // the per-wavefront step count of an unrolled instance, or 0
     // split-K workspace (W8_SPLIT with splits > 1): the arrival counters (one per column and
@@ -475,8 +488,9 @@ struct W8Plan {
     size_t scratch_bytes = 0;
 };
 
+// max_scratch: the most workspace the caller can provide (the no-allocation entry's fixed array).
 static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
-                         uint32_t layout) {
+                         uint32_t layout, size_t max_scratch) {
     W8Plan p;
     // W column-major, X and Y either way (the kernel's 32-bit buffer offsets span 32 columns of
     // W and 16 rows of X).  A column-major X of one row with unit stride is the same bytes as a
@@ -488,17 +502,26 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
         xrow = true;
         kldx = K;
     }
-    const bool x_ok = xrow ? (kldx % 8 == 0 && kldx >= K && kldx <= (int64_t(1) << 26))
-                           : (M % 8 == 0 && ldx % 8 == 0 && ldx >= M && K * ldx <= (int64_t(1) << 30));
-    if ((layout & 2u) == 0 && x_ok && N % KM_COLS == 0 && K > 0 && K % 16 == 0 && ldw % 16 == 0 && ldw >= K &&
-        ldw <= (int64_t(1) << 31) / KM_WCOLS && aligned(W, 16) && aligned(X, 16) && N <= 0x7fffffff &&
-        M <= 0x7fffffff && (M + 15) / 16 <= 65535) {
+    bool x_ok = xrow ? (kldx % 8 == 0 && kldx >= K && kldx <= (int64_t(1) << 26) && aligned(X, 16))
+                     : (M % 8 == 0 && ldx % 8 == 0 && ldx >= M && K * ldx <= (int64_t(1) << 30) && aligned(X, 16));
+    // otherwise a column-major X is copied row-major (leading dimension K) into the workspace
+    const size_t copy_bytes = (size_t)((M * K * 2 + 255) / 256 * 256);
+    const bool x_copy = !x_ok && !xrow && K <= (int64_t(1) << 26) && M * K <= (int64_t(1) << 36) &&
+                        W8_COUNTER_BYTES + copy_bytes <= max_scratch;
+    if ((layout & 2u) == 0 && (x_ok || x_copy) && N % KM_COLS == 0 && K > 0 && K % 16 == 0 && ldw % 16 == 0 &&
+        ldw >= K && ldw <= (int64_t(1) << 31) / KM_WCOLS && aligned(W, 16) && N <= 0x7fffffff && M <= 0x7fffffff &&
+        (M + 15) / 16 <= 65535) {
         p.path = W8_KMAJOR;
         p.mblocks = (M + 15) / 16;
         p.cblocks = N / KM_COLS;
-        p.xrow = xrow;
+        p.xrow = x_ok ? xrow : true;
         p.yrow = layout & 4u;
-        p.kldx = kldx;
+        p.kldx = x_ok ? kldx : K;
+        if (!x_ok) {
+            p.x_copy = true;
+            p.counter_bytes = W8_COUNTER_BYTES;
+            p.scratch_bytes = W8_COUNTER_BYTES + copy_bytes;
+        }
         return p;
     }
     // W row-major, X and Y either way (a row-major X in 16-byte loads)
@@ -563,10 +586,19 @@ static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const voi
         return LAVA_HIP_OK;
     }
     if (p.path == W8_KMAJOR) {
+        const f16* xk = (const f16*)X;
+        if (p.x_copy) {
+            f16* xr = reinterpret_cast<f16*>(static_cast<char*>(ws) + p.counter_bytes);
+            const int64_t total = M * K;
+            hipLaunchKernelGGL(w8a16_x_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                               (const f16*)X, xr, M, K, ldx);
+            LAVA_LAUNCH_CHECK("w8a16_x_rows_kernel");
+            xk = xr;
+        }
         auto go = [&](auto kernel) {
-            hipLaunchKernelGGL(kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_WAVES), 0, s,
-                               (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, (int)M, (int)N, (int)K,
-                               p.kldx, ldw, ldy);
+            hipLaunchKernelGGL(kernel, dim3((unsigned)p.cblocks, (unsigned)p.mblocks), dim3(64 * KM_WAVES), 0, s, xk,
+                               (const int8_t*)W, (const f16*)scale, (float*)Y, (int)M, (int)N, (int)K, p.kldx, ldw,
+                               ldy);
         };
         if (p.xrow)
             p.yrow ? go(w8a16_kmajor_kernel<true, true>) : go(w8a16_kmajor_kernel<true, false>);
@@ -678,7 +710,7 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
     if (rc != LAVA_HIP_OK || M == 0 || N == 0) return rc;
     rc = lava_hip_init();
     if (rc != LAVA_HIP_OK) return rc;
-    const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout);
+    const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout, SIZE_MAX);
     hipStream_t s = as_stream(stream);
     if (p.scratch_bytes == 0) return launch_w8a16(p, X, W, scale, Y, nullptr, M, N, K, ldx, ldw, ldy, layout, s);
     int dev = 0;
@@ -706,7 +738,7 @@ extern "C" int lava_hip_gemm_w8a16_noalloc(const void* X, const void* W, const v
                                            uint32_t layout, void* stream) {
     int rc = check_w8a16_args(X, W, scale, Y, M, N, K, ldx, ldw, ldy, layout, "gemm_w8a16_noalloc");
     if (rc != LAVA_HIP_OK || M == 0 || N == 0) return rc;
-    const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout);
+    const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout, LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES);
     LAVA_ARG(p.scratch_bytes <= LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES,
              "gemm_w8a16_noalloc: this shape needs %zu bytes of split-K scratch; the no-allocation entry holds at most "
              "%zu (M = %lld, N = %lld, K = %lld)", p.scratch_bytes, (size_t)LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES,

@@ -149,8 +149,10 @@ def test_w8a16_weights_column_major(gpu, oracle, M, N, K):
     (16, 14336, 4096, "F", "F"), (16, 4096, 4096, "F", "C"), (16, 4096, 4096, "C", "F"),
     # two row blocks, the second of 8 rows; a partial last stage
     (24, 96, 400, "F", "C"), (8, 4096, 1040, "F", "F"), (40, 256, 1024, "F", "F"),
-    # one row with unit stride (read as row-major); M not a multiple of 8 (the generic kernel)
-    (1, 4096, 4096, "F", "F"), (5, 256, 128, "F", "F"),
+    # one row with unit stride (read as row-major); M not a multiple of 8 (X copied row-major into
+    # the workspace first)
+    (1, 4096, 4096, "F", "F"), (5, 256, 128, "F", "F"), (3, 4096, 4096, "F", "C"), (7, 14336, 4096, "F", "F"),
+    (12, 1024, 1040, "F", "F"), (21, 512, 256, "F", "C"),
     # four row blocks; a long K (down projection)
     (64, 2048, 4096, "F", "C"), (16, 4096, 14336, "C", "C")])
 def test_w8a16_weights_column_major_orders(gpu, oracle, M, N, K, xo, yo):

@@ -56,13 +56,14 @@ def test_noalloc_without_split_and_argument_errors(gpu, oracle):
         lh._lib.call("lava_hip_gemm_w8a16_noalloc", 16, 16, 16, 16, 16, 128, 256, 256, 100, 128, 7, None)
 
 
-@pytest.mark.parametrize("xo,yo", [("C", "C"), ("F", "F")])
-def test_noalloc_column_major_weights(gpu, oracle, xo, yo):
-    """W column-major (K contiguous per column): the whole-column kernel, no scratch; the
+@pytest.mark.parametrize("M,xo,yo", [(16, "C", "C"), (16, "F", "F"), (5, "F", "C")])
+def test_noalloc_column_major_weights(gpu, oracle, M, xo, yo):
+    """W column-major (K contiguous per column): the whole-column kernel (no scratch, or the
+    scratch holding a row-major copy of a column-major X whose M is not a multiple of 8); the
     no-allocation entry gives the same bits as the allocating one."""
     lh = gpu
-    M, N, K = 16, 4096, 4096
-    announce(f"w8a16_noalloc: W column-major, X {xo}, Y {yo}")
+    N, K = 4096, 4096
+    announce(f"w8a16_noalloc: W column-major, M={M}, X {xo}, Y {yo}")
     X = lh.HIPDeviceArray("f16", (M, K), order=xo)
     W = lh.HIPDeviceArray("i8", (K, N), order="F")
     s = lh.HIPDeviceArray("f16", (N,))
