@@ -396,8 +396,10 @@ int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y
                         int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream);
 
 /* lava_hip_gemm_w8a16 without any allocation: the same kernels and results (bit for bit),
- * with the split-K workspace (arrival counters and partial blocks) in a fixed per-GPU device
- * array of LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES instead of a library-allocated one.  No
+ * with the workspace (split-K arrival counters and partial blocks, or the row-major copy of a
+ * column-major X) in a fixed per-GPU device array of LAVA_HIP_W8A16_NOALLOC_SCRATCH_BYTES
+ * instead of a library-allocated one -- except that a column-major X whose copy would not fit
+ * (M not a multiple of 8 and M x K above 1 M elements) runs on the generic kernel.  No
  * counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  No call makes a hipMalloc,
  * hipFree or other allocating call; a shape whose plan needs more scratch than the array holds
