@@ -226,8 +226,10 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
 }
 
 // W column-major (K contiguous per output column: the usual layout of a linear layer's weight,
-// W^T row-major), X and Y row-major.  Each column's dot product streams contiguous memory, so a
-// workgroup takes whole columns over all of K -- no split across workgroups, no exchange:
+// W^T row-major), X and Y either way (a column-major X is staged as k-lines, below; one the
+// kernel cannot stage is copied row-major by the host first).  Each column's dot product streams
+// contiguous memory, so a workgroup takes whole columns over all of K -- no split across
+// workgroups, no exchange:
 //  * a workgroup owns KM_COLS = 32 columns (two 16 x 16 MFMA tiles) of one 16-row block of X;
 //    its KM_KSPLIT = 2 wavefronts take half of K each and are added through LDS at the end;
 //  * a wavefront streams its 32 columns in stages of KM_SEG = 128 k: W (32 columns x 128 bytes)
@@ -235,7 +237,8 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
 //    stages (LDS DMA, one 128-byte run of a column per 8 lanes -- HBM serves 128-byte runs of a
 //    column at ~4.8 TB/s against ~3.4 for the 64-byte runs a direct MFMA-layout load would
 //    make), waited for with vmcnt: no barriers between wavefronts.  A stage's buffer is refilled
-//    as soon as its fragments are in registers, before its MFMAs;
+//    as soon as its fragments are in registers, before its MFMAs.  W's DMA carries the
+//    nontemporal hint (W is read once; ~7 % faster);
 //  * 68 KB of LDS per workgroup holds the chip to two workgroups per CU, which spreads a grid
 //    of a few hundred workgroups evenly (a third per CU, from a shallower ring, measured slower);
 //  * LDS rows are XOR-swizzled (16-byte slot = chunk ^ row) so the fragment reads of 16 rows hit
