@@ -378,9 +378,9 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
  *   Y (M x N, fp32) = (X (M x K, fp16) * float(W (K x N, int8))) .* s[col] (fp16).
  * layout: bit0 X row-major, bit1 W row-major, bit2 Y row-major.  Two weight-streaming
  * kernels, every call one launch:
- *  - W column-major (K contiguous per output column), X and Y either way: N a multiple of
- *    32, K of 16, 16-byte aligned W with a leading dimension a multiple of 16.  Whole columns
- *    per workgroup.  X is read in place when row-major (16-byte aligned, ldx a multiple of 8),
+ *  - W column-major (K contiguous per output column), X and Y either way: any N, K a
+ *    multiple of 16, 16-byte aligned W with a leading dimension a multiple of 16.  Whole
+ *    columns per workgroup.  X is read in place when row-major (16-byte aligned, ldx a multiple of 8),
  *    or column-major with M a multiple of 8 (or M == 1 with ldx == 1); any other column-major X
  *    is first copied row-major into the workspace (M x K fp16).
  *  - W row-major, X and Y either way: K a multiple of 32, N of 128 (a row-major X 16-byte

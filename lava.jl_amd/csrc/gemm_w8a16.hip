@@ -55,6 +55,17 @@ struct ScaleStrided {
         return e * (float)s[base + STRIDE * col];
     }
 };
+// The same with the columns at or past n (a ragged last column block) giving zero; the load is
+// unconditional, from a clamped index, so that the loads of a fragment stay in flight together
+// (a predicated load waits for each in turn).
+template <int STRIDE>
+struct ScaleStridedBounded {
+    __device__ float operator()(uint32_t, uint32_t col, float e, const f16* s, uint32_t base, uint32_t n) const {
+        const uint32_t c = base + STRIDE * col;
+        const float sc = (float)s[c < n ? c : n - 1];
+        return c < n ? e * sc : 0.f;
+    }
+};
 
 // Wavefront gw = split * W8_WAVES + w takes the 32-row steps [gw ks, min((gw + 1) ks,
 // total_steps)) of K.  KSTEPS > 0: the host guarantees exactly KSTEPS each, fully
@@ -299,7 +310,7 @@ __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* 
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int cg = w % KM_CG, ks = w / KM_CG;         // column group, K range
     const int q = lane & 15, g = lane >> 4;
-    // the host keeps N a multiple of KM_COLS; this wavefront's columns start at n0
+    // this wavefront's columns start at n0 (the last block may pass N)
     const int n0 = blockIdx.x * KM_COLS + cg * KM_WCOLS;
     const int m0 = blockIdx.y * 16;
     const int stages = (K + KM_SEG - 1) / KM_SEG;
@@ -308,7 +319,8 @@ __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* 
     const int nst = s_end - s_begin;
 
     // buffer resources over this workgroup's 32 columns of W and 16 rows of X
-    const v4i w_rs = make_rsrc(W + (int64_t)n0 * ldw, (uint32_t)(KM_WCOLS * ldw));
+    // (a ragged last column block: the range ends at column N, so columns past it read zero)
+    const v4i w_rs = make_rsrc(W + (int64_t)n0 * ldw, (uint32_t)(max(0, min(KM_WCOLS, N - n0)) * ldw));
     // (X column-major: the host keeps M a multiple of 8, so a 16-byte chunk of 8 rows is wholly
     // inside or wholly past M)
     const v4i x_rs = XROW ? make_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(16 * ldx * 2))
@@ -429,12 +441,12 @@ __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* 
         Frag<float, 16, 16, Accumulator> f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) f.v[j] = sum[j];
-        f = perelement(ScaleStrided<1>{}, f, scale, (uint32_t)(n0 + 16 * t));
+        f = perelement(ScaleStridedBounded<1>{}, f, scale, (uint32_t)(n0 + 16 * t), (uint32_t)N);
         const int col = n0 + 16 * t + q;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int row = m0 + 4 * g + j;
-            if (row < M) Y[YROW ? (int64_t)row * ldy + col : row + (int64_t)col * ldy] = f.v[j];
+            if (row < M && col < N) Y[YROW ? (int64_t)row * ldy + col : row + (int64_t)col * ldy] = f.v[j];
         }
     }
 }
@@ -511,12 +523,12 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
     const size_t copy_bytes = (size_t)((M * K * 2 + 255) / 256 * 256);
     const bool x_copy = !x_ok && !xrow && K <= (int64_t(1) << 26) && M * K <= (int64_t(1) << 36) &&
                         W8_COUNTER_BYTES + copy_bytes <= max_scratch;
-    if ((layout & 2u) == 0 && (x_ok || x_copy) && N % KM_COLS == 0 && K > 0 && K % 16 == 0 && ldw % 16 == 0 &&
+    if ((layout & 2u) == 0 && (x_ok || x_copy) && K > 0 && K % 16 == 0 && ldw % 16 == 0 &&
         ldw >= K && ldw <= (int64_t(1) << 31) / KM_WCOLS && aligned(W, 16) && N <= 0x7fffffff && M <= 0x7fffffff &&
         (M + 15) / 16 <= 65535) {
         p.path = W8_KMAJOR;
         p.mblocks = (M + 15) / 16;
-        p.cblocks = N / KM_COLS;
+        p.cblocks = (N + KM_COLS - 1) / KM_COLS;
         p.xrow = x_ok ? xrow : true;
         p.yrow = layout & 4u;
         p.kldx = x_ok ? kldx : K;

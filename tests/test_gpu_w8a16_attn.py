@@ -135,6 +135,9 @@ def test_w8a16_stream_destroy_releases_workspace(gpu, oracle):
                                    # K not a multiple of the 128-k stage: a partial last stage, and
                                    # K quarters of unequal length (some empty when K < 4 stages)
                                    (16, 4096, 1040), (3, 256, 48), (17, 64, 4112), (16, 32, 400),
+                                   # N not a multiple of the 32-column block: a ragged last block (an LM
+                                   # head with an odd vocabulary, and small N)
+                                   (16, 50257, 1024), (5, 100, 256), (16, 33, 128), (1, 1, 64),
                                    # K not a multiple of 16: the generic kernel
                                    (4, 64, 40)])
 def test_w8a16_weights_column_major(gpu, oracle, M, N, K):
@@ -203,8 +206,8 @@ def test_w8a16_weights_column_major_strided(gpu, oracle, M, N, K, padx, padw):
 
 def test_w8a16_column_major_generic(gpu, oracle):
     lh = gpu
-    announce("w8a16 column-major operands, N not a multiple of 32 (generic kernel)")
-    M, N, K = 8, 100, 64
+    announce("w8a16 column-major operands, K not a multiple of 16 (generic kernel)")
+    M, N, K = 8, 100, 40
     X, W, s = w8_inputs(lh, M, N, K, order="F")
     Y = lh.HIPDeviceArray("f32", (M, N), order="F")
     lh.w8a16(Y, X, W, s)
