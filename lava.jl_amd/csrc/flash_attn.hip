@@ -532,6 +532,29 @@ __device__ __forceinline__ void f5_xor32_pair(float x, float& a, float& b) {
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
 }
 
+// q = fp16(q * c) in place, two elements per instruction: the mixed-precision FMA takes an fp16
+// half of q (op_sel picks which), fp32 c and a zero addend, and rounds the exact product once to
+// fp16 (measured over all 65536 fp16 values at four scales: the correctly rounded product in every
+// case, except that -0 comes out +0, which adds nothing to a dot product; (f16)((float)q * c),
+// rounded twice, differs in up to 3 % of them) -- one instruction instead of two converts, a
+// multiply and a pack.  The trailing s_nop gives a following MFMA that reads q the wait states a
+// VALU write needs before it (this is asm, so the compiler does not count it as a VALU write).
+__device__ __forceinline__ void fa_scale_f16(f16x8& q, float c) {
+    uint4 u = __builtin_bit_cast(uint4, q);
+    asm("v_fma_mixlo_f16 %0, %0, %4, 0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %0, %4, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixlo_f16 %1, %1, %4, 0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %1, %1, %4, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixlo_f16 %2, %2, %4, 0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %2, %2, %4, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixlo_f16 %3, %3, %4, 0 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %3, %3, %4, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]\n\t"
+        "s_nop 1"
+        : "+v"(u.x), "+v"(u.y), "+v"(u.z), "+v"(u.w)
+        : "v"(c));
+    q = __builtin_bit_cast(f16x8, u);
+}
+
 template <bool CAUSAL>
 __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams p) {
     constexpr int DH = 128;
@@ -659,9 +682,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
 #pragma unroll
             for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
-                for (int ks = 0; ks < NKS; ++ks)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) qf[qh][ks][e] = (f16)((float)qf[qh][ks][e] * c);
+                for (int ks = 0; ks < NKS; ++ks) fa_scale_f16(qf[qh][ks], c);
         }
         const float c_raw = fast ? 1.f : c;      // the multiplier S needs on the fp32 path
         f16x8 ones{};                            // bias A operand: 1 at k = 0 of every key row
@@ -704,9 +725,12 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                 if (qh == 1 && f + F5_PFK < 16) fr[f % F5_PFK] = kread(f + F5_PFK);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            // mask: causal key > query (the diagonal block and any past it); else keys >= S
-            if (CAUSAL ? kb >= last : (kb + 1) * F5_BK > p.S) {
-                int dv = CAUSAL ? kb * F5_BK - q0 + 4 * h - r32 : kb * F5_BK + 4 * h - p.S;
+            // mask: causal key > query; else keys >= S.  A pair's causal last block is its diagonal
+            // block (it starts at the pair's first query, kb * 64 = q0, for every pair with a query
+            // below S; the others are never stored), where key tile 1 lies wholly above query half
+            // 0 and key tile 0 wholly below query half 1: only the two diagonal 32 x 32 tiles compare.
+            if (CAUSAL ? kb == last : (kb + 1) * F5_BK > p.S) {
+                int dv = CAUSAL ? 4 * h - r32 : kb * F5_BK + 4 * h - p.S;
                 asm volatile("; mask" : "+v"(dv));
 #pragma unroll
                 for (int kt = 0; kt < 2; ++kt)
@@ -715,6 +739,10 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
 #pragma unroll
                         for (int r = 0; r < 16; ++r) {
                             const int kr = 32 * kt + 8 * (r >> 2) + (r & 3);
+                            if (CAUSAL && kt != qh) {
+                                if (kt > qh) st[kt][qh][r] = -INFINITY;
+                                continue;
+                            }
                             const bool off = CAUSAL ? dv > 32 * qh - kr : dv >= -kr;
                             st[kt][qh][r] = off ? -INFINITY : st[kt][qh][r];
                         }
@@ -918,12 +946,20 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                                          (f16)(o[dt][qh][4 * g4 + 2] * inv[qh]), (f16)(o[dt][qh][4 * g4 + 3] * inv[qh])};
                         *(lds_f16x4*)(uintptr_t)(ost[qh] + (uint32_t)(r32 * RB + (((4 * dt + g4) ^ (r32 & 15)) << 4) + 8 * h)) = v;
                     }
+            // all 16 rows of a lane group read before the first store (one LDS round trip), one
+            // 64-bit base per lane and a row stride
+            const int lrow = lane / CH, cc = lane % CH;
+            f16x8 rv[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const int row = 4 * i + lane / CH, c = lane % CH;
-                const f16x8 v = *(const lds_f16x8*)(uintptr_t)(ost[i / 8] + (uint32_t)((row % 32) * RB + ((c ^ (row & 15)) << 4)));
-                if (q0 + row < p.S && c < dch) __builtin_nontemporal_store(v, reinterpret_cast<f16x8*>(Ob + (int64_t)(q0 + row) * p.osl + 8 * c));
+                const int row = 4 * i + lrow;
+                rv[i] = *(const lds_f16x8*)(uintptr_t)(ost[i / 8] + (uint32_t)((row % 32) * RB + ((cc ^ (row & 15)) << 4)));
             }
+            f16* obase = Ob + (int64_t)(q0 + lrow) * p.osl + 8 * cc;
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (q0 + 4 * i + lrow < p.S && cc < dch)
+                    __builtin_nontemporal_store(rv[i], reinterpret_cast<f16x8*>(obase + (int64_t)(4 * i) * p.osl));
         } else {
 #pragma unroll
             for (int qh = 0; qh < 2; ++qh) {
