@@ -383,9 +383,10 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
  *    columns per workgroup.  X is read in place when row-major (16-byte aligned, ldx a multiple of 8),
  *    or column-major with M a multiple of 8 (or M == 1 with ldx == 1); any other column-major X
  *    is first copied row-major into the workspace (M x K fp16).
- *  - W row-major, X and Y either way: K a multiple of 32, N of 128 (a row-major X 16-byte
- *    aligned with ldx a multiple of 8).  Narrower N splits K across workgroups, whose
- *    last-arriving workgroup per column block adds the partial blocks from the workspace.
+ *  - W row-major, X and Y either way: K a multiple of 32, N of 8, 8-byte aligned W with ldw
+ *    a multiple of 8 (a row-major X 16-byte aligned with ldx a multiple of 8).  Narrower N
+ *    splits K across workgroups, whose last-arriving workgroup per column block adds the
+ *    partial blocks from the workspace.
  * The workspace (split-K partials, or the copy of X) is owned by the library, one per
  * (device, stream): a call that grows it allocates (hipMalloc) and so is not capturable --
  * make one call of the largest shape outside capture first.  Calls on one stream from

@@ -71,8 +71,9 @@ struct ScaleStridedBounded {
 // total_steps)) of K.  KSTEPS > 0: the host guarantees exactly KSTEPS each, fully
 // unrolled; KSTEPS == 0: any count (zero included), in unrolled groups of W8_DEPTH.
 // xrow / yrow (wave-uniform): X and Y row-major, else column-major (a lane then gathers its 8
-// k-values of X with 2-byte loads, ldx apart; Y is stored column by column).
-template <int KSTEPS>
+// k-values of X with 2-byte loads, ldx apart; Y is stored column by column).  RAGGED: N is a
+// multiple of 8 but not of W8_COLS (the last column block is partial).
+template <int KSTEPS, bool RAGGED>
 __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restrict__ X, const int8_t* __restrict__ W,
                                                     const f16* __restrict__ scale, float* __restrict__ Y,
                                                     float* partial, unsigned* counters, int M, int N, int64_t ldx,
@@ -94,7 +95,10 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
     // A operand rows: X[m0 + q][k .. k + 8) for this lane's group; rows >= M read as 0
     const bool xrow_ok = (m0 + q) < M;
     const f16* xp = xrow ? X + (int64_t)(m0 + q) * ldx + k_wave + 8 * g : X + (k_wave + 8 * g) * ldx + (m0 + q);
-    const int8_t* wp = W + (k_wave + 8 * g) * ldw + n0 + 8 * q;
+    // B operand columns n0 + 8 q .. + 7; in a ragged last column block (N a multiple of 8) a lane
+    // whose columns lie at or past N reads the last 8 columns instead: those MFMA columns are
+    // never stored, and every load stays in flight unconditionally
+    const int8_t* wp = W + (k_wave + 8 * g) * ldw + (RAGGED ? min(n0 + 8 * q, N - 8) : n0 + 8 * q);
 
     f32x4 acc[8];
 #pragma unroll
@@ -171,7 +175,10 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
         Frag<float, 16, 16, Accumulator> f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) f.v[j] = acc[t][j];
-        f = perelement(ScaleStrided<8>{}, f, scale, (uint32_t)(n0 + t));
+        if constexpr (RAGGED)
+            f = perelement(ScaleStridedBounded<8>{}, f, scale, (uint32_t)(n0 + t), (uint32_t)N);
+        else
+            f = perelement(ScaleStrided<8>{}, f, scale, (uint32_t)(n0 + t));
 #pragma unroll
         for (int j = 0; j < 4; ++j) red[w][4 * g + j][8 * q + t] = f.v[j];
     }
@@ -189,6 +196,7 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
         v[i] = a;
     }
     const int grow = m0 + row;
+    const bool col_ok = !RAGGED || n0 + c4 < N;   // 4 columns wholly in or out (N a multiple of 8)
     if (splits > 1) {
         // Partial block of this split, [split][mb * 16 + row][N].  The stores are agent-scope
         // atomic (coherent across the XCDs' L2 caches, written through to memory) and complete
@@ -197,8 +205,10 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
         // loads, adds all of them in split order and resets the counter for the next call.
         const int64_t rows_pad = (int64_t)gridDim.z * 16;
         float* mine = partial + ((int64_t)split * rows_pad + (int64_t)mb * 16 + row) * N + n0 + c4;
+        if (col_ok) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) __hip_atomic_store(mine + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int i = 0; i < 4; ++i) __hip_atomic_store(mine + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         __shared__ int last;
@@ -213,7 +223,7 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
         f32x4 y = {0.f, 0.f, 0.f, 0.f};
         for (int sp = 0; sp < splits; ++sp) {
             f32x4 pv;
-            if (sp == split) {
+            if (sp == split || !col_ok) {
                 pv = v;
             } else {
                 const float* other = partial + ((int64_t)sp * rows_pad + (int64_t)mb * 16 + row) * N + n0 + c4;
@@ -224,7 +234,7 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
         }
         v = y;
     }
-    if (grow < M) {
+    if (grow < M && col_ok) {
         if (yrow) {
             float* yp = Y + (int64_t)grow * ldy + n0 + c4;
 #pragma unroll
@@ -541,7 +551,7 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
     }
     // W row-major, X and Y either way (a row-major X in 16-byte loads)
     const bool x_row = layout & 1u;
-    const bool fast = (layout & 2u) && N % W8_COLS == 0 && K > 0 && K % W8_KSTEP == 0 &&
+    const bool fast = (layout & 2u) && N % 8 == 0 && K > 0 && K % W8_KSTEP == 0 &&
                       K / W8_KSTEP <= 0x7fffffff && ldw % 8 == 0 && aligned(W, 8) &&
                       (x_row ? ldx % 8 == 0 && aligned(X, 16) : true) && N <= 0x7fffffff && M <= 0x7fffffff &&
                       (M + 15) / 16 <= 65535;
@@ -551,7 +561,7 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
     p.yrow = layout & 4u;
     p.mblocks = (M + 15) / 16;
     p.total_steps = K / W8_KSTEP;
-    p.cblocks = N / W8_COLS;
+    p.cblocks = (N + W8_COLS - 1) / W8_COLS;
     // split K (up to 16 ways; the partial blocks cost 8 * splits bytes per output element of
     // extra traffic) while the grid still fits the 256 CUs in one round, keeping >= 4 steps per
     // wavefront: at 16 x 4096 . 4096 x 14336 the 224-workgroup grid (2 splits) streams faster
@@ -574,7 +584,8 @@ template <int KS>
 static void launch_split_ks(const W8Plan& p, const void* X, const void* W, const void* scale, void* Y, float* partial,
                             unsigned* counters, int64_t M, int64_t N, int64_t ldx, int64_t ldw, int64_t ldy,
                             hipStream_t s) {
-    hipLaunchKernelGGL(w8a16_kernel<KS>, dim3((unsigned)p.cblocks, (unsigned)p.splits, (unsigned)p.mblocks),
+    auto kernel = N % W8_COLS == 0 ? w8a16_kernel<KS, false> : w8a16_kernel<KS, true>;
+    hipLaunchKernelGGL(kernel, dim3((unsigned)p.cblocks, (unsigned)p.splits, (unsigned)p.mblocks),
                        dim3(64 * W8_WAVES), 0, s, (const f16*)X, (const int8_t*)W, (const f16*)scale, (float*)Y, partial,
                        counters, (int)M, (int)N, ldx, ldw, ldy, p.splits, (int)p.ks, (int)p.total_steps, (int)p.xrow,
                        (int)p.yrow);

@@ -73,6 +73,54 @@ def test_w8a16_row_major_w_orders(gpu, oracle, M, N, K, xo, yo):
     assert oracle.rel_frobenius(y1, ref) <= 1e-3
 
 
+@pytest.mark.parametrize("M,N,K,xo,yo", [(16, 136, 4096, "C", "C"), (16, 8, 256, "C", "C"), (5, 1000, 1024, "F", "C"),
+                                         (16, 14344, 4096, "C", "C"), (1, 50264, 64, "C", "F"), (33, 2056, 1120, "F", "F"),
+                                         (16, 200, 96, "C", "C"), (7, 392, 32, "C", "C")])
+def test_w8a16_row_major_w_ragged_n(gpu, oracle, M, N, K, xo, yo):
+    """Row-major W with N a multiple of 8 but not of 128: the split-K kernel's last column block
+    reads the last 8 columns in place of those past N and stores only the columns below N (split
+    and unsplit K); repeat calls identical."""
+    lh = gpu
+    announce(f"w8a16 W row-major ragged N M={M} N={N} K={K} X {xo} Y {yo}")
+    X = lh.HIPDeviceArray("f16", (M, K), order=xo)
+    W = lh.HIPDeviceArray("i8", (K, N), order="C")
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(X, lh_mod.seed(9, 0))
+    lh.fill_i8(W, lh_mod.seed(9, 1), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(9, 2), 0.001, 0.02)
+    Y = lh.HIPDeviceArray("f32", (M, N), order=yo)
+    Y.fill_bytes(0xFF)
+    lh.w8a16(Y, X, W, s)
+    y1 = Y.to_numpy()
+    lh.w8a16(Y, X, W, s)
+    np.testing.assert_array_equal(Y.to_numpy(), y1)
+    ref = oracle.w8a16_rows(np.ascontiguousarray(X.to_numpy()), W.to_numpy(), s.to_numpy(), N, K, K, N, np.arange(M))
+    assert oracle.rel_frobenius(y1, ref) <= 1e-3
+
+
+@pytest.mark.parametrize("M,N,K,padw,pady", [(16, 200, 512, 56, 24), (3, 1032, 4096, 8, 8)])
+def test_w8a16_row_major_w_ragged_n_padding(gpu, oracle, M, N, K, padw, pady):
+    """Row-major W and Y with leading dimensions past a ragged N: the columns past N of Y keep
+    their bytes (no store lands there) and the weight padding is never used."""
+    lh = gpu
+    announce(f"w8a16 W row-major ragged N padded M={M} N={N} K={K} ldw=N+{padw} ldy=N+{pady}")
+    ldw, ldy = N + padw, N + pady
+    X = lh.HIPDeviceArray("f16", (M, K), order="C")
+    Wp = lh.HIPDeviceArray("i8", (K, ldw), order="C")
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(X, lh_mod.seed(10, 0))
+    lh.fill_i8(Wp, lh_mod.seed(10, 1), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(10, 2), 0.001, 0.02)
+    Yp = lh.HIPDeviceArray("f32", (M, ldy), order="C")
+    Yp.fill_bytes(0xFF)
+    lh.w8a16_raw(X.ptr, Wp.ptr, s.ptr, Yp.ptr, M, N, K, K, ldw, ldy, layout=7)
+    yp = Yp.to_numpy()
+    assert (yp[:, N:].view(np.uint32) == 0xFFFFFFFF).all()
+    Wh = np.ascontiguousarray(Wp.to_numpy()[:, :N])
+    ref = oracle.w8a16_rows(X.to_numpy(), Wh, s.to_numpy(), N, K, K, N, np.arange(M))
+    assert oracle.rel_frobenius(np.ascontiguousarray(yp[:, :N]), ref) <= 1e-3
+
+
 def test_w8a16_two_threads_one_stream(gpu, oracle):
     """Split-K calls from two host threads on the NULL stream: each call's kernel pair is
     enqueued whole, so neither thread's partial sums are overwritten by the other's."""
