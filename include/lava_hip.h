@@ -419,8 +419,9 @@ int lava_hip_gemm_w8a16_noalloc(const void* X, const void* W, const void* scale,
  * (src/device/tensor_intrinsics.jl:279-281).  causal != 0 masks key > query.
  * Q, K, V share `strides`; O uses `ostrides` (NULL = same as strides).  MFMA kernels take
  * D <= 128 (a multiple of 8), and 128 < D <= 256 (a multiple of 8) with scale > 0 (two
- * launches, one per 128-column half of V and O); any other D (<= 256) runs on a generic
- * kernel. */
+ * launches, one per 128-column half of V and O), when Q, K and V are 16-byte aligned with
+ * strides[1..3] multiples of 8 and O is 8-byte aligned with ostrides[1..3] multiples of 4; any
+ * other D (<= 256) or layout runs on a generic kernel (one thread per query). */
 int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const void* V, void* O, int64_t B, int64_t H, int64_t S,
                                 int64_t D, const int64_t* strides, const int64_t* ostrides, float scale, int causal,
                                 void* stream);
