@@ -147,3 +147,106 @@ def test_sweep_w8a16(gpu, oracle, layout, M, N, K):
     Xh, Wh = np.ascontiguousarray(X.to_numpy()), np.ascontiguousarray(W.to_numpy())
     ref = oracle.w8a16_rows(Xh, Wh, s.to_numpy(), N, K, K, N, np.arange(M))
     assert oracle.rel_frobenius(y1, ref) <= 1e-3
+
+
+# ---- larger shapes: multi-round grids, XCD orders, K splits; sampled rows against the oracle
+# and, for the GEMM, every element through sum_ij C_ij = (colsum A) . (rowsum B)
+def _gemm_large_cases():
+    rng = np.random.default_rng(8192256)
+    out = []
+    for _ in range(12):
+        dt = str(rng.choice(["f16", "bf16", "i8"]))
+        layout = int(rng.integers(0, 8))
+        M = _dim(rng, 900, 3000, mult_p=0.6, mults=(8, 256))
+        N = _dim(rng, 900, 3000, mult_p=0.6, mults=(8, 256))
+        K = _dim(rng, 256, 3000, mult_p=0.7, mults=(8, 64, 256))
+        out.append((dt, layout, M, N, K))
+    return out
+
+
+@pytest.mark.parametrize("dt,layout,M,N,K", _gemm_large_cases())
+def test_sweep_gemm_large(gpu, oracle, dt, layout, M, N, K):
+    from test_gpu_gemm import check_rows, full_checksum, make_inputs
+    lh = gpu
+    announce(f"sweep gemm large {dt} layout={layout} M={M} N={N} K={K}")
+    A, B = make_inputs(gpu, dt, M, N, K, layout, lh_mod.seed(61, M + N), lh_mod.seed(62, K))
+    C = lh.HIPDeviceArray("i32" if dt == "i8" else "f32", (M, N), order="C" if layout & 4 else "F")
+    C.fill_bytes(0xFF)
+    lh.gemm(C, A, B)
+    rng = np.random.default_rng(M * 31 + N * 17 + K)
+    rows = np.unique(np.concatenate([[0, 255, 256, M - 1], rng.integers(0, M, 12)]))
+    check_rows(oracle, dt, A, B, C, rows, layout)
+    lhs, rhs = full_checksum(C, A, B, dt)
+    if dt == "i8":
+        assert lhs == rhs
+    else:
+        assert abs(lhs - rhs) <= 1e-3 * (abs(rhs) + math.sqrt(M * N * K))
+
+
+def _attn_large_cases():
+    rng = np.random.default_rng(40964096)
+    out = []
+    for D in (64, 96, 128, 128, 128, 200, 256, 48):
+        S = _dim(rng, 1000, 4096, mult_p=0.5, mults=(64, 256))
+        H = int(rng.integers(1, 9))
+        B = int(rng.integers(1, 4))
+        causal = bool(rng.random() < 0.75)
+        scale = 1.0 / math.sqrt(D) if rng.random() < 0.7 else round(float(rng.uniform(0.02, 0.3)), 6)
+        out.append((D, S, H, B, causal, scale))
+    return out
+
+
+@pytest.mark.parametrize("D,S,H,B,causal,scale", _attn_large_cases())
+def test_sweep_attention_large(gpu, oracle, D, S, H, B, causal, scale):
+    lh = gpu
+    announce(f"sweep flash large D={D} S={S} H={H} B={B} causal={causal} scale={scale}")
+    Q, K, V = (lh.HIPDeviceArray("f16", (D, S, H, B)) for _ in range(3))
+    for t, a in enumerate((Q, K, V)):
+        lh.fill_normal(a, lh_mod.seed(71 + t, D * 7919 + S))
+    O = lh.HIPDeviceArray("f16", (D, S, H, B))
+    O.fill_bytes(0xFF)
+    lh.flash_attn_fwd(O, Q, K, V, scale=scale, causal=causal)
+    st = (1, D, D * S, D * S * H)
+    q, k, v = (a.to_numpy().ravel(order="F") for a in (Q, K, V))
+    o = O.to_numpy()
+    assert not np.isnan(o).any()
+    rng = np.random.default_rng(S * 13 + D)
+    rows = np.unique(np.concatenate([[0, 63, 64, 255, 256, S - 1], rng.integers(0, S, 40)]))
+    heads = {(0, 0), (B - 1, H - 1), (int(rng.integers(0, B)), int(rng.integers(0, H)))}
+    for b, h in sorted(heads):
+        ref = oracle.attn_rows(q, k, v, S, D, st, scale, causal, b, h, rows)
+        err = oracle.rel_frobenius(o[:, rows, h, b].T.astype(np.float64), ref)
+        assert err <= 2e-3, (b, h, err)
+
+
+def _w8_large_cases():
+    rng = np.random.default_rng(1614336 * 2)
+    out = []
+    for _ in range(10):
+        layout = int(rng.integers(0, 8))
+        M = int(rng.choice([1, 5, 8, 16, 33, 64]))
+        N = _dim(rng, 900, 20000, mult_p=0.7, mults=(8, 32, 128))
+        K = _dim(rng, 512, 8192, mult_p=0.8, mults=(16, 32, 128))
+        out.append((layout, M, N, K))
+    return out
+
+
+@pytest.mark.parametrize("layout,M,N,K", _w8_large_cases())
+def test_sweep_w8a16_large(gpu, oracle, layout, M, N, K):
+    lh = gpu
+    announce(f"sweep w8a16 large layout={layout} M={M} N={N} K={K}")
+    X = lh.HIPDeviceArray("f16", (M, K), order="C" if layout & 1 else "F")
+    W = lh.HIPDeviceArray("i8", (K, N), order="C" if layout & 2 else "F")
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(X, lh_mod.seed(81, M + K))
+    lh.fill_i8(W, lh_mod.seed(82, N + K), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(83, N), 0.001, 0.02)
+    Y = lh.HIPDeviceArray("f32", (M, N), order="C" if layout & 4 else "F")
+    Y.fill_bytes(0xFF)
+    lh.w8a16(Y, X, W, s)
+    y = Y.to_numpy()
+    assert not np.isnan(y).any()
+    rows = np.unique(np.array([0, M // 2, M - 1]))
+    Xh, Wh = np.ascontiguousarray(X.to_numpy()), np.ascontiguousarray(W.to_numpy())
+    ref = oracle.w8a16_rows(Xh, Wh, s.to_numpy(), N, K, K, N, rows)
+    assert oracle.rel_frobenius(np.ascontiguousarray(y[rows]), ref) <= 1e-3
