@@ -10,7 +10,7 @@ before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
-                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy]
+                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|gemm_shapes|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -87,6 +87,13 @@ TIMED_MEAN_MS = [0.0]
 SETTLE_S = [1.0]
 # launches per timed step for the kernels of a few tens of microseconds (W8A16, the 256^3 GEMM)
 SHORT_GROUP = 10
+# (M, N, K, B row-major) of the gemm_shapes workload
+GEMM_SHAPES = [(8192, 8192, 8192, False), (4096, 4096, 4096, False), (2048, 2048, 2048, False),
+               (1024, 1024, 1024, False), (8192, 14336, 4096, False), (8192, 4096, 14336, False),
+               (8192, 12288, 4096, False), (8192, 4096, 4096, False), (5000, 3000, 2000, False),
+               (16384, 16384, 2048, False), (256, 4096, 4096, False), (64, 14336, 4096, False),
+               (2048, 4096, 4096, False), (1536, 1536, 8192, False), (128, 28672, 8192, False),
+               (2048, 2048, 8192, False), (8192, 14336, 4096, True), (4096, 4096, 4096, True)]
 
 
 def load_traffic(name: str):
@@ -286,7 +293,7 @@ def main():
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96", "attn_d256",
-                             "copy", "vendor_bf16", "w8a16_wrow", "w8a16_julia"])
+                             "copy", "vendor_bf16", "w8a16_wrow", "w8a16_julia", "gemm_shapes"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -354,6 +361,32 @@ def main():
                                                             "zero-clamped loads, bounds-checked store)"},
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "gemm_shapes":
+        # bf16 products off the square configs: language-model projections (8192 tokens), a
+        # ragged non-square product, few-row (decode-like) products; A row-major, B column-major
+        # (K-contiguous, the headline convention) and, for two shapes, B row-major
+        rows = []
+        for (M, N, Kd, brow) in GEMM_SHAPES:
+            if brow:
+                A = lh.HIPDeviceArray("bf16", (M, Kd), order="C")
+                B = lh.HIPDeviceArray("bf16", (Kd, N), order="C")
+                C = lh.HIPDeviceArray("f32", (M, N), order="C")
+                lh.fill_uniform(A, lh.seed(1, 0), -1.0, 1.0)
+                lh.fill_uniform(B, lh.seed(1, 1), -1.0, 1.0)
+                lh.synchronize()
+                kms, _ = timed(lh, lambda: lh.gemm(C, A, B, stream=stream), K, W, stream)
+                flop = 2.0 * M * N * Kd
+                del A, B, C
+            else:
+                flop, kms, _ = bench_gemm(lh, "bf16", 0, K, W, stream, 1, shape=(M, N, Kd))
+            t = flop / (kms * 1e-3) / 1e12
+            rows.append({"M": M, "N": N, "K": Kd, "B": "row" if brow else "col", "kernel_ms": round(kms, 4),
+                         "TFLOP/s": round(t, 1), "frac": round(t / PEAK_BF16_TFLOPS, 3)})
+        gm = math.exp(sum(math.log(r["TFLOP/s"]) for r in rows) / len(rows))
+        out.update({"value": round(gm, 2), "unit": "TFLOP/s", "ms_per_step": None, "dtype": "bf16",
+                    "config": {"workload": "bf16 GEMM over a list of shapes (geometric mean of the per-shape "
+                                           "kernel TFLOP/s), fp32 C row-major, A row-major", "shapes": rows},
+                    "roofline": roofline("mfma", gm, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "attn_d64":
         flop, kms, wms = bench_attn(lh, K, W, stream, D=64)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
