@@ -5,8 +5,8 @@
 // Compute-bound shapes take the 256 x 256 tile kernel (gemm_tn_kernel.hpp) in any
 // operand layout (K-contiguous operands read directly, M/N-contiguous ones through
 // transposing LDS reads, 16- or 8-bit) -- whole tiles, or ragged extents with
-// zero-clamped loads.  Products of at most 16 such tiles, and 16-bit products that the tile
-// kernel would run on few CUs or mostly empty tiles (small_gemm_eligible's rate estimate), take
+// zero-clamped loads.  Products of at most 16 such tiles, and products that the tile kernel
+// would run on few CUs or mostly empty tiles (small_gemm_eligible's rate estimate), take
 // the 64 x 64 small-product kernel; the rest (extents that split a 16-byte chunk) the staged
 // kernel.
 #include <hip/hip_runtime.h>

@@ -294,17 +294,21 @@ bool small_gemm_eligible(const void* A, const void* B, int64_t M, int64_t N, int
     constexpr int64_t EV = 16 / (int64_t)sizeof(T);
     const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
     bool small = tiles256 <= SMALL_GEMM_MAX_TILES;
-    if (!small && sizeof(T) == 2) {
-        // Rate estimates (bf16, measured on the bench's shape list): the tile kernel ~1500 TFLOP/s
-        // times the share of the 256 CUs its tiles occupy times the useful share of the tile area,
-        // the small kernel ~450 times the share of 512 workgroups its 64 x 64 tiles fill.  E.g.
-        // 64 x 14336 x 4096: 94 -> 234 TFLOP/s; 1536^2 x 8192: 275 -> 342; 2048 x 4096 x 4096 stays
-        // on the tile kernel (898 against 494).
+    if (!small) {
+        // Rate estimates (measured on shape lists): the tile kernel ~1500 TFLOP/s (bf16; int8 ~3000
+        // TOP/s) times the share of the 256 CUs its tiles occupy times the useful share of the tile
+        // area, the small kernel ~450 (int8 ~400) times the share of 512 workgroups its 64 x 64
+        // tiles fill.  E.g. bf16 64 x 14336 x 4096: 94 -> 234 TFLOP/s; 1536^2 x 8192: 275 -> 342;
+        // 2048 x 4096 x 4096 stays on the tile kernel (898 against 494); int8 64 x 14336 x 4096:
+        // 166 -> 388 TOP/s, while 128 x 28672 x 8192 (723 against 517) and 2048^3 (651 against 507)
+        // stay on the tile kernel.
+        const double tile_rate = sizeof(T) == 1 ? 3000.0 : 1500.0;
+        const double small_rate = sizeof(T) == 1 ? 400.0 : 450.0;
         const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
         const double occ256 = tiles256 >= 256 ? 1.0 : (double)tiles256 / 256.0;
         const double useful = (double)M * (double)N / ((double)tiles256 * 65536.0);
         const double occ64 = tiles64 >= 512 ? 1.0 : (double)tiles64 / 512.0;
-        small = 1500.0 * occ256 * useful < 450.0 * occ64;
+        small = tile_rate * occ256 * useful < small_rate * occ64;
     }
     return small && aligned(A, 16) && aligned(B, 16) && lda % EV == 0 && ldb % EV == 0 &&
            ((arow || !brow) ? K % EV == 0 : true) && (arow || M % EV == 0) && (!brow || N % EV == 0);

@@ -13,8 +13,8 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
                        int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi);
 
 // Products the 256 x 256 tile kernel would run on few CUs or on mostly empty tiles, on 64 x 64
-// tiles (16 times the workgroups): at most SMALL_GEMM_MAX_TILES 256 x 256 tiles, and for 16-bit
-// types any product where the small kernel's estimated rate is the higher (small_gemm_eligible).
+// tiles (16 times the workgroups): at most SMALL_GEMM_MAX_TILES 256 x 256 tiles, and any product
+// where the small kernel's estimated rate is the higher (small_gemm_eligible).
 // small_gemm_eligible() also says whether the layout fits the kernel's 16-byte chunks (C
 // row-major; arow / brow: A / B row-major).
 constexpr int64_t SMALL_GEMM_MAX_TILES = 16;
