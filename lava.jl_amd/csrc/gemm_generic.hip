@@ -293,6 +293,8 @@ bool small_gemm_eligible(const void* A, const void* B, int64_t M, int64_t N, int
                          bool arow, bool brow) {
     constexpr int64_t EV = 16 / (int64_t)sizeof(T);
     const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
+    // the launch puts M / 64 in gridDim.y (at most 65535)
+    if ((M + 63) / 64 > 65535 || (N + 63) / 64 > 0x7fffffff) return false;
     bool small = tiles256 <= SMALL_GEMM_MAX_TILES;
     if (!small) {
         // Rate estimates (measured on shape lists): the tile kernel ~1500 TFLOP/s (bf16; int8 ~3000
