@@ -93,7 +93,8 @@ GEMM_SHAPES = [(8192, 8192, 8192, False), (4096, 4096, 4096, False), (2048, 2048
                (8192, 12288, 4096, False), (8192, 4096, 4096, False), (5000, 3000, 2000, False),
                (16384, 16384, 2048, False), (256, 4096, 4096, False), (64, 14336, 4096, False),
                (2048, 4096, 4096, False), (1536, 1536, 8192, False), (128, 28672, 8192, False),
-               (2048, 2048, 8192, False), (8192, 14336, 4096, True), (4096, 4096, 4096, True)]
+               (2048, 2048, 8192, False), (8192, 14336, 4096, True), (4096, 4096, 4096, True),
+               (512, 512, 4096, False), (1024, 1024, 8192, False)]
 
 
 def load_traffic(name: str):

@@ -7,7 +7,8 @@
 // transposing LDS reads, 16- or 8-bit) -- whole tiles, or ragged extents with
 // zero-clamped loads.  Products of at most 16 such tiles, and products that the tile kernel
 // would run on few CUs or mostly empty tiles (small_gemm_eligible's rate estimate), take
-// the 64 x 64 small-product kernel; the rest (extents that split a 16-byte chunk) the staged
+// the 64 x 64 small-product kernel (with K split over the stream's workspace where its tiles
+// alone would leave CUs idle: small_gemm_splits); the rest (extents that split a 16-byte chunk) the staged
 // kernel.
 #include <hip/hip_runtime.h>
 
@@ -60,8 +61,13 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     }
     hipStream_t s = as_stream(stream);
     Acc* c = static_cast<Acc*>(C);
-    if (small_gemm_eligible<T>(a, b, M, N, K, lda, ldb, arow, brow))
+    if (small_gemm_eligible<T>(a, b, M, N, K, lda, ldb, arow, brow)) {
+        if constexpr (!EPI) {
+            const SmallSplit sp = small_gemm_splits<T>(M, N, K);
+            if (sp.splits > 1) return launch_gemm_small_splitk<T>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, stream, sp);
+        }
         return launch_gemm_small<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
+    }
     const int fit = tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
     if (fit != TN_NO)
         return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, fit == TN_RAGGED, arow, !brow);

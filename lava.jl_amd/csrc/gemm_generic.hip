@@ -15,6 +15,7 @@
 //    tile of C, fragments loaded straight from global memory.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "gemm_common.hpp"
@@ -114,10 +115,13 @@ __global__ void __launch_bounds__(256) gemm_staged_kernel(const T* __restrict__ 
 // multiple of EV when an operand is K-contiguous, M (N) a multiple of EV when A (B) is M (N)-
 // contiguous -- so every 16-byte chunk is wholly inside or wholly outside the matrix, and the
 // outside ones read as zero.
+// Split K: workgroup z multiplies K elements [z kspan, min(K, (z + 1) kspan)) and writes its
+// product at C + z zstride (kspan a multiple of the 512-byte chunk; one split: kspan = K).
 template <typename T, bool AROW, bool BROW, typename OutT, bool EPI>
 __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A, const T* __restrict__ B,
                                                          OutT* __restrict__ C, int64_t M, int64_t N, int64_t K,
-                                                         int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi) {
+                                                         int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi,
+                                                         int64_t kspan, int64_t zstride) {
     using Acc = typename Mfma16<T>::acc_elem;
     using AccV = typename Mfma16<T>::acc_t;
     constexpr int EV = 16 / (int)sizeof(T);   // elements per 16-byte chunk
@@ -135,6 +139,8 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
     const int wm = w >> 1, wn = w & 1;
+    const int64_t kb = (int64_t)blockIdx.z * kspan, ke = min(K, kb + kspan);
+    C += (int64_t)blockIdx.z * zstride;
 
     // 16-byte chunk i (of 8) of this thread for the K-chunk at k0 of operand X, whose rows r0 ..
     // r0 + 63 (m or n) are K-contiguous (kcont) or M/N-contiguous
@@ -154,7 +160,7 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
                 p = X + kk * ld + rr;
             }
             reg[i] = make_uint4(0, 0, 0, 0);
-            if (rr < rows && kk < K) reg[i] = *reinterpret_cast<const uint4*>(p);
+            if (rr < rows && kk < ke) reg[i] = *reinterpret_cast<const uint4*>(p);
         }
     };
     auto store = [&](uint8_t* S, auto kcont, auto tr, const uint4* reg) {
@@ -203,17 +209,17 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = AccV{0, 0, 0, 0};
     uint4 ra[8], rb[8];
-    load(A, AK{}, lda, m0, M, 0, ra);
-    load(B, BK{}, ldb, n0, N, 0, rb);
-    for (int64_t k0 = 0; k0 < K; k0 += KC) {
+    load(A, AK{}, lda, m0, M, kb, ra);
+    load(B, BK{}, ldb, n0, N, kb, rb);
+    for (int64_t k0 = kb; k0 < ke; k0 += KC) {
         store(As, AK{}, ATR{}, ra);
         store(Bs, BK{}, BTR{}, rb);
         __syncthreads();
-        if (k0 + KC < K) {   // the next chunk, in flight during this one's MFMAs
+        if (k0 + KC < ke) {   // the next chunk, in flight during this one's MFMAs
             load(A, AK{}, lda, m0, M, k0 + KC, ra);
             load(B, BK{}, ldb, n0, N, k0 + KC, rb);
         }
-        const int64_t nks = min((int64_t)(KC / KE), (K - k0 + KE - 1) / KE);
+        const int64_t nks = min((int64_t)(KC / KE), (ke - k0 + KE - 1) / KE);
 #pragma unroll
         for (int ks = 0; ks < KC / KE; ++ks) {
             if (ks < nks) {
@@ -249,6 +255,25 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
                 }
             }
         }
+}
+
+// The split-K sum: C[m][n] = the splits' partial products P[z][m][n] (row-major, M x N each)
+// added in split order, so a result does not depend on the order the workgroups ran in; int32
+// partials add modulo 2^32, as the MFMA accumulates.  Grid (ceil(N / 256), M).
+template <typename Acc>
+__global__ void __launch_bounds__(256) splitk_sum_kernel(const Acc* __restrict__ P, Acc* __restrict__ C, int64_t M,
+                                                         int64_t N, int64_t ldc, int splits) {
+    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    if (n >= N) return;
+    const int64_t e = m * N + n, mn = M * N;
+    Acc sum = P[e];
+    for (int z = 1; z < splits; ++z) {
+        if constexpr (std::is_same<Acc, int32_t>::value)
+            sum = (int32_t)((uint32_t)sum + (uint32_t)P[z * mn + e]);
+        else
+            sum += P[z * mn + e];
+    }
+    C[m * ldc + n] = sum;
 }
 
 __global__ void __launch_bounds__(256) coopmat_tiles_kernel(const f16* __restrict__ A, const f16* __restrict__ B,
@@ -320,25 +345,81 @@ template bool small_gemm_eligible<bf16>(const void*, const void*, int64_t, int64
 template bool small_gemm_eligible<int8_t>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool,
                                           bool);
 
+namespace {
 template <typename T, typename OutT, bool EPI>
-int launch_gemm_small(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                      int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi) {
-    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
+int launch_small_grid(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                      int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi, int splits,
+                      int64_t kspan, int64_t zstride) {
+    const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)splits);
     if (arow && brow)
         hipLaunchKernelGGL((gemm_small_kernel<T, true, true, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
-                           ldb, ldc, epi);
+                           ldb, ldc, epi, kspan, zstride);
     else if (arow)
         hipLaunchKernelGGL((gemm_small_kernel<T, true, false, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
-                           ldb, ldc, epi);
+                           ldb, ldc, epi, kspan, zstride);
     else if (brow)
         hipLaunchKernelGGL((gemm_small_kernel<T, false, true, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
-                           ldb, ldc, epi);
+                           ldb, ldc, epi, kspan, zstride);
     else
         hipLaunchKernelGGL((gemm_small_kernel<T, false, false, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K,
-                           lda, ldb, ldc, epi);
+                           lda, ldb, ldc, epi, kspan, zstride);
     LAVA_LAUNCH_CHECK("gemm_small_kernel");
     return LAVA_HIP_OK;
 }
+}  // namespace
+
+template <typename T, typename OutT, bool EPI>
+int launch_gemm_small(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                      int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi) {
+    return launch_small_grid<T, OutT, EPI>(A, B, C, M, N, K, lda, ldb, ldc, arow, brow, s, epi, 1, K > 0 ? K : 1, 0);
+}
+
+template <typename T>
+SmallSplit small_gemm_splits(int64_t M, int64_t N, int64_t K) {
+    constexpr int64_t KC = 512 / (int64_t)sizeof(T);   // the kernel's K chunk
+    const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64);
+    const int64_t chunks = (K + KC - 1) / KC;
+    SmallSplit r;
+    // Measured (bf16, one box): 512^2 x 4096 (64 tiles, 16 chunks) 73 -> 124 TFLOP/s, 1024^2 x
+    // 8192 (256 tiles, 32 chunks) 323 -> 379, 64 x 14336 x 4096 232 -> 259, while 1024^3 (256
+    // tiles, 4 chunks) fell 186 -> 128: the partial products' round trip and the second launch
+    // outweigh a short K, more so where the tiles already occupy half the chip.
+    if (tiles > 256 || chunks < (tiles > 128 ? 16 : 8)) return r;
+    int64_t want = std::min<int64_t>(std::min<int64_t>(chunks / 2, 512 / tiles), SMALL_GEMM_MAX_SPLITS);
+    if (want < 2) return r;
+    const int64_t per = (chunks + want - 1) / want;   // chunks per split
+    r.splits = (int)((chunks + per - 1) / per);
+    r.kspan = per * KC;
+    return r;
+}
+
+template <typename T>
+int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
+                             int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, void* stream,
+                             const SmallSplit& sp) {
+    using Acc = typename Mfma16<T>::acc_elem;
+    hipStream_t s = as_stream(stream);
+    const size_t part = (size_t)M * (size_t)N * sizeof(Acc);
+    return with_stream_workspace(STREAM_WS_RESERVED + part * (size_t)sp.splits, stream, [&](void* ws) {
+        Acc* P = reinterpret_cast<Acc*>(static_cast<uint8_t*>(ws) + STREAM_WS_RESERVED);
+        int rc = launch_small_grid<T, Acc, false>(A, B, P, M, N, K, lda, ldb, N, arow, brow, s, Epilogue{}, sp.splits,
+                                                 sp.kspan, M * N);
+        if (rc != LAVA_HIP_OK) return rc;
+        hipLaunchKernelGGL((splitk_sum_kernel<Acc>), dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0, s,
+                           P, C, M, N, ldc, sp.splits);
+        LAVA_LAUNCH_CHECK("splitk_sum_kernel");
+        return LAVA_HIP_OK;
+    });
+}
+template SmallSplit small_gemm_splits<f16>(int64_t, int64_t, int64_t);
+template SmallSplit small_gemm_splits<bf16>(int64_t, int64_t, int64_t);
+template SmallSplit small_gemm_splits<int8_t>(int64_t, int64_t, int64_t);
+template int launch_gemm_small_splitk<f16>(const f16*, const f16*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                           int64_t, bool, bool, void*, const SmallSplit&);
+template int launch_gemm_small_splitk<bf16>(const bf16*, const bf16*, float*, int64_t, int64_t, int64_t, int64_t,
+                                            int64_t, int64_t, bool, bool, void*, const SmallSplit&);
+template int launch_gemm_small_splitk<int8_t>(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t,
+                                              int64_t, int64_t, int64_t, bool, bool, void*, const SmallSplit&);
 
 #define LAVA_STAGED_INST(T, O, E)                                                                              \
     template int launch_gemm_staged<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t, \

@@ -25,6 +25,22 @@ template <typename T, typename OutT, bool EPI>
 int launch_gemm_small(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                       int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi);
 
+// Split K for the small kernel's plain products (no epilogue): a product of at most 256 64 x 64
+// tiles and at least 8 K chunks of 512 bytes (16 above 128 tiles) runs in `splits` K ranges of kspan elements (each
+// >= 2 chunks, splits x tiles <= 512, splits <= SMALL_GEMM_MAX_SPLITS) whose partial products go
+// to the stream's workspace and are summed in split order into C by a second kernel.
+constexpr int64_t SMALL_GEMM_MAX_SPLITS = 16;
+struct SmallSplit {
+    int splits = 1;
+    int64_t kspan = 0;
+};
+template <typename T>
+SmallSplit small_gemm_splits(int64_t M, int64_t N, int64_t K);
+template <typename T>
+int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
+                             int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, void* stream,
+                             const SmallSplit& sp);
+
 // The 16x16x16 vocabulary-tile GEMM (fp16 -> fp32); M, N, K multiples of 16.
 int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s);

@@ -26,6 +26,7 @@
 //  * the scale multiply is the fused per-element epilogue, applied to every partial.
 #include <hip/hip_runtime.h>
 
+#include <functional>
 #include <map>
 #include <mutex>
 #include <vector>
@@ -493,7 +494,7 @@ enum W8Path { W8_GENERIC = 0, W8_SPLIT = 1, W8_KMAJOR = 2 };
 
 // Arrival counters at the front of a split-K workspace: the split rule keeps splits * column
 // blocks * row blocks <= 256 with splits >= 2, so at most 128 counters are ever in use.
-constexpr size_t W8_COUNTER_BYTES = 4096;
+constexpr size_t W8_COUNTER_BYTES = STREAM_WS_RESERVED;
 static_assert(W8_COUNTER_BYTES >= 128 * sizeof(unsigned), "counter region");
 
 struct W8Plan {
@@ -659,7 +660,7 @@ static int check_w8a16_args(const void* X, const void* W, const void* scale, con
     return LAVA_HIP_OK;
 }
 
-// ---- the split-K workspace of lava_hip_gemm_w8a16 ------------------------------------------
+// ---- the per-stream workspace (W8A16 and the small-product GEMM's split-K) -------------------
 // One buffer per (device, stream), owned by the library.  The lock is held from the
 // workspace lookup through the launch, so calls from several threads on one stream use the
 // workspace one after another (stream order).  A buffer that
@@ -673,6 +674,28 @@ struct W8Workspace {
 };
 static std::mutex g_ws_mutex;
 static std::map<std::pair<int, void*>, W8Workspace> g_ws;
+
+int with_stream_workspace(size_t bytes, void* stream, const std::function<int(void*)>& launch) {
+    int dev = 0;
+    LAVA_HIP_TRY(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    W8Workspace& ws = g_ws[{dev, stream}];
+    bytes = bytes < STREAM_WS_RESERVED ? STREAM_WS_RESERVED : bytes;
+    if (ws.bytes < bytes) {
+        void* buf = nullptr;
+        LAVA_HIP_TRY(hipMalloc(&buf, bytes));
+        // the W8A16 arrival counters start at zero (every call leaves them at zero)
+        const int rc = lava_hip_fill_bytes(buf, 0, STREAM_WS_RESERVED, stream);
+        if (rc != LAVA_HIP_OK) {
+            (void)hipFree(buf);
+            return rc;
+        }
+        if (ws.buf) ws.retired.push_back(ws.buf);
+        ws.buf = buf;
+        ws.bytes = bytes;
+    }
+    return launch(ws.buf);
+}
 
 void w8a16_release_stream(void* stream) {
     std::lock_guard<std::mutex> lock(g_ws_mutex);
@@ -739,24 +762,9 @@ extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* sca
     const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout, SIZE_MAX);
     hipStream_t s = as_stream(stream);
     if (p.scratch_bytes == 0) return launch_w8a16(p, X, W, scale, Y, nullptr, M, N, K, ldx, ldw, ldy, layout, s);
-    int dev = 0;
-    LAVA_HIP_TRY(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    W8Workspace& ws = g_ws[{dev, stream}];
-    if (ws.bytes < p.scratch_bytes) {
-        void* buf = nullptr;
-        LAVA_HIP_TRY(hipMalloc(&buf, p.scratch_bytes));
-        // the arrival counters start at zero (every call leaves them at zero)
-        rc = lava_hip_fill_bytes(buf, 0, W8_COUNTER_BYTES, stream);
-        if (rc != LAVA_HIP_OK) {
-            (void)hipFree(buf);
-            return rc;
-        }
-        if (ws.buf) ws.retired.push_back(ws.buf);
-        ws.buf = buf;
-        ws.bytes = p.scratch_bytes;
-    }
-    return launch_w8a16(p, X, W, scale, Y, ws.buf, M, N, K, ldx, ldw, ldy, layout, s);
+    return with_stream_workspace(p.scratch_bytes, stream, [&](void* ws) {
+        return launch_w8a16(p, X, W, scale, Y, ws, M, N, K, ldx, ldw, ldy, layout, s);
+    });
 }
 
 extern "C" int lava_hip_gemm_w8a16_noalloc(const void* X, const void* W, const void* scale, void* Y, int64_t M,

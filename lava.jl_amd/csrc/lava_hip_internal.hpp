@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdint.h>
 
+#include <functional>
+
 #include "lava_hip.h"
 
 namespace lava {
@@ -17,8 +19,16 @@ int check_launch(const char* kernel);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
-// Frees the W8A16 split-K workspaces kept for `stream` (called by lava_hip_stream_destroy
-// once the stream has drained).
+// The library's workspace for `stream` on the current device: grown to at least `bytes` (a
+// grown buffer is retired, not freed), then launch(buffer) runs under the lock that orders its
+// users, so calls from several threads use it one after another in stream order.  The first
+// STREAM_WS_RESERVED bytes hold the W8A16 split-K arrival counters, which every call leaves at
+// zero; other users write only past them.
+constexpr size_t STREAM_WS_RESERVED = 4096;
+int with_stream_workspace(size_t bytes, void* stream, const std::function<int(void*)>& launch);
+
+// Frees the workspaces kept for `stream` (called by lava_hip_stream_destroy once the stream
+// has drained).
 void w8a16_release_stream(void* stream);
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
