@@ -92,8 +92,8 @@ int lava_hip_synchronize(void);
 int lava_hip_stream_synchronize(void* stream);
 /* A non-blocking stream (hipStreamNonBlocking, default priority). */
 int lava_hip_stream_create(void** stream);
-/* Waits for the stream's work, frees the W8A16 workspace the library kept for it, then
- * destroys it. */
+/* Waits for the stream's work, frees the workspace the library kept for it (W8A16 and
+ * small-product GEMM split-K), then destroys it. */
 int lava_hip_stream_destroy(void* stream);
 int lava_hip_event_create(void** event);
 int lava_hip_event_destroy(void* event);
@@ -318,7 +318,11 @@ int lava_hip_tensor_muladd_16x16x16(const void* A, const lava_hip_tensor_layout*
  * named at src/device/coopmat_intrinsics.jl:90; the staged form
  * src/device/coopmat_intrinsics.jl:104-148; the coopmat2 form
  * test/glsl/coopmat2_gemm_regs.comp:37-84 with push block {pa, pb, pc, M, N, K}).
- * Any M, N, K >= 0; layout flags as above; lda/ldb/ldc >= the extent they stride. */
+ * Any M, N, K >= 0; layout flags as above; lda/ldb/ldc >= the extent they stride.
+ * A product of at most 256 64 x 64 tiles with a long K (at least 8 K chunks of 512 bytes, 16
+ * above 128 tiles) splits K: partial products go to the per-stream workspace described at
+ * lava_hip_gemm_w8a16 (allocated or grown on first use, same locking and lifetime) and are
+ * summed in a fixed order, so repeat calls give the same bits. */
 int lava_hip_gemm_f16_f32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                           int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
 /* The bf16 form (no Lava counterpart: the coopmat component table has no bf16,
