@@ -259,21 +259,40 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
 
 // The split-K sum: C[m][n] = the splits' partial products P[z][m][n] (row-major, M x N each)
 // added in split order, so a result does not depend on the order the workgroups ran in; int32
-// partials add modulo 2^32, as the MFMA accumulates.  Grid (ceil(N / 256), M).
-template <typename Acc>
+// partials add modulo 2^32, as the MFMA accumulates.  VEC (N a multiple of 4): each thread sums 4
+// adjacent columns through 16-byte loads (P is 16-byte aligned).  Grid (ceil(N / (256 VEC)), M).
+template <typename Acc, int VEC>
 __global__ void __launch_bounds__(256) splitk_sum_kernel(const Acc* __restrict__ P, Acc* __restrict__ C, int64_t M,
                                                          int64_t N, int64_t ldc, int splits) {
-    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x, m = blockIdx.y;
+    const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VEC, m = blockIdx.y;
     if (n >= N) return;
     const int64_t e = m * N + n, mn = M * N;
-    Acc sum = P[e];
-    for (int z = 1; z < splits; ++z) {
+    auto add = [](Acc x, Acc y) -> Acc {
         if constexpr (std::is_same<Acc, int32_t>::value)
-            sum = (int32_t)((uint32_t)sum + (uint32_t)P[z * mn + e]);
+            return (int32_t)((uint32_t)x + (uint32_t)y);
         else
-            sum += P[z * mn + e];
+            return x + y;
+    };
+    if constexpr (VEC == 4) {
+        using V = typename std::conditional<std::is_same<Acc, int32_t>::value, int4, float4>::type;
+        V sum = *reinterpret_cast<const V*>(P + e);
+        for (int z = 1; z < splits; ++z) {
+            const V p = *reinterpret_cast<const V*>(P + z * mn + e);
+            sum.x = add(sum.x, p.x);
+            sum.y = add(sum.y, p.y);
+            sum.z = add(sum.z, p.z);
+            sum.w = add(sum.w, p.w);
+        }
+        Acc* c = C + m * ldc + n;
+        c[0] = sum.x;
+        c[1] = sum.y;
+        c[2] = sum.z;
+        c[3] = sum.w;
+    } else {
+        Acc sum = P[e];
+        for (int z = 1; z < splits; ++z) sum = add(sum, P[z * mn + e]);
+        C[m * ldc + n] = sum;
     }
-    C[m * ldc + n] = sum;
 }
 
 __global__ void __launch_bounds__(256) coopmat_tiles_kernel(const f16* __restrict__ A, const f16* __restrict__ B,
@@ -405,8 +424,12 @@ int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_ele
         int rc = launch_small_grid<T, Acc, false>(A, B, P, M, N, K, lda, ldb, N, arow, brow, s, Epilogue{}, sp.splits,
                                                  sp.kspan, M * N);
         if (rc != LAVA_HIP_OK) return rc;
-        hipLaunchKernelGGL((splitk_sum_kernel<Acc>), dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256), 0, s,
-                           P, C, M, N, ldc, sp.splits);
+        if (N % 4 == 0)
+            hipLaunchKernelGGL((splitk_sum_kernel<Acc, 4>), dim3((unsigned)((N + 1023) / 1024), (unsigned)M), dim3(256),
+                               0, s, P, C, M, N, ldc, sp.splits);
+        else
+            hipLaunchKernelGGL((splitk_sum_kernel<Acc, 1>), dim3((unsigned)((N + 255) / 256), (unsigned)M), dim3(256),
+                               0, s, P, C, M, N, ldc, sp.splits);
         LAVA_LAUNCH_CHECK("splitk_sum_kernel");
         return LAVA_HIP_OK;
     });

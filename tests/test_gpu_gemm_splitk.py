@@ -24,9 +24,10 @@ pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
 
-# (M, N, K): 64 tiles x 16 chunks (8 splits); ragged M/N with a short last K range (6 splits);
-# one tile row of a wide product (4 splits); 256 tiles x 32 chunks (2 splits)
-SHAPES_16 = [(512, 512, 4096), (136, 200, 3000), (64, 4096, 2048), (1024, 1024, 8192)]
+# (M, N, K): 64 tiles x 16 chunks (8 splits); ragged M/N with a short last K range (6 splits),
+# also with M and N not multiples of 4 (the sum's one-column form); one tile row of a wide
+# product (4 splits); 256 tiles x 32 chunks (2 splits)
+SHAPES_16 = [(512, 512, 4096), (136, 200, 3000), (130, 202, 3000), (64, 4096, 2048), (1024, 1024, 8192)]
 SHAPES_I8 = [(512, 512, 8192), (136, 208, 6000), (64, 4096, 4096)]
 
 
