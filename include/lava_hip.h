@@ -93,17 +93,58 @@ int lava_hip_stream_synchronize(void* stream);
 /* A non-blocking stream (hipStreamNonBlocking, default priority). */
 int lava_hip_stream_create(void** stream);
 /* Waits for the stream's work, frees the workspace the library kept for it (W8A16 and
- * small-product GEMM split-K), then destroys it. */
+ * small-product GEMM split-K; buffers a graph captured on the stream may still use are kept
+ * until the process ends), then destroys it. */
 int lava_hip_stream_destroy(void* stream);
 int lava_hip_event_create(void** event);
 int lava_hip_event_destroy(void* event);
 int lava_hip_event_record(void* event, void* stream);
 int lava_hip_event_elapsed_ms(float* ms, void* start, void* stop);
+/* HIP graphs of the library's calls (thin wrappers over hipStreamBeginCapture in global mode,
+ * hipStreamEndCapture + hipGraphInstantiate, hipGraphLaunch, hipGraphExecDestroy): what a caller
+ * that replays a fixed sequence of launches uses instead of a tracing compiler.  While a stream
+ * captures in global mode, an allocating call anywhere in the process fails; the compute entry
+ * points then plan within the workspace the stream already has (lava_hip_gemm_w8a16) or take
+ * lava_hip_gemm_w8a16_noalloc.  The NULL stream cannot be captured. */
+int lava_hip_graph_capture_begin(void* stream);
+int lava_hip_graph_capture_end(void* stream, void** exec);
+int lava_hip_graph_launch(void* exec, void* stream);
+int lava_hip_graph_destroy(void* exec);
 /* Thread-local message of the last failure on this thread ("" if none).
  * Replaces LavaError/LavaCompilationError reporting (src/runtime/errors.jl:12-51). */
 const char* lava_hip_last_error(void);
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
 int lava_hip_version(void);
+/* Frees every workspace the library keeps (W8A16 split-K partials or the row-major copy of X,
+ * small-product GEMM split-K partials), after waiting for each device that holds one
+ * (hipDeviceSynchronize): the release path of the NULL stream's workspaces, which
+ * lava_hip_stream_destroy does not reach, and of streams created outside the library.  Buffers
+ * that a graph captured on a stream may still use are kept until the process ends.  No
+ * counterpart in the reference (Lava owns no memory); the next call that needs a workspace
+ * allocates one again. */
+int lava_hip_release_workspaces(void);
+
+/* ========================================================================= */
+/* Diagnostics (no counterpart in the reference): which kernels a call ran,   */
+/* and a kernel choice pinned for tests and A/B measurements.                */
+/* ========================================================================= */
+
+/* The names of the kernels this thread launched since its last lava_hip_kernel_log_clear(),
+ * '+'-separated, the newest last (at most 255 bytes; the oldest names are dropped first). */
+const char* lava_hip_kernel_log(void);
+void lava_hip_kernel_log_clear(void);
+
+/* Pins, process-wide, the kernel a family's dispatcher picks (choice 0 restores the automatic
+ * choice).  A pinned kernel that cannot take a call's shape or layout is passed over for the
+ * automatic choice.  Families and choices:
+ *  LAVA_HIP_FAMILY_ATTN: 3 flash_fwd3_kernel (D = 64 or 128, scale > 0), 5 flash_fwd5_kernel
+ *                        (D <= 128, a multiple of 8, any scale);
+ *  LAVA_HIP_FAMILY_GEMM: 1 the 256 x 256 tile kernel, 2 the 64 x 64 small-product kernel
+ *                        without a K split, 3 the staged kernel.
+ * Unknown families or choices return LAVA_HIP_ERR_INVALID_ARG. */
+#define LAVA_HIP_FAMILY_ATTN 1
+#define LAVA_HIP_FAMILY_GEMM 2
+int lava_hip_set_kernel_override(int family, int choice);
 
 /* ========================================================================= */
 /* Device capabilities: the MI355X answer to `caps(backend)::DeviceCaps`       */
@@ -322,7 +363,9 @@ int lava_hip_tensor_muladd_16x16x16(const void* A, const lava_hip_tensor_layout*
  * A product of at most 256 64 x 64 tiles with a long K (at least 8 K chunks of 512 bytes, 16
  * above 128 tiles) splits K: partial products go to the per-stream workspace described at
  * lava_hip_gemm_w8a16 (allocated or grown on first use, same locking and lifetime) and are
- * summed in a fixed order, so repeat calls give the same bits. */
+ * summed in a fixed order, so repeat calls give the same bits.  These are the only plain-GEMM
+ * shapes that allocate; under graph capture they split only within the workspace the stream
+ * already has, and run unsplit otherwise. */
 int lava_hip_gemm_f16_f32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                           int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
 /* The bf16 form (no Lava counterpart: the coopmat component table has no bf16,
@@ -392,9 +435,14 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
  *    splits K across workgroups, whose last-arriving workgroup per column block adds the
  *    partial blocks from the workspace.
  * The workspace (split-K partials, or the copy of X) is owned by the library, one per
- * (device, stream): a call that grows it allocates (hipMalloc) and so is not capturable --
- * make one call of the largest shape outside capture first.  Calls on one stream from
- * several threads are serialised around the workspace; lava_hip_stream_destroy frees it.
+ * (device, stream): a call that grows it allocates (hipMalloc).  A call on a stream that is
+ * capturing a graph never allocates: it plans within the workspace the stream already has
+ * (fewer K splits, or the generic kernel instead of the copy of X; same results to rounding
+ * of the split sums) -- make one call of the largest shape outside capture first to capture
+ * the same plan.  A graph captured with a workspace holds its address: the buffer is then kept
+ * until the process ends, and replaying the graph while calls on its capture stream run
+ * races on it (serialise them).  Calls on one stream from several threads are serialised
+ * around the workspace; lava_hip_stream_destroy and lava_hip_release_workspaces free it.
  * Any other layout or shape runs on a generic kernel.  Results are deterministic (fixed
  * summation order). */
 int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N, int64_t K,

@@ -32,7 +32,6 @@
 //    across groups of the XCD's heads (fa_order).
 #include <hip/hip_runtime.h>
 
-#include <cstdlib>
 #include <type_traits>
 #include <utility>
 
@@ -749,7 +748,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
             }
             // t = how far this block's largest exponent lies above the running maximum
             const bool fast_blk = fast;           // st holds S' (fast) or S (fp32 path)
-            float t[2];
+            float vl[2];   // this lane's largest score per query half
 #pragma unroll
             for (int qh = 0; qh < 2; ++qh) {
                 float v = -INFINITY;
@@ -757,14 +756,18 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                 for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) v = fmaxf(v, st[kt][qh][r]);
-                float a, bb2;
-                f5_xor32_pair(v, a, bb2);
-                const float mx = fmaxf(a, bb2);
-                t[qh] = fast_blk ? mx : fmaf(mx, c_raw, -m_run[qh]);
+                vl[qh] = fast_blk ? v : fmaf(v, c_raw, -m_run[qh]);
             }
-            const bool rescale = first || __builtin_amdgcn_ballot_w64(t[0] > F3_RESCALE || t[1] > F3_RESCALE) != 0;
+            const bool rescale = first || __builtin_amdgcn_ballot_w64(vl[0] > F3_RESCALE || vl[1] > F3_RESCALE) != 0;
             float sub[2] = {0.f, 0.f};
             if (rescale) {
+                float t[2];
+#pragma unroll
+                for (int qh = 0; qh < 2; ++qh) {
+                    float a, bb2;
+                    f5_xor32_pair(vl[qh], a, bb2);
+                    t[qh] = fmaxf(a, bb2);
+                }
                 float mn[2];
                 bool ovf = false;
 #pragma unroll
@@ -1061,18 +1064,17 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     // on flash_fwd5_kernel (score/output wavefront pairs, zero-padded to 128; the scale folds into
     // Q^T, so any sign), D = 64 and D = 256 with a positive scale on flash_fwd3_kernel (ping-pong
     // wavefront pairs; its base-2 running maximum assumes one); all take any S (a ragged last
-    // block of queries or keys is zero-filled and masked).  LAVA_HIP_ATTN_KERNEL=3 in the environment runs D = 128 with a
-    // positive scale on flash_fwd3_kernel as well (a comparison switch; both are
-    // parity-tested).  Everything else runs on flash_generic_kernel.
+    // block of queries or keys is zero-filled and masked).  lava_hip_set_kernel_override
+    // (LAVA_HIP_FAMILY_ATTN, 3) pins flash_fwd3_kernel for D = 128 as well, 5 flash_fwd5_kernel for
+    // D = 64 (tests and A/B timing).  Everything else runs on flash_generic_kernel.
     bool lay_ok = D >= 8 && D <= FA_D && D % 8 == 0 && strides[0] == 1 && os[0] == 1;
     for (int i = 1; i < 4; ++i) lay_ok = lay_ok && strides[i] % 8 == 0 && os[i] % 4 == 0;
     lay_ok = lay_ok && aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8) &&
              S * strides[1] * 2 < ((int64_t)1 << 31);
     const int64_t blocks3 = ((S + F3_BQ - 1) / F3_BQ) * H * B;
     const int64_t blocks5 = ((S + F5_BQ - 1) / F5_BQ) * H * B;
-    const char* sel = getenv("LAVA_HIP_ATTN_KERNEL");
-    const bool want3 = sel && sel[0] == '3';
-    const bool fast3 = lay_ok && scale > 0.f && (D == 64 || (D == FA_D && want3)) && blocks3 <= 0x7fffffff;
+    const int pin = kernel_override(LAVA_HIP_FAMILY_ATTN);
+    const bool fast3 = lay_ok && scale > 0.f && (D == 64 ? pin != 5 : D == FA_D && pin == 3) && blocks3 <= 0x7fffffff;
     const bool fast5 = lay_ok && !fast3 && blocks5 <= 0x7fffffff;
     // 128 < D <= 256 (a multiple of 8) with a positive scale: the ping-pong kernel over Q/K rows
     // zero-padded to 256, once per 128-column half of V and O (the scores are computed twice)

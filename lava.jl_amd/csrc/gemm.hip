@@ -6,7 +6,7 @@
 // operand layout (K-contiguous operands read directly, M/N-contiguous ones through
 // transposing LDS reads, 16- or 8-bit) -- whole tiles, or ragged extents with
 // zero-clamped loads.  Products of at most 16 such tiles, and products that the tile kernel
-// would run on few CUs or mostly empty tiles (small_gemm_eligible's rate estimate), take
+// would run on few CUs or mostly empty tiles (small_gemm_preferred's rate estimate), take
 // the 64 x 64 small-product kernel (with K split over the stream's workspace where its tiles
 // alone would leave CUs idle: small_gemm_splits); the rest (extents that split a 16-byte chunk) the staged
 // kernel.
@@ -61,15 +61,27 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     }
     hipStream_t s = as_stream(stream);
     Acc* c = static_cast<Acc*>(C);
-    if (small_gemm_eligible<T>(a, b, M, N, K, lda, ldb, arow, brow)) {
+    // A kernel pinned by lava_hip_set_kernel_override (tests, A/B timing) runs where it fits.
+    const int pin = kernel_override(LAVA_HIP_FAMILY_GEMM);
+    const bool small_fits = small_gemm_fits<T>(a, b, M, N, K, lda, ldb, arow, brow);
+    const int fit = tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
+    bool use_small;
+    if (pin == 2)
+        use_small = small_fits;
+    else if (pin == 3 || (pin == 1 && fit != TN_NO))
+        use_small = false;
+    else
+        use_small = small_fits && small_gemm_preferred<T>(M, N, K);
+    if (use_small) {
         if constexpr (!EPI) {
-            const SmallSplit sp = small_gemm_splits<T>(M, N, K);
-            if (sp.splits > 1) return launch_gemm_small_splitk<T>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, stream, sp);
+            const SmallSplit sp = pin == 2 ? SmallSplit{} : small_gemm_splits<T>(M, N, K);
+            // under graph capture, split only within the workspace the stream already has
+            if (sp.splits > 1 && small_splitk_bytes<T>(M, N, sp) <= stream_workspace_cap(stream))
+                return launch_gemm_small_splitk<T>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, stream, sp);
         }
         return launch_gemm_small<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
     }
-    const int fit = tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
-    if (fit != TN_NO)
+    if (fit != TN_NO && pin != 3)
         return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, fit == TN_RAGGED, arow, !brow);
     LAVA_REQUIRE((N + 63) / 64 <= 0x7fffffff && (M + 63) / 64 <= 65535, LAVA_HIP_ERR_UNSUPPORTED,
                  "%s: too many 64-row tiles for the staged kernel (M=%lld N=%lld)", name, (long long)M, (long long)N);

@@ -111,7 +111,7 @@ __global__ void __launch_bounds__(256) gemm_staged_kernel(const T* __restrict__ 
 //    144), and its fragments are read with two ds_read_b64_tr_b16 (4 k-values of one column per
 //    lane each);
 //  * an M/N-contiguous int8 operand is transposed by byte stores into the [row][k] layout.
-// Host conditions (small_gemm_eligible): 16-byte aligned operands and leading dimensions, K a
+// Host conditions (small_gemm_fits): 16-byte aligned operands and leading dimensions, K a
 // multiple of EV when an operand is K-contiguous, M (N) a multiple of EV when A (B) is M (N)-
 // contiguous -- so every 16-byte chunk is wholly inside or wholly outside the matrix, and the
 // outside ones read as zero.
@@ -333,36 +333,41 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
 }
 
 template <typename T>
-bool small_gemm_eligible(const void* A, const void* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                         bool arow, bool brow) {
-    constexpr int64_t EV = 16 / (int64_t)sizeof(T);
+bool small_gemm_preferred(int64_t M, int64_t N, int64_t) {
     const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
+    if (tiles256 <= SMALL_GEMM_MAX_TILES) return true;
+    // Rate estimates (measured on shape lists): the tile kernel ~1500 TFLOP/s (bf16; int8 ~3000
+    // TOP/s) times the share of the 256 CUs its tiles occupy times the useful share of the tile
+    // area, the small kernel ~450 (int8 ~400) times the share of 512 workgroups its 64 x 64
+    // tiles fill.  E.g. bf16 64 x 14336 x 4096: 94 -> 234 TFLOP/s; 1536^2 x 8192: 275 -> 342;
+    // 2048 x 4096 x 4096 stays on the tile kernel (898 against 494); int8 64 x 14336 x 4096:
+    // 166 -> 388 TOP/s, while 128 x 28672 x 8192 (723 against 517) and 2048^3 (651 against 507)
+    // stay on the tile kernel.
+    const double tile_rate = sizeof(T) == 1 ? 3000.0 : 1500.0;
+    const double small_rate = sizeof(T) == 1 ? 400.0 : 450.0;
+    const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
+    const double occ256 = tiles256 >= 256 ? 1.0 : (double)tiles256 / 256.0;
+    const double useful = (double)M * (double)N / ((double)tiles256 * 65536.0);
+    const double occ64 = tiles64 >= 512 ? 1.0 : (double)tiles64 / 512.0;
+    return tile_rate * occ256 * useful < small_rate * occ64;
+}
+
+template <typename T>
+bool small_gemm_fits(const void* A, const void* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, bool arow,
+                     bool brow) {
+    constexpr int64_t EV = 16 / (int64_t)sizeof(T);
     // the launch puts M / 64 in gridDim.y (at most 65535)
     if ((M + 63) / 64 > 65535 || (N + 63) / 64 > 0x7fffffff) return false;
-    bool small = tiles256 <= SMALL_GEMM_MAX_TILES;
-    if (!small) {
-        // Rate estimates (measured on shape lists): the tile kernel ~1500 TFLOP/s (bf16; int8 ~3000
-        // TOP/s) times the share of the 256 CUs its tiles occupy times the useful share of the tile
-        // area, the small kernel ~450 (int8 ~400) times the share of 512 workgroups its 64 x 64
-        // tiles fill.  E.g. bf16 64 x 14336 x 4096: 94 -> 234 TFLOP/s; 1536^2 x 8192: 275 -> 342;
-        // 2048 x 4096 x 4096 stays on the tile kernel (898 against 494); int8 64 x 14336 x 4096:
-        // 166 -> 388 TOP/s, while 128 x 28672 x 8192 (723 against 517) and 2048^3 (651 against 507)
-        // stay on the tile kernel.
-        const double tile_rate = sizeof(T) == 1 ? 3000.0 : 1500.0;
-        const double small_rate = sizeof(T) == 1 ? 400.0 : 450.0;
-        const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
-        const double occ256 = tiles256 >= 256 ? 1.0 : (double)tiles256 / 256.0;
-        const double useful = (double)M * (double)N / ((double)tiles256 * 65536.0);
-        const double occ64 = tiles64 >= 512 ? 1.0 : (double)tiles64 / 512.0;
-        small = tile_rate * occ256 * useful < small_rate * occ64;
-    }
-    return small && aligned(A, 16) && aligned(B, 16) && lda % EV == 0 && ldb % EV == 0 &&
+    return aligned(A, 16) && aligned(B, 16) && lda % EV == 0 && ldb % EV == 0 &&
            ((arow || !brow) ? K % EV == 0 : true) && (arow || M % EV == 0) && (!brow || N % EV == 0);
 }
-template bool small_gemm_eligible<f16>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool, bool);
-template bool small_gemm_eligible<bf16>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool, bool);
-template bool small_gemm_eligible<int8_t>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool,
-                                          bool);
+#define LAVA_SMALL_RULE_INST(T)                                                                                      \
+    template bool small_gemm_preferred<T>(int64_t, int64_t, int64_t);                                                 \
+    template bool small_gemm_fits<T>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool, bool);
+LAVA_SMALL_RULE_INST(f16)
+LAVA_SMALL_RULE_INST(bf16)
+LAVA_SMALL_RULE_INST(int8_t)
+#undef LAVA_SMALL_RULE_INST
 
 namespace {
 template <typename T, typename OutT, bool EPI>
@@ -413,13 +418,20 @@ SmallSplit small_gemm_splits(int64_t M, int64_t N, int64_t K) {
 }
 
 template <typename T>
+size_t small_splitk_bytes(int64_t M, int64_t N, const SmallSplit& sp) {
+    return STREAM_WS_RESERVED + (size_t)M * (size_t)N * sizeof(typename Mfma16<T>::acc_elem) * (size_t)sp.splits;
+}
+template size_t small_splitk_bytes<f16>(int64_t, int64_t, const SmallSplit&);
+template size_t small_splitk_bytes<bf16>(int64_t, int64_t, const SmallSplit&);
+template size_t small_splitk_bytes<int8_t>(int64_t, int64_t, const SmallSplit&);
+
+template <typename T>
 int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
                              int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, void* stream,
                              const SmallSplit& sp) {
     using Acc = typename Mfma16<T>::acc_elem;
     hipStream_t s = as_stream(stream);
-    const size_t part = (size_t)M * (size_t)N * sizeof(Acc);
-    return with_stream_workspace(STREAM_WS_RESERVED + part * (size_t)sp.splits, stream, [&](void* ws) {
+    return with_stream_workspace(small_splitk_bytes<T>(M, N, sp), stream, [&](void* ws) {
         Acc* P = reinterpret_cast<Acc*>(static_cast<uint8_t*>(ws) + STREAM_WS_RESERVED);
         int rc = launch_small_grid<T, Acc, false>(A, B, P, M, N, K, lda, ldb, N, arow, brow, s, Epilogue{}, sp.splits,
                                                  sp.kspan, M * N);

@@ -14,13 +14,15 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
 
 // Products the 256 x 256 tile kernel would run on few CUs or on mostly empty tiles, on 64 x 64
 // tiles (16 times the workgroups): at most SMALL_GEMM_MAX_TILES 256 x 256 tiles, and any product
-// where the small kernel's estimated rate is the higher (small_gemm_eligible).
-// small_gemm_eligible() also says whether the layout fits the kernel's 16-byte chunks (C
-// row-major; arow / brow: A / B row-major).
+// where the small kernel's estimated rate is the higher (small_gemm_preferred).
+// small_gemm_fits() says whether the layout fits the kernel's 16-byte chunks (C row-major;
+// arow / brow: A / B row-major).
 constexpr int64_t SMALL_GEMM_MAX_TILES = 16;
 template <typename T>
-bool small_gemm_eligible(const void* A, const void* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                         bool arow, bool brow);
+bool small_gemm_preferred(int64_t M, int64_t N, int64_t K);
+template <typename T>
+bool small_gemm_fits(const void* A, const void* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, bool arow,
+                     bool brow);
 template <typename T, typename OutT, bool EPI>
 int launch_gemm_small(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                       int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi);
@@ -36,6 +38,9 @@ struct SmallSplit {
 };
 template <typename T>
 SmallSplit small_gemm_splits(int64_t M, int64_t N, int64_t K);
+// Workspace bytes of a split plan: the W8A16 counter region, then one M x N partial per split.
+template <typename T>
+size_t small_splitk_bytes(int64_t M, int64_t N, const SmallSplit& sp);
 template <typename T>
 int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
                              int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, void* stream,

@@ -29,6 +29,7 @@
 #include <functional>
 #include <map>
 #include <mutex>
+#include <set>
 #include <vector>
 
 #include "lava_coopmat.hpp"
@@ -514,7 +515,8 @@ struct W8Plan {
     size_t scratch_bytes = 0;
 };
 
-// max_scratch: the most workspace the caller can provide (the no-allocation entry's fixed array).
+// max_scratch: the most workspace the caller can provide (the no-allocation entry's fixed array, or
+// under graph capture the workspace the stream already has).
 static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldw,
                          uint32_t layout, size_t max_scratch) {
     W8Plan p;
@@ -567,8 +569,12 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
     // extra traffic) while the grid still fits the 256 CUs in one round, keeping >= 4 steps per
     // wavefront: at 16 x 4096 . 4096 x 14336 the 224-workgroup grid (2 splits) streams faster
     // than the 448-workgroup one (4 splits), and 1 split (112 workgroups) is ~20 % slower
+    // (and within max_scratch: under graph capture the workspace the stream already has)
+    auto split_bytes = [&](int sp) {
+        return W8_COUNTER_BYTES + (size_t)sp * (size_t)p.mblocks * 16 * (size_t)N * sizeof(float);
+    };
     while (p.splits < 16 && p.cblocks * p.mblocks * p.splits * 2 <= 256 &&
-           p.total_steps / (W8_WAVES * p.splits * 2) >= 4)
+           p.total_steps / (W8_WAVES * p.splits * 2) >= 4 && split_bytes(p.splits * 2) <= max_scratch)
         p.splits *= 2;
     p.ks = (p.total_steps + W8_WAVES * p.splits - 1) / (W8_WAVES * p.splits);
     p.ksteps = p.ks * W8_WAVES * p.splits == p.total_steps ? (int)p.ks : 0;   // unrolled instances need equal shares
@@ -576,7 +582,7 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
         // the counters keep a fixed place at the front of a workspace that calls of other
         // shapes reuse: every counter is zero between calls, and no partial block covers one
         p.counter_bytes = W8_COUNTER_BYTES;
-        p.scratch_bytes = p.counter_bytes + (size_t)p.splits * (size_t)p.mblocks * 16 * (size_t)N * sizeof(float);
+        p.scratch_bytes = split_bytes(p.splits);
     }
     return p;
 }
@@ -663,25 +669,55 @@ static int check_w8a16_args(const void* X, const void* W, const void* scale, con
 // ---- the per-stream workspace (W8A16 and the small-product GEMM's split-K) -------------------
 // One buffer per (device, stream), owned by the library.  The lock is held from the
 // workspace lookup through the launch, so calls from several threads on one stream use the
-// workspace one after another (stream order).  A buffer that
-// grows is retired, not freed -- work already enqueued or a graph captured earlier may
-// still use it -- and every buffer of a stream is freed by lava_hip_stream_destroy
-// (after the stream drains); buffers of the NULL stream live until the process ends.
+// workspace one after another (stream order).  A buffer that grows is retired, not freed --
+// work already enqueued may still use it -- and every buffer of a stream is freed by
+// lava_hip_stream_destroy (after the stream drains) or lava_hip_release_workspaces (after the
+// device drains).  A stream that is capturing a graph never allocates (hipMalloc is not
+// capturable): its calls plan within the buffer it has (stream_workspace_cap), and that buffer
+// is marked as held by a graph, which may replay it after the stream is gone, so it is moved
+// to g_ws_kept instead of being freed.
 struct W8Workspace {
     void* buf = nullptr;
     size_t bytes = 0;
+    bool captured = false;          // a graph captured on the stream holds buf
     std::vector<void*> retired;
 };
 static std::mutex g_ws_mutex;
 static std::map<std::pair<int, void*>, W8Workspace> g_ws;
+static std::vector<void*> g_ws_kept;    // buffers graphs may hold: kept until the process ends
+
+// Whether `stream` is capturing a graph; a failed query counts as capturing (the caller then
+// does not allocate), and its error is taken off HIP's last-error slot so that the next launch
+// check does not report it.
+static bool stream_capturing(void* stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(as_stream(stream), &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return true;
+    }
+    return st != hipStreamCaptureStatusNone;
+}
+
+size_t stream_workspace_cap(void* stream) {
+    if (!stream_capturing(stream)) return SIZE_MAX;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    auto it = g_ws.find({dev, stream});
+    return it == g_ws.end() ? 0 : it->second.bytes;
+}
 
 int with_stream_workspace(size_t bytes, void* stream, const std::function<int(void*)>& launch) {
     int dev = 0;
     LAVA_HIP_TRY(hipGetDevice(&dev));
+    const bool capturing = stream_capturing(stream);
     std::lock_guard<std::mutex> lock(g_ws_mutex);
     W8Workspace& ws = g_ws[{dev, stream}];
     bytes = bytes < STREAM_WS_RESERVED ? STREAM_WS_RESERVED : bytes;
     if (ws.bytes < bytes) {
+        LAVA_REQUIRE(!capturing, LAVA_HIP_ERR_UNSUPPORTED,
+                     "the stream is capturing a graph and its workspace (%zu bytes) is smaller than this call needs "
+                     "(%zu bytes): make one call of this shape outside capture first", ws.bytes, bytes);
         void* buf = nullptr;
         LAVA_HIP_TRY(hipMalloc(&buf, bytes));
         // the W8A16 arrival counters start at zero (every call leaves them at zero)
@@ -690,11 +726,28 @@ int with_stream_workspace(size_t bytes, void* stream, const std::function<int(vo
             (void)hipFree(buf);
             return rc;
         }
-        if (ws.buf) ws.retired.push_back(ws.buf);
+        if (ws.buf) (ws.captured ? g_ws_kept : ws.retired).push_back(ws.buf);
         ws.buf = buf;
         ws.bytes = bytes;
+        ws.captured = false;
     }
+    if (capturing) ws.captured = true;
     return launch(ws.buf);
+}
+
+// Frees (or, if a graph may hold it, keeps) every buffer of one workspace entry, on its device.
+static void release_entry(int dev, W8Workspace& ws) {
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    (void)hipSetDevice(dev);
+    for (void* b : ws.retired) (void)hipFree(b);
+    if (ws.buf) {
+        if (ws.captured)
+            g_ws_kept.push_back(ws.buf);
+        else
+            (void)hipFree(ws.buf);
+    }
+    (void)hipSetDevice(cur);
 }
 
 void w8a16_release_stream(void* stream) {
@@ -704,12 +757,7 @@ void w8a16_release_stream(void* stream) {
             ++it;
             continue;
         }
-        int cur = 0;
-        (void)hipGetDevice(&cur);
-        (void)hipSetDevice(it->first.first);
-        for (void* b : it->second.retired) (void)hipFree(b);
-        if (it->second.buf) (void)hipFree(it->second.buf);
-        (void)hipSetDevice(cur);
+        release_entry(it->first.first, it->second);
         it = g_ws.erase(it);
     }
 }
@@ -753,13 +801,31 @@ static int scratch_for_device(void** out, void* stream) {
 
 using namespace lava;
 
+extern "C" int lava_hip_release_workspaces(void) {
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    int cur = 0;
+    LAVA_HIP_TRY(hipGetDevice(&cur));
+    std::set<int> devs;
+    for (auto& e : g_ws) devs.insert(e.first.first);
+    for (int d : devs) {   // the buffers' last users may still be queued on any stream of the device
+        LAVA_HIP_TRY(hipSetDevice(d));
+        const hipError_t e = hipDeviceSynchronize();
+        (void)hipSetDevice(cur);
+        LAVA_HIP_TRY(e);
+    }
+    for (auto& e : g_ws) release_entry(e.first.first, e.second);
+    g_ws.clear();
+    return LAVA_HIP_OK;
+}
+
 extern "C" int lava_hip_gemm_w8a16(const void* X, const void* W, const void* scale, void* Y, int64_t M, int64_t N,
                                    int64_t K, int64_t ldx, int64_t ldw, int64_t ldy, uint32_t layout, void* stream) {
     int rc = check_w8a16_args(X, W, scale, Y, M, N, K, ldx, ldw, ldy, layout, "gemm_w8a16");
     if (rc != LAVA_HIP_OK || M == 0 || N == 0) return rc;
     rc = lava_hip_init();
     if (rc != LAVA_HIP_OK) return rc;
-    const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout, SIZE_MAX);
+    // planned within the workspace the stream has when it is capturing a graph
+    const W8Plan p = plan_w8a16(X, W, M, N, K, ldx, ldw, layout, stream_workspace_cap(stream));
     hipStream_t s = as_stream(stream);
     if (p.scratch_bytes == 0) return launch_w8a16(p, X, W, scale, Y, nullptr, M, N, K, ldx, ldw, ldy, layout, s);
     return with_stream_workspace(p.scratch_bytes, stream, [&](void* ws) {

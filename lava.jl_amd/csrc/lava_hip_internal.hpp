@@ -14,8 +14,11 @@ namespace lava {
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();
 int hip_fail(hipError_t e, const char* what);
-// Launch check: the error (if any) hipGetLastError reports for the launch just made.
+// Launch check: the error (if any) hipGetLastError reports for the launch just made; a launch
+// that succeeded is appended to the thread's kernel log (lava_hip_kernel_log).
 int check_launch(const char* kernel);
+// The kernel choice pinned for a family (LAVA_HIP_FAMILY_*) by lava_hip_set_kernel_override; 0 = automatic.
+int kernel_override(int family);
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
@@ -25,7 +28,13 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 // STREAM_WS_RESERVED bytes hold the W8A16 split-K arrival counters, which every call leaves at
 // zero; other users write only past them.
 constexpr size_t STREAM_WS_RESERVED = 4096;
+// A call on a stream that is capturing a graph does not allocate: it must fit the workspace the
+// stream already has (the buffer is then kept until the process ends, since the graph holds
+// its address).
 int with_stream_workspace(size_t bytes, void* stream, const std::function<int(void*)>& launch);
+// The most workspace a call on `stream` may plan for: unlimited (SIZE_MAX) unless the stream is
+// capturing a graph, then the size of the buffer it already has (0 if none).
+size_t stream_workspace_cap(void* stream);
 
 // Frees the workspaces kept for `stream` (called by lava_hip_stream_destroy once the stream
 // has drained).

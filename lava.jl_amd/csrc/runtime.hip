@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "lava_hip_internal.hpp"
@@ -30,13 +31,41 @@ int hip_fail(hipError_t e, const char* what) {
     return e == hipErrorNoDevice ? LAVA_HIP_ERR_NO_DEVICE : LAVA_HIP_ERR_HIP;
 }
 
+// Names of the kernels this thread launched, '+'-separated, the newest last (lava_hip_kernel_log).
+static thread_local char g_klog[256] = "";
+
+static void log_kernel(const char* name) {
+    const size_t m = strlen(name);
+    if (m + 1 >= sizeof(g_klog)) return;
+    size_t n = strlen(g_klog);
+    while (n > 0 && n + 1 + m + 1 > sizeof(g_klog)) {   // drop the oldest names until this one fits
+        const char* plus = strchr(g_klog, '+');
+        if (plus == nullptr) {
+            n = 0;
+            break;
+        }
+        memmove(g_klog, plus + 1, strlen(plus + 1) + 1);
+        n = strlen(g_klog);
+    }
+    if (n > 0) g_klog[n++] = '+';
+    memcpy(g_klog + n, name, m + 1);
+}
+
 int check_launch(const char* kernel) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         set_error("launch of %s failed: %s (%d)", kernel, hipGetErrorString(e), (int)e);
         return LAVA_HIP_ERR_HIP;
     }
+    log_kernel(kernel);
     return LAVA_HIP_OK;
+}
+
+// Kernel choices pinned by lava_hip_set_kernel_override, per family (0 = automatic).
+static std::atomic<int> g_override[3];
+
+int kernel_override(int family) {
+    return family > 0 && family < 3 ? g_override[family].load(std::memory_order_relaxed) : 0;
 }
 
 __global__ void fill_bytes_kernel(uint8_t* __restrict__ dst, uint8_t value, size_t n) {
@@ -80,6 +109,18 @@ using namespace lava;
 extern "C" {
 
 const char* lava_hip_last_error(void) { return g_err; }
+
+const char* lava_hip_kernel_log(void) { return g_klog; }
+
+void lava_hip_kernel_log_clear(void) { g_klog[0] = 0; }
+
+int lava_hip_set_kernel_override(int family, int choice) {
+    const bool ok = (family == LAVA_HIP_FAMILY_ATTN && (choice == 0 || choice == 3 || choice == 5)) ||
+                    (family == LAVA_HIP_FAMILY_GEMM && choice >= 0 && choice <= 3);
+    LAVA_ARG(ok, "set_kernel_override: unknown family %d or choice %d", family, choice);
+    g_override[family].store(choice, std::memory_order_relaxed);
+    return LAVA_HIP_OK;
+}
 
 int lava_hip_version(void) { return 100; }
 
@@ -226,6 +267,37 @@ int lava_hip_event_elapsed_ms(float* ms, void* start, void* stop) {
     LAVA_ARG(ms != nullptr && start != nullptr && stop != nullptr, "event_elapsed_ms: null argument");
     LAVA_HIP_TRY(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)));
     LAVA_HIP_TRY(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_graph_capture_begin(void* stream) {
+    LAVA_ARG(stream != nullptr, "graph_capture_begin: the NULL stream cannot be captured");
+    LAVA_HIP_TRY(hipStreamBeginCapture(as_stream(stream), hipStreamCaptureModeGlobal));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_graph_capture_end(void* stream, void** exec) {
+    LAVA_ARG(stream != nullptr && exec != nullptr, "graph_capture_end: null stream or output pointer");
+    *exec = nullptr;
+    hipGraph_t g = nullptr;
+    LAVA_HIP_TRY(hipStreamEndCapture(as_stream(stream), &g));
+    hipGraphExec_t e = nullptr;
+    const hipError_t r = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);   // the executable graph keeps what it needs
+    LAVA_HIP_TRY(r);
+    *exec = e;
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_graph_launch(void* exec, void* stream) {
+    LAVA_ARG(exec != nullptr, "graph_launch: null graph");
+    LAVA_HIP_TRY(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(exec), as_stream(stream)));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_graph_destroy(void* exec) {
+    if (exec == nullptr) return LAVA_HIP_OK;
+    LAVA_HIP_TRY(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(exec)));
     return LAVA_HIP_OK;
 }
 

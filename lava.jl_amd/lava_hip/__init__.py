@@ -5,8 +5,9 @@ include/lava_hip.h).  This package is its Python host mirror: loader, device
 arrays, the host half of the vocabulary, and destination-first kernel calls.
 """
 from . import _lib
-from ._lib import InvalidArgument, LavaHIPError, NoDevice, Unsupported, load
-from .device import Event, HIPDeviceArray, Stream, device_count, synchronize
+from ._lib import (FAMILY_ATTN, FAMILY_GEMM, InvalidArgument, LavaHIPError, NoDevice, Unsupported, kernel_log,
+                   kernel_log_clear, load, release_workspaces, set_kernel_override)
+from .device import Event, Graph, HIPDeviceArray, Stream, device_count, synchronize
 from .kernels import (coopmat_accinit_muladd, coopmat_convert, coopmat_convert_use, coopmat_convert_use_muladd,
                       coopmat_elementwise, coopmat_foreach_act, coopmat_gemm_tiles, coopmat_length,
                       coopmat_muladd_16x16x16, coopmat_perelement_pair, coopmat_perelement_rowcol,

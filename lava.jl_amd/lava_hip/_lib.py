@@ -110,7 +110,18 @@ PROTOTYPES: dict[str, tuple] = {
     "lava_hip_gemm_w8a16_noalloc": (ci, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_flash_attn_fwd_f16": (ci, [vp, vp, vp, vp, i64, i64, i64, i64, C.POINTER(i64),
                                          C.POINTER(i64), C.c_float, ci, vp]),
+    "lava_hip_release_workspaces": (ci, []),
+    "lava_hip_graph_capture_begin": (ci, [vp]),
+    "lava_hip_graph_capture_end": (ci, [vp, C.POINTER(vp)]),
+    "lava_hip_graph_launch": (ci, [vp, vp]),
+    "lava_hip_graph_destroy": (ci, [vp]),
+    "lava_hip_kernel_log": (C.c_char_p, []),
+    "lava_hip_kernel_log_clear": (None, []),
+    "lava_hip_set_kernel_override": (ci, [ci, ci]),
 }
+
+# kernel families of lava_hip_set_kernel_override
+FAMILY_ATTN, FAMILY_GEMM = 1, 2
 
 _lib: C.CDLL | None = None
 
@@ -154,3 +165,23 @@ def check(status: int) -> None:
 
 def call(name: str, *args) -> None:
     check(getattr(load(), name)(*args))
+
+
+def kernel_log() -> list[str]:
+    """Names of the kernels this thread launched since the last kernel_log_clear()."""
+    raw = load().lava_hip_kernel_log()
+    return raw.decode().split("+") if raw else []
+
+
+def kernel_log_clear() -> None:
+    load().lava_hip_kernel_log_clear()
+
+
+def set_kernel_override(family: int, choice: int) -> None:
+    """Pin a family's kernel choice process-wide (0 = automatic); for tests and A/B timing."""
+    call("lava_hip_set_kernel_override", family, choice)
+
+
+def release_workspaces() -> None:
+    """Free the library's workspaces (waits for the device first)."""
+    call("lava_hip_release_workspaces")

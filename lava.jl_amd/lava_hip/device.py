@@ -180,6 +180,53 @@ class Event:
             pass
 
 
+class Graph:
+    """A HIP graph captured from the library's calls on a (non-NULL) stream:
+
+        g = Graph(stream)
+        with g.capture():
+            gemm(C, A, B, stream=stream.handle)
+        g.launch()
+
+    Capture is in global mode, so an allocating call anywhere in the process fails while it runs."""
+
+    def __init__(self, stream: Stream):
+        self.stream = stream
+        self.handle = None
+
+    def capture(self):
+        graph = self
+
+        class _Capture:
+            def __enter__(self_):
+                _lib.call("lava_hip_graph_capture_begin", graph.stream.handle)
+                return graph
+
+            def __exit__(self_, exc_type, exc, tb):
+                e = C.c_void_p()
+                status = _lib.load().lava_hip_graph_capture_end(graph.stream.handle, C.byref(e))
+                graph.handle = e.value
+                if exc_type is None:
+                    _lib.check(status)
+                return False
+
+        return _Capture()
+
+    def launch(self, stream: Stream | None = None) -> None:
+        _lib.call("lava_hip_graph_launch", self.handle, (stream or self.stream).handle)
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.call("lava_hip_graph_destroy", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def synchronize() -> None:
     _lib.call("lava_hip_synchronize")
 

@@ -67,3 +67,28 @@ def announce(msg: str) -> None:
 @pytest.fixture
 def rng():
     return np.random.default_rng(12345)
+
+
+def _pinned_gemm(gpu, choice, name):
+    gpu.set_kernel_override(gpu.FAMILY_GEMM, choice)
+    gpu.kernel_log_clear()
+    try:
+        yield
+        log = gpu.kernel_log()
+    finally:
+        gpu.set_kernel_override(gpu.FAMILY_GEMM, 0)
+    assert name in log, f"expected {name} in the kernel log, got {log}"
+
+
+@pytest.fixture
+def tile_kernel(gpu):
+    """Runs a test's GEMMs on the 256 x 256 tile kernel (pinned with lava_hip_set_kernel_override,
+    so that the rate rule cannot move them to another kernel) and checks afterwards, through the
+    library's kernel log, that it ran."""
+    yield from _pinned_gemm(gpu, 1, "gemm_tn_kernel")
+
+
+@pytest.fixture
+def staged_kernel(gpu):
+    """As tile_kernel, for the staged (any-layout, bounds-predicated) kernel."""
+    yield from _pinned_gemm(gpu, 3, "gemm_staged_kernel")

@@ -91,7 +91,12 @@ def test_gemm_small_products(gpu, oracle, layout, dt, shape):
     acc = "i32" if dt == "i8" else "f32"
     C = lh.HIPDeviceArray(acc, (M, N), order="C" if layout & 4 else "F")
     C.fill_bytes(0xFF)
+    lh.kernel_log_clear()
     lh.gemm(C, A, B)
+    # the 64 x 64 kernel, or the staged one where an M/N-contiguous operand's extent splits a
+    # 16-byte chunk (int8 A column-major with M = 520): never the 256 x 256 tile kernel
+    log = lh.kernel_log()
+    assert "gemm_small_kernel" in log or "gemm_staged_kernel" in log, log
     rows = np.unique(np.concatenate([np.arange(0, M, 7), [M - 1]]))
     check_rows(oracle, dt, A, B, C, rows, layout)
 
@@ -159,7 +164,7 @@ def test_gemm_tn_full_size(gpu, oracle, dt, n):
 
 @pytest.mark.parametrize("layout", range(8))
 @pytest.mark.parametrize("shape", [(2048, 1536, 1024), (1280, 1024, 640), (1296, 1040, 528)])
-def test_gemm_i8_tile_kernel_layouts(gpu, oracle, layout, shape):
+def test_gemm_i8_tile_kernel_layouts(gpu, oracle, tile_kernel, layout, shape):
     """int8 on the tile kernel in every operand layout: M/N-contiguous operands staged as
     [k][m] and read through ds_read_b64_tr_b8 (whole tiles; ragged M and N; ragged K).
     Bit-exact on sampled rows."""

@@ -65,21 +65,21 @@ def run_case(lh, oracle, ab, d, M, N, K, layout, act, with_bias, with_res, seed)
 @pytest.mark.parametrize("act", ACTS)
 @pytest.mark.parametrize("d", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("ab", ["f16", "bf16"])
-def test_gemm_ex_tn_bias_residual(gpu, oracle, ab, d, act):
+def test_gemm_ex_tn_bias_residual(gpu, oracle, tile_kernel, ab, d, act):
     """The fast kernel with both accumulator-init terms, every output type and activation."""
     announce(f"gemm_ex TN {ab}->{d} act={act} bias+residual")
     run_case(gpu, oracle, ab, d, 256, 512, 256, 1 | 4, act, True, True, 3000)
 
 
 @pytest.mark.parametrize("with_bias,with_res", [(False, False), (True, False), (False, True)])
-def test_gemm_ex_tn_init_terms(gpu, oracle, with_bias, with_res):
+def test_gemm_ex_tn_init_terms(gpu, oracle, tile_kernel, with_bias, with_res):
     """Each accumulator-init term alone (and neither: a plain GEMM narrowed to bf16)."""
     announce(f"gemm_ex TN bias={with_bias} residual={with_res}")
     run_case(gpu, oracle, "bf16", "bf16", 512, 256, 384, 1 | 4, "gelu_tanh", with_bias, with_res, 3100)
 
 
 @pytest.mark.parametrize("d", ["f32", "bf16"])
-def test_gemm_ex_column_major_d(gpu, oracle, d):
+def test_gemm_ex_column_major_d(gpu, oracle, tile_kernel, d):
     """D column-major: computed as D^T by the TN kernel, the per-row bias then runs
     along the kernel's columns and the residual is read transposed."""
     announce(f"gemm_ex column-major D -> {d}")
@@ -87,7 +87,7 @@ def test_gemm_ex_column_major_d(gpu, oracle, d):
 
 
 @pytest.mark.parametrize("layout", range(8))
-def test_gemm_ex_staged_ragged(gpu, oracle, layout):
+def test_gemm_ex_staged_ragged(gpu, oracle, staged_kernel, layout):
     """Ragged extents, every layout: the staged kernel with the epilogue and bounds."""
     announce(f"gemm_ex staged ragged layout={layout}")
     run_case(gpu, oracle, "f16", "f16", 100, 70, 50, layout, "gelu_erf", True, True, 3300 + 10 * layout)

@@ -6,7 +6,8 @@ tensor read the clamp value (zero by default) and the clamping store writes only
 the elements inside it (src/device/tensor_intrinsics.jl, `lava_tensor_store`).
 Here A row-major and B column-major with any M and N, and K a multiple of the
 16-byte chunk, take the 256 x 256 TN kernel: out-of-range lanes read zero, the
-store is bounds-checked.  Checked:
+store is bounds-checked.  These tests pin the tile kernel (the dispatch rule sends
+some of these shapes to the small-product kernel) and check that it ran.  Checked:
   * every row (or, for the larger shapes, edge rows plus a sample) against the
     oracle: rel. Frobenius <= 1e-3 for f16/bf16, bit-exact for int8;
   * C with padded rows (ldc > N, not a multiple of 4 -> element stores) and guard
@@ -59,7 +60,7 @@ def check(oracle, dt, got, A, B, M, N, K, lda, ldb, rows):
 @pytest.mark.parametrize("crow", [True, False])
 @pytest.mark.parametrize("dt,shape", [("f16", s) for s in SHAPES_16] + [("bf16", s) for s in SHAPES_16[:4]]
                          + [("i8", s) for s in SHAPES_I8])
-def test_tn_ragged(gpu, oracle, dt, shape, crow):
+def test_tn_ragged(gpu, oracle, tile_kernel, dt, shape, crow):
     """A row-major, B column-major; C row-major (the TN kernel as is) or column-major
     (computed as C^T = B^T A^T, so the ragged extents swap roles)."""
     lh = gpu
@@ -77,7 +78,7 @@ def test_tn_ragged(gpu, oracle, dt, shape, crow):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "i8"])
-def test_tn_ragged_store_stays_inside(gpu, oracle, dt):
+def test_tn_ragged_store_stays_inside(gpu, oracle, tile_kernel, dt):
     """C row-major with ldc = N + 3 (rows not 16-byte aligned: element stores) inside a
     buffer with two guard rows: the padding columns and the guard rows keep their bytes."""
     lh = gpu
@@ -101,7 +102,7 @@ def test_tn_ragged_store_stays_inside(gpu, oracle, dt):
 
 
 @pytest.mark.parametrize("d,crow", [("bf16", True), ("f16", False), ("f32", True)])
-def test_tn_ragged_epilogue(gpu, oracle, d, crow):
+def test_tn_ragged_epilogue(gpu, oracle, tile_kernel, d, crow):
     """bias + residual + gelu_tanh on a ragged TN shape, narrowed to D's type."""
     lh = gpu
     M, N, K = 515, 389, 136
@@ -132,7 +133,7 @@ LAYOUT_SHAPES = [(512, 768, 256), (1000, 776, 520), (264, 1032, 8), (2048, 256, 
 @pytest.mark.parametrize("shape", LAYOUT_SHAPES)
 @pytest.mark.parametrize("layout", range(8))
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-def test_tile_kernel_every_layout(gpu, oracle, dt, layout, shape):
+def test_tile_kernel_every_layout(gpu, oracle, tile_kernel, dt, layout, shape):
     """16-bit operands in all 8 layouts at sizes the 256 x 256 tile kernel takes: a
     K-contiguous operand (A row-major, B column-major) is read directly, an M/N-contiguous
     one (A column-major, B row-major) through transposing LDS reads; column-major C swaps
@@ -156,7 +157,7 @@ def test_tile_kernel_every_layout(gpu, oracle, dt, layout, shape):
 
 
 @pytest.mark.parametrize("layout", [0, 2, 3, 6])
-def test_tile_kernel_layouts_epilogue(gpu, oracle, layout):
+def test_tile_kernel_layouts_epilogue(gpu, oracle, tile_kernel, layout):
     """The fused epilogue on the M/N-contiguous forms (bias + residual + gelu, bf16 out)."""
     lh = gpu
     M, N, K = 520, 784, 264
@@ -182,7 +183,7 @@ def test_tile_kernel_layouts_epilogue(gpu, oracle, layout):
 
 
 @pytest.mark.parametrize("layout", range(8))
-def test_tile_kernel_padded_leading_dims(gpu, oracle, layout):
+def test_tile_kernel_padded_leading_dims(gpu, oracle, tile_kernel, layout):
     """Leading dimensions larger than the extents (every operand padded by 8 elements,
     C by 4): the tile kernel's operand forms address through lda / ldb / ldc, and the
     padding of C is not written."""

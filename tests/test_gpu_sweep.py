@@ -38,7 +38,7 @@ def _gemm_cases():
     for _ in range(96):
         dt = str(rng.choice(["f16", "bf16", "i8"]))
         layout = int(rng.integers(0, 8))
-        big = rng.random() < 0.3          # past 256 x 256: the tile kernel, ragged or not
+        big = rng.random() < 0.3          # past 256 x 256: the tile or the small kernel (rate rule)
         M = _dim(rng, 1, 700 if big else 300)
         N = _dim(rng, 1, 700 if big else 300)
         K = _dim(rng, 1, 600)

@@ -265,6 +265,15 @@ def test_w8a16_column_major_generic(gpu, oracle):
 
 
 # ------------------------------------------------------------------ attention
+@pytest.fixture
+def so_kernel(gpu):
+    """Checks, after the test, that its calls ran on the score/output kernel (flash_fwd5_kernel),
+    through the library's kernel log."""
+    gpu.kernel_log_clear()
+    yield
+    assert "flash_fwd5_kernel" in gpu.kernel_log(), gpu.kernel_log()
+
+
 def attn_inputs(lh, E, L, H, B, cfg=4):
     Q, K, V = (lh.HIPDeviceArray("f16", (E, L, H, B)) for _ in range(3))
     for t, a in enumerate((Q, K, V)):
@@ -289,7 +298,7 @@ def check_heads(oracle, Q, K, V, O, scale, causal, heads, rows):
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("E,L,H,B", [(128, 128, 1, 1), (128, 512, 3, 2), (128, 1024, 2, 1)])
-def test_flash_fast_path(gpu, oracle, causal, E, L, H, B):
+def test_flash_fast_path(gpu, oracle, so_kernel, causal, E, L, H, B):
     lh = gpu
     announce(f"flash fwd D={E} S={L} H={H} B={B} causal={causal}")
     Q, K, V = attn_inputs(lh, E, L, H, B)
@@ -301,7 +310,7 @@ def test_flash_fast_path(gpu, oracle, causal, E, L, H, B):
 
 
 @pytest.mark.parametrize("H,B", [(4, 2), (8, 3), (8, 4), (5, 1)])
-def test_flash_causal_block_orders(gpu, oracle, H, B):
+def test_flash_causal_block_orders(gpu, oracle, so_kernel, H, B):
     """Causal workgroup orders: B * H = 8 (one head per XCD), 24 (three per XCD, no
     4-head groups), 32 (groups of 4 heads), 5 (no split by XCD); every head's rows."""
     lh = gpu
@@ -317,22 +326,27 @@ def test_flash_causal_block_orders(gpu, oracle, H, B):
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("L", [128, 777, 1024])
-def test_flash_pingpong_kernel_d128(gpu, oracle, causal, L, monkeypatch):
-    """D = 128 on the ping-pong kernel (LAVA_HIP_ATTN_KERNEL=3; the default D = 128 path
-    is the score/output split kernel), including a ragged S."""
+def test_flash_pingpong_kernel_d128(gpu, oracle, causal, L):
+    """D = 128 on the ping-pong kernel (pinned with lava_hip_set_kernel_override; the default
+    D = 128 path is the score/output split kernel), including a ragged S."""
     lh = gpu
-    monkeypatch.setenv("LAVA_HIP_ATTN_KERNEL", "3")
     announce(f"flash fwd ping-pong kernel D=128 S={L} causal={causal}")
     Q, K, V = attn_inputs(lh, 128, L, 2, 1)
     O = lh.HIPDeviceArray("f16", (128, L, 2, 1))
     O.fill_bytes(0xFF)
-    lh.flash_attn_fwd(O, Q, K, V, causal=causal)
+    lh.set_kernel_override(lh.FAMILY_ATTN, 3)
+    lh.kernel_log_clear()
+    try:
+        lh.flash_attn_fwd(O, Q, K, V, causal=causal)
+        assert lh.kernel_log() == ["flash_fwd3_kernel"], lh.kernel_log()
+    finally:
+        lh.set_kernel_override(lh.FAMILY_ATTN, 0)
     check_heads(oracle, Q, K, V, O, 1 / math.sqrt(128), causal, [(0, 0), (0, 1)], np.arange(L))
 
 
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("L", [1, 7, 100, 255, 257, 1000, 1537])
-def test_flash_fast_ragged_s(gpu, oracle, causal, L):
+def test_flash_fast_ragged_s(gpu, oracle, so_kernel, causal, L):
     """D = 128 with S not a multiple of the 256-query block: the fast kernel zero-fills the
     K/V rows past S (offsets beyond the buffer resource), masks their scores, computes the
     queries past S on zeros and does not store them.  Every row of every head up to S = 257,
@@ -430,7 +444,7 @@ def test_flash_d256_nonpositive_scale(gpu, oracle, causal):
 
 @pytest.mark.parametrize("E,L,causal", [(32, 200, True), (16, 32, True), (96, 130, False), (48, 100, False),
                                          (8, 257, True), (120, 300, False), (80, 512, True), (96, 1000, True)])
-def test_flash_padded_head_dims(gpu, oracle, E, L, causal):
+def test_flash_padded_head_dims(gpu, oracle, so_kernel, E, L, causal):
     """Head dimensions below 128 (multiples of 8) on the score/output kernel, zero-padded to
     128: the padding columns of Q and K read zero and add nothing to the scores; those of O
     are not written."""
@@ -445,7 +459,7 @@ def test_flash_padded_head_dims(gpu, oracle, E, L, causal):
     assert not np.isnan(O.to_numpy()).any()
 
 
-def test_flash_golden(gpu):
+def test_flash_golden(gpu, so_kernel):
     from pathlib import Path
     lh = gpu
     announce("flash golden S=32 D=16")
@@ -457,7 +471,7 @@ def test_flash_golden(gpu):
     assert o.rel_frobenius(O.to_numpy(), g["attn_o"]) <= 2e-3
 
 
-def test_flash_full_config(gpu, oracle):
+def test_flash_full_config(gpu, oracle, so_kernel):
     """B=4, H=32, S=4096, D=128, causal, scale 1/sqrt(128).  Sampled
     heads and rows against the oracle, plus properties of every row: causal row 0
     equals v_0 exactly (up to fp16 rounding), and no element is NaN."""
@@ -481,7 +495,7 @@ def test_flash_full_config(gpu, oracle):
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("scale", [1.0, 0.6, 0.05])
 @pytest.mark.parametrize("L", [300, 512])
-def test_flash_d128_scales(gpu, oracle, causal, scale, L):
+def test_flash_d128_scales(gpu, oracle, so_kernel, causal, scale, L):
     """The D = 128 kernel folds scale * log2(e) into Q^T when it is at most 1 (0.6, 0.05:
     P = exp2 of the accumulator, the running maximum entering as a bias k-step) and
     multiplies in fp32 otherwise (1.0: scale * log2(e) = 1.44)."""
@@ -500,11 +514,11 @@ def test_flash_d128_scales(gpu, oracle, causal, scale, L):
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("scale", [0.0, -0.0883883])
 @pytest.mark.parametrize("E", [128, 64])
-def test_flash_scale_zero_and_negative(gpu, oracle, causal, scale, E):
+def test_flash_scale_zero_and_negative(gpu, oracle, so_kernel, causal, scale, E):
     """A softmax scale of zero (every visible key weighs the same) or below zero (the
-    scores change sign, so the running maximum is taken over negated products): D = 128
-    runs on the score/output kernel (the scale folds into Q^T), D = 64 on the generic
-    kernel; both against the oracle."""
+    scores change sign, so the running maximum is taken over negated products): D = 128 and
+    D = 64 (zero-padded to 128) run on the score/output kernels, whose scale folds into Q^T;
+    against the oracle."""
     lh = gpu
     L, H, B = 256, 2, 1
     announce(f"flash D={E} scale={scale} S={L} causal={causal}")
@@ -524,7 +538,7 @@ def test_flash_scale_zero_and_negative(gpu, oracle, causal, scale, E):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_flash_d128_maximum_beyond_fp16(gpu, oracle, causal):
+def test_flash_d128_maximum_beyond_fp16(gpu, oracle, so_kernel, causal):
     """Scores whose running maximum (in base-2 units) lies beyond +-60000, where the bias
     k-step cannot carry it in fp16: the wavefront switches to the fp32 path.  Scores are
     exact in fp32 (integers): q0 = k0 = 256 plus small integer parts, so every score is
@@ -579,7 +593,7 @@ def test_flash_strided_layouts(gpu, oracle, causal, E, L):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-def test_flash_o_rows_8_byte_aligned(gpu, oracle, causal):
+def test_flash_o_rows_8_byte_aligned(gpu, oracle, so_kernel, causal):
     """O with a row stride of D + 4 elements (rows 8-byte aligned only): the D = 128 kernel
     stores O rows in 8-byte pieces instead of staging whole 16-byte-aligned rows."""
     lh = gpu

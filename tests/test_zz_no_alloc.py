@@ -80,3 +80,48 @@ def test_noalloc_column_major_weights(gpu, oracle, M, xo, yo):
     ref = oracle.w8a16_rows(np.ascontiguousarray(X.to_numpy()), np.ascontiguousarray(W.to_numpy()), s.to_numpy(),
                             N, K, K, N, np.arange(M))
     assert oracle.rel_frobenius(Y_na.to_numpy(), ref) <= 1e-3
+
+
+@pytest.mark.parametrize("case", ["split", "x_copy"])
+def test_noalloc_under_graph_capture(gpu, oracle, case):
+    """The entry captured into a HIP graph on a fresh stream in global capture mode, where any
+    hipMalloc in the process fails: a split-K shape (W row-major: counters and partial blocks in
+    the fixed array) and a column-major X with M not a multiple of 8 (its row-major copy in the
+    fixed array).  The graph, replayed three times with eager calls and synchronisations between
+    the replays, gives the allocating entry's bits every time."""
+    lh = gpu
+    if case == "split":
+        M, N, K, xo, wo = 16, 4096, 4096, "C", "C"
+    else:
+        M, N, K, xo, wo = 5, 4096, 2048, "F", "F"
+    announce(f"w8a16_noalloc under graph capture: {case} M={M} N={N} K={K}")
+    X = lh.HIPDeviceArray("f16", (M, K), order=xo)
+    W = lh.HIPDeviceArray("i8", (K, N), order=wo)
+    s = lh.HIPDeviceArray("f16", (N,))
+    lh.fill_normal(X, lh_mod.seed(45, 0))
+    lh.fill_i8(W, lh_mod.seed(45, 1), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(45, 2), 0.001, 0.02)
+    Y_ref = lh.HIPDeviceArray("f32", (M, N), order="C")
+    lh.w8a16(Y_ref, X, W, s)
+    lh.synchronize()
+    ref = Y_ref.to_numpy()
+    st = lh.Stream()
+    Y = lh.HIPDeviceArray("f32", (M, N), order="C")
+    g = lh.Graph(st)
+    with g.capture():
+        lh.w8a16_noalloc(Y, X, W, s, stream=st.handle)
+    Y_eager = lh.HIPDeviceArray("f32", (M, N), order="C")
+    for rep in range(3):
+        Y.fill_bytes(0xFF)
+        lh.synchronize()
+        g.launch()
+        st.synchronize()
+        np.testing.assert_array_equal(Y.to_numpy(), ref, err_msg=f"replay {rep}")
+        lh.w8a16_noalloc(Y_eager, X, W, s)   # eager work on the same fixed array between replays
+        lh.synchronize()
+        np.testing.assert_array_equal(Y_eager.to_numpy(), ref)
+    g.close()
+    st.close()
+    want = oracle.w8a16_rows(np.ascontiguousarray(X.to_numpy()), np.ascontiguousarray(W.to_numpy()), s.to_numpy(),
+                             N, K, K, N, np.arange(M))
+    assert oracle.rel_frobenius(ref, want) <= 1e-3
