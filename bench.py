@@ -10,7 +10,8 @@ before timing starts.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
-                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|gemm_shapes|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy]
+                              gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|gemm_shapes|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy|
+                              hbm_read|gemm_u8]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -281,8 +282,43 @@ def cpu_baseline_gemm(n=8192, budget_s=20.0):
     dt = time.perf_counter() - t0
     tflops = 2.0 * rows * n * n / dt / 1e12
     return {"value": round(tflops, 5), "unit": "TFLOP/s", "cores": o.num_threads(), "kind": "port",
+            "note": CPU_NOTE,
             "sample": f"{rows} rows of C of the bf16 8192^3 GEMM (2*{rows}*8192*8192 FLOP, fp32 accumulate, "
                       f"includes decoding B), oracle/lava_oracle.c oracle_gemm_f32acc, {dt:.1f} s"}
+
+
+# what the CPU figures are (BASELINE.md asks for the Lava/lavapipe path, which cannot run on the box)
+CPU_NOTE = ("lavapipe baseline unavailable (no Julia, Mantle or Lavapipe_jll on the GPU box); not the Lava path: "
+            "the build's own CPU restatement (oracle/lava_oracle.c, OpenMP over all host threads)")
+
+
+def cpu_baseline_attn(B=4, H=32, S=4096, D=128, budget_s=10.0):
+    """The oracle's causal attention (fp64 softmax(q K^T s) V per query row, a restatement, not the
+    Lava path) on all host threads, over as many heads of the headline problem as fit the time
+    budget (at least one), all S query rows of each.  FLOP by the GPU figure's convention: a
+    head is 0.5 * 4 * S^2 * D."""
+    sys.path.insert(0, str(REPO))
+    import numpy as np
+    from oracle import oracle as o
+    n = D * S
+    st = (1, D, D * S, D * S * H)
+    rows = np.arange(S)
+    heads, dt = 0, 0.0
+    while heads == 0 or (dt / heads) * (heads + 1) <= budget_s:
+        h = heads % H
+        q, k, v = (o.fill_normal(n, "f16", 0x4C415641 + 4 * 256 + t + 16 * h) for t in range(3))
+        t0 = time.perf_counter()
+        o.attn_rows(q, k, v, S, D, (1, D, D * S, D * S), 1.0 / math.sqrt(D), True, 0, 0, rows)
+        dt += time.perf_counter() - t0
+        heads += 1
+        if heads >= B * H:
+            break
+    flop = heads * 0.5 * 4.0 * S * S * D
+    return {"value": round(flop / dt / 1e12, 6), "unit": "TFLOP/s", "cores": o.num_threads(), "kind": "port",
+            "note": CPU_NOTE,
+            "sample": f"{heads} head(s) of the causal B=4 H=32 S=4096 D=128 problem, all {S} query rows each "
+                      f"({flop:.3g} FLOP by the 0.5*4*S^2*D convention; fp64 arithmetic), "
+                      f"oracle/lava_oracle.c oracle_attn_rows, {dt:.1f} s"}
 
 
 # ---------------------------------------------------------------- main
@@ -294,7 +330,7 @@ def main():
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96", "attn_d256",
-                             "copy", "vendor_bf16", "w8a16_wrow", "w8a16_julia", "gemm_shapes"])
+                             "copy", "hbm_read", "vendor_bf16", "w8a16_wrow", "w8a16_julia", "gemm_shapes", "gemm_u8"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -446,6 +482,22 @@ def main():
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_INT8_TOPS, "TOP/s",
                                          load_traffic("gemm_i8_4096"))})
+    elif args.workload == "gemm_u8":
+        n = 4096
+        A = lh.HIPDeviceArray("u8", (n, n), order="C")
+        B = lh.HIPDeviceArray("u8", (n, n), order="F")
+        C = lh.HIPDeviceArray("u32", (n, n), order="C")
+        lh.fill_i8(A, lh.seed(2, 0))
+        lh.fill_i8(B, lh.seed(2, 1))
+        lh.synchronize()
+        kms, wms = timed(lh, lambda: lh.gemm(C, A, B, stream=stream), K, W, stream)
+        flop = 2.0 * n ** 3
+        out.update({"value": round(flop / (kms * 1e-3) / 1e12, 2), "unit": "TOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "u8", "config": {"workload": "uint8 GEMM 4096^3 -> uint32, A row-major, B column-major "
+                                                          "(signed MFMA on bytes flipped by 128, row/column-sum "
+                                                          "correction)"},
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_INT8_TOPS, "TOP/s", None)})
     elif args.workload in W8A16_WORKLOADS:
         xo, wo, yo, what, traffic_key = W8A16_WORKLOADS[args.workload]
         nbytes, kms, wms = bench_w8a16(lh, K, W, stream, x_order=xo, w_order=wo, y_order=yo)
@@ -463,6 +515,38 @@ def main():
                     "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
 
+    elif args.workload == "hbm_read":
+        # the HBM read ceiling: a tuned read-only stream (16-byte nontemporal loads, 8 in flight
+        # per thread; the launch shapes a sweep of 4 / 8 / 16 loads in flight and 448 to 16384
+        # workgroups found best), over 4 GiB, and over the W8A16 weight size (58.7 MB, 6 rotating
+        # copies: 352 MB > the 256 MB MALL)
+        nbytes = 1 << 32
+        src = lh.HIPDeviceArray("u8", (nbytes,))
+        sink = lh.HIPDeviceArray("u32", (8192 * 256,))
+        src.fill_bytes(3)
+        lh.synchronize()
+        kms, wms = timed(lh, lambda: lh._lib.call("lava_hip_read_stream", src.ptr, nbytes, sink.ptr, 8192, 8, stream),
+                         K, W, stream)
+        del src
+        wb = 4096 * 14336
+        bufs = [lh.HIPDeviceArray("u8", (wb,)) for _ in range(6)]
+        for b_ in bufs:
+            b_.fill_bytes(5)
+        lh.synchronize()
+        it = [0]
+
+        def launch_w():
+            lh._lib.call("lava_hip_read_stream", bufs[it[0] % 6].ptr, wb, sink.ptr, 448, 8, stream)
+            it[0] += 1
+
+        wms_k, _ = timed(lh, launch_w, K, W, stream, group=SHORT_GROUP)
+        out.update({"value": round(nbytes / (kms * 1e-3) / 1e9, 1), "unit": "GB/s", "ms_per_step": round(wms, 4),
+                    "dtype": "u8", "config": {"workload": "HBM read stream of 4 GiB (read bytes; 16-byte "
+                                                          "nontemporal loads, 8 per thread in flight, 8192 x 256 threads)"},
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
+                    "w8a16_size": {"bytes": wb, "copies": 6, "us": round(wms_k * 1e3, 2),
+                                   "GBs": round(wb / (wms_k * 1e-3) / 1e9, 1), "launch": "448 x 256 threads"},
+                    "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s", nbytes)})
     elif args.workload == "copy":
         # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain 1 GiB device copy
         nbytes = 1 << 30
@@ -486,6 +570,8 @@ def main():
 
     if args.workload in ("headline", "gemm_bf16") and not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline_gemm()
+    if args.workload in ("headline", "attn") and not args.no_cpu_baseline:
+        (out["attn_fwd"] if args.workload == "headline" else out)["cpu_baseline"] = cpu_baseline_attn()
     print(json.dumps(out), flush=True)
 
 

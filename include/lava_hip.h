@@ -64,7 +64,7 @@ extern "C" {
 #define LAVA_HIP_REDUCE_ROW 1u
 #define LAVA_HIP_REDUCE_COLUMN 2u
 #define LAVA_HIP_REDUCE_ROW_AND_COLUMN 3u
-#define LAVA_HIP_REDUCE_TWO_BY_TWO 4u /* declared by the reference, unverified there: unsupported */
+#define LAVA_HIP_REDUCE_TWO_BY_TWO 4u /* 2 x 2 blocks (lava_hip_coopmat_reduce_into); unverified in the reference */
 
 /* reduce combiners */
 #define LAVA_HIP_COMBINE_ADD 0
@@ -142,6 +142,13 @@ void lava_hip_kernel_log_clear(void);
  *  LAVA_HIP_FAMILY_GEMM: 1 the 256 x 256 tile kernel, 2 the 64 x 64 small-product kernel
  *                        without a K split, 3 the staged kernel.
  * Unknown families or choices return LAVA_HIP_ERR_INVALID_ARG. */
+/* Reads [src, src + bytes) once with 16-byte nontemporal loads, `unroll` (4, 8 or 16) in flight
+ * per thread, `blocks` workgroups of 256 threads, and writes the XOR of what each thread read to
+ * sink[thread] (sink holds blocks * 256 words): the HBM read bandwidth the part sustains, the
+ * ceiling the W8A16 weight stream is measured against.  src 16-byte aligned, bytes a multiple
+ * of 16. */
+int lava_hip_read_stream(const void* src, size_t bytes, uint32_t* sink, int blocks, int unroll, void* stream);
+
 #define LAVA_HIP_FAMILY_ATTN 1
 #define LAVA_HIP_FAMILY_GEMM 2
 int lava_hip_set_kernel_override(int family, int choice);
@@ -212,6 +219,22 @@ int lava_hip_coopmat_perelement_pair(const float* m, const float* o, float* out,
  * (src/device/coopmat_intrinsics.jl:685-755).  combine: LAVA_HIP_COMBINE_*. */
 int lava_hip_coopmat_reduce(const float* in, float* out, int tile, uint32_t mask, int combine, int64_t ntiles,
                             void* stream);
+
+/* coopmat_reduce into a destination of another extent -- coopmat2's flexible dimensions, which
+ * the reference's flash form uses to resize a Br x Bc matrix to Br x HSV_pad with
+ * smearReduce(x, y) = x (src/device/coopmat_intrinsics.jl:685-720;
+ * src/vocabulary/coopmat.jl:289-312).  m: fp32 tile x tile Accumulators (tile 16 or 32);
+ * Dst: fp32 dst_rows x dst_cols; both column-major in memory, ntiles of each consecutive.
+ *   Row (1):          dst_rows == tile, dst_cols 16, 32 or 64: Dst[r][c] = combination of row r;
+ *   Column (2):       dst_cols == tile, dst_rows 16, 32 or 64: Dst[r][c] = combination of column c;
+ *   RowAndColumn (3): dst_rows, dst_cols 16, 32 or 64: every element the combination of all of m;
+ *   TwoByTwo (4):     dst = tile / 2 x tile / 2, Dst[i][j] = f(f(m[2i][2j], m[2i][2j+1]),
+ *                     f(m[2i+1][2j], m[2i+1][2j+1])), the 2 x 2 block reduce of the published
+ *                     SPV_NV_cooperative_matrix2 extension, in that order (the reference declares
+ *                     the bit, src/vocabulary/coopmat.jl:289-297, and calls it unverified).
+ * Other destination shapes return LAVA_HIP_ERR_INVALID_ARG. */
+int lava_hip_coopmat_reduce_into(const float* in, float* out, int tile, int dst_rows, int dst_cols, uint32_t mask,
+                                 int combine, int64_t ntiles, void* stream);
 
 /* convert(AcceleratedMatrix{T,...}, m) of fp32 tiles to F16 or BF16, RNE
  * (src/vocabulary/coopmat.jl:178-182; src/compiler/passes/exact_narrowing.jl:31-36).
@@ -375,6 +398,16 @@ int lava_hip_gemm_bf16_f32(const void* A, const void* B, void* C, int64_t M, int
 /* int8 x int8 -> int32, all operands signed (src/compiler/spirv/coopmat.jl:115-151),
  * exact with two's-complement wrap of the 32-bit accumulator. */
 int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                         int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
+
+/* uint8 x uint8 -> uint32, all operands unsigned (src/compiler/spirv/coopmat.jl:115-151 emits no
+ * signed-component bits for UInt8 coopmats; test/spirv/test_coopmat_int8.jl:71-98), exact with
+ * the 32-bit accumulator's wrap; C holds uint32.  The MFMA is signed only: the tile kernel
+ * multiplies the bytes flipped by 128 (u - 128) and adds 128 (row sum + column sum) + 16384 K
+ * back in its epilogue.  Shapes the tile kernel does not take (fewer than 256 x 256 outputs, a
+ * K-contiguous K or an M/N-contiguous M/N not a multiple of 16, 16-byte misaligned operands) run
+ * on a one-thread-per-element kernel.  Same layouts and leading-dimension rules as above. */
+int lava_hip_gemm_u8_u32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
 
 /* The coopmat2 (tensor-addressed, workgroup-scope) GEMM: C = fp16(A B), fp32 accumulate.

@@ -12,6 +12,8 @@
 // kernel.
 #include <hip/hip_runtime.h>
 
+#include <utility>
+
 #include "gemm_kernels.hpp"
 #include "lava_hip_internal.hpp"
 
@@ -88,6 +90,51 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     return launch_gemm_staged<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
 }
 
+// C = A B over unsigned bytes, uint32 accumulate (wrapping): the tile kernel in its U8 mode for
+// the shapes it takes, otherwise one thread per element of C.
+int gemm_u8_entry(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                  int64_t ldc, uint32_t layout, void* stream) {
+    const char* name = "gemm_u8_u32";
+    LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative extent (M=%lld N=%lld K=%lld)", name, (long long)M,
+             (long long)N, (long long)K);
+    LAVA_ARG(layout <= 7u, "%s: layout %u has bits beyond A/B/C row-major", name, layout);
+    if (M == 0 || N == 0) return LAVA_HIP_OK;
+    LAVA_ARG(C != nullptr, "%s: null C", name);
+    LAVA_ARG(K == 0 || (A != nullptr && B != nullptr), "%s: null A or B", name);
+    bool arow = layout & 1u, brow = layout & 2u;
+    const bool crow = layout & 4u;
+    const int64_t k1 = K > 0 ? K : 1;
+    LAVA_ARG(lda >= (arow ? k1 : M), "%s: lda = %lld is smaller than %s", name, (long long)lda, arow ? "K" : "M");
+    LAVA_ARG(ldb >= (brow ? N : k1), "%s: ldb = %lld is smaller than %s", name, (long long)ldb, brow ? "N" : "K");
+    LAVA_ARG(ldc >= (crow ? N : M), "%s: ldc = %lld is smaller than %s", name, (long long)ldc, crow ? "N" : "M");
+    LAVA_ARG(aligned(C, 4), "%s: C not aligned to 4 bytes", name);
+    LAVA_REQUIRE((M * N + 255) / 256 <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "%s: problem too large", name);
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    hipStream_t s = as_stream(stream);
+    if (K > 0) {
+        const int8_t* a = static_cast<const int8_t*>(A);
+        const int8_t* b = static_cast<const int8_t*>(B);
+        int64_t m = M, n = N, la = lda, lb = ldb;
+        bool ar = arow, br = brow;
+        if (!crow) {   // C^T = B^T A^T, row-major
+            std::swap(a, b);
+            std::swap(m, n);
+            std::swap(la, lb);
+            const bool t = ar;
+            ar = !br;
+            br = !t;
+        }
+        const int fit = kernel_override(LAVA_HIP_FAMILY_GEMM) == 3
+                            ? TN_NO
+                            : tn_gemm_eligible<int8_t>(a, b, C, m, n, K, la, lb, ldc, sizeof(int32_t), ar, !br);
+        if (fit != TN_NO)
+            return launch_gemm_tn_u8(a, b, static_cast<int32_t*>(C), m, n, K, la, lb, ldc, s, fit == TN_RAGGED, ar, !br);
+    }
+    return launch_gemm_u8_generic(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B),
+                                  static_cast<uint32_t*>(C), M, N, K, lda, ldb, ldc, layout, s);
+}
+
 template <typename T, typename OutT>
 int gemm_ex_entry(const void* A, const void* B, void* D, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                   int64_t ldd, uint32_t layout, const float* bias, const float* residual, int64_t ldr, int act,
@@ -123,6 +170,11 @@ int lava_hip_gemm_bf16_f32(const void* A, const void* B, void* C, int64_t M, int
 int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
     return gemm_entry<int8_t>("gemm_i8_i32", A, B, C, M, N, K, lda, ldb, ldc, layout, stream);
+}
+
+int lava_hip_gemm_u8_u32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                         int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
+    return gemm_u8_entry(A, B, C, M, N, K, lda, ldb, ldc, layout, stream);
 }
 
 int lava_hip_gemm_ex(int ab_dtype, int d_dtype, const void* A, const void* B, void* D, int64_t M, int64_t N,

@@ -472,6 +472,30 @@ LAVA_STAGED_INST(bf16, f16, true)
 LAVA_STAGED_INST(bf16, bf16, true)
 #undef LAVA_STAGED_INST
 
+// Unsigned bytes, any shape and layout: one thread per element of C, uint32 sums (wrapping, as
+// the cooperative-matrix integer accumulator does).
+__global__ void __launch_bounds__(256) gemm_u8_generic_kernel(const uint8_t* __restrict__ A,
+                                                              const uint8_t* __restrict__ B, uint32_t* __restrict__ C,
+                                                              int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
+                                                              int64_t ldc, uint32_t layout) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= M * N) return;
+    const bool arow = layout & 1u, brow = layout & 2u, crow = layout & 4u;
+    const int64_t m = idx / N, n = idx % N;
+    uint32_t acc = 0;
+    for (int64_t k = 0; k < K; ++k)
+        acc += (uint32_t)A[arow ? m * lda + k : k * lda + m] * (uint32_t)B[brow ? k * ldb + n : n * ldb + k];
+    C[crow ? m * ldc + n : n * ldc + m] = acc;
+}
+
+int launch_gemm_u8_generic(const uint8_t* A, const uint8_t* B, uint32_t* C, int64_t M, int64_t N, int64_t K,
+                           int64_t lda, int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s) {
+    hipLaunchKernelGGL(gemm_u8_generic_kernel, dim3((unsigned)((M * N + 255) / 256)), dim3(256), 0, s, A, B, C, M, N,
+                       K, lda, ldb, ldc, layout);
+    LAVA_LAUNCH_CHECK("gemm_u8_generic_kernel");
+    return LAVA_HIP_OK;
+}
+
 int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s) {
     const int64_t waves = (M / 16) * (N / 16);

@@ -62,5 +62,12 @@ int tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int
 template <typename T, typename OutT, bool EPI>
 int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                    int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged, bool ak, bool bk);
+// Unsigned bytes x unsigned bytes -> uint32 (wrapped) on the tile kernel: signed MFMAs on the
+// bytes flipped by 128, corrected by the row and column sums (gemm_tn_kernel.hpp).
+int launch_gemm_tn_u8(const int8_t* A, const int8_t* B, int32_t* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                      int64_t ldb, int64_t ldc, hipStream_t s, bool ragged, bool ak, bool bk);
+// Any shape and layout: one thread per element of C, bytes widened and summed in uint32.
+int launch_gemm_u8_generic(const uint8_t* A, const uint8_t* B, uint32_t* C, int64_t M, int64_t N, int64_t K,
+                           int64_t lda, int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s);
 
 }  // namespace lava

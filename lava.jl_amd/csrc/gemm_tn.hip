@@ -13,8 +13,30 @@ LAVA_TN_LAYOUT_EXTERN(int8_t, int32_t, false, false, true)
 LAVA_TN_LAYOUT_EXTERN(int8_t, int32_t, false, true, false)
 LAVA_TN_LAYOUT_EXTERN(int8_t, int32_t, false, false, false)
 
+LAVA_TN_LAYOUT_U8_EXTERN(false, true)
+LAVA_TN_LAYOUT_U8_EXTERN(true, false)
+LAVA_TN_LAYOUT_U8_EXTERN(false, false)
+
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_INST, true, true)
 LAVA_TN_LAYOUT_INST(int8_t, int32_t, false, true, true)
+LAVA_TN_LAYOUT_U8_INST(true, true)
+
+// The unsigned 8-bit product on the tile kernel (bytes in int8_t storage), any operand form.
+int launch_gemm_tn_u8(const int8_t* A, const int8_t* B, int32_t* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                      int64_t ldb, int64_t ldc, hipStream_t s, bool ragged, bool ak, bool bk) {
+    const Epilogue none{};
+    if (ak && bk)
+        return launch_gemm_tn_layout<int8_t, int32_t, false, true, true, true>(A, B, C, M, N, K, lda, ldb, ldc, s, none,
+                                                                                ragged);
+    if (!ak && bk)
+        return launch_gemm_tn_layout<int8_t, int32_t, false, false, true, true>(A, B, C, M, N, K, lda, ldb, ldc, s, none,
+                                                                                 ragged);
+    if (ak && !bk)
+        return launch_gemm_tn_layout<int8_t, int32_t, false, true, false, true>(A, B, C, M, N, K, lda, ldb, ldc, s, none,
+                                                                                 ragged);
+    return launch_gemm_tn_layout<int8_t, int32_t, false, false, false, true>(A, B, C, M, N, K, lda, ldb, ldc, s, none,
+                                                                              ragged);
+}
 
 template <typename T, typename OutT, bool EPI>
 int launch_gemm_tn(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,

@@ -240,10 +240,20 @@ struct TnSide<int8_t, false> {
 // register-file bytes per flop), and its fragments (16 rows x 64 bytes of K per k-step)
 // let the whole stage be read by the middle of the k-tile, so that the barrier sits there
 // and each DMA gets a full k-tile to land.
-template <typename T, typename OutT, bool EPI, bool RAGGED, bool AK, bool BK>
+//
+// U8 (T = int8_t storage holding unsigned bytes, int32 C holding the uint32 product): the MFMA is
+// signed only, so each fragment's bytes are flipped to s = u - 128 (XOR 0x80) before the first
+// MFMA that reads it, and the lane adds its fragments' signed bytes (v_dot4 against ones) into
+// per-row and per-column sums RA, CB.  Per k position u_a u_b = s_a s_b + 128 (s_a + s_b) + 16384,
+// so C = A_s B_s + 128 (RA[m] + CB[n]) + 16384 Kp, all modulo 2^32 -- exactly the uint32-wrapped
+// unsigned product.  Kp counts every k position the kernel accumulated, the zero padding of a
+// ragged K too: a padded position has u = 0, s = -128 on both sides and adds 16384 - 32768 +
+// 16384 = 0 to the identity.
+template <typename T, typename OutT, bool EPI, bool RAGGED, bool AK, bool BK, bool U8 = false>
 __global__ void __launch_bounds__(256, 1)
     gemm_tn16_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
                      int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi, TnBounds bnd) {
+    static_assert(!U8 || (std::is_same<T, int8_t>::value && !EPI), "U8: bytes in int8_t storage, plain int32 output");
     using AccV = typename Mfma16<T>::acc_t;
     typedef typename Mfma16<T>::acc_elem Acc;
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TN_SLICE];  // [stage][A,B][32 KB]
@@ -334,6 +344,28 @@ __global__ void __launch_bounds__(256, 1)
         rd16(fa, smem, 0, t);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // U8: signed-byte sums of this wavefront's A rows (ra[i]: row 16 i + lane % 16 of its 128) and
+    // B columns (rb[j]), over the k bytes of this lane's 16-lane group
+    int32_t ra[8], rb[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ra[i] = rb[i] = 0;
+    auto flip = [&](uint4& v, int32_t& sum) __attribute__((always_inline)) {
+        v.x ^= 0x80808080u;
+        v.y ^= 0x80808080u;
+        v.z ^= 0x80808080u;
+        v.w ^= 0x80808080u;
+        sum = __builtin_amdgcn_sdot4((int)v.x, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)v.y, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)v.z, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)v.w, 0x01010101, sum, false);
+    };
+    // before MFMA q of a k-step: the fragments it reads first (b[q] for q < 8, a[q / 8] at q % 8 == 0)
+    auto flip_for = [&](F16& f, int q) __attribute__((always_inline)) {
+        if constexpr (U8) {
+            if (q < 8) flip(f.b[q], rb[q]);
+            if ((q & 7) == 0) flip(f.a[q >> 3], ra[q >> 3]);
+        }
+    };
 
     for (int kt = 0; kt < ktiles; ++kt) {
         const int st = kt & 1;
@@ -342,6 +374,7 @@ __global__ void __launch_bounds__(256, 1)
         const uint32_t kofs2 = (uint32_t)(kt + 2 < ktiles ? kt + 2 : ktiles - 1) * TN_KB;
 #pragma unroll
         for (int q = 0; q < 64; ++q) {
+            flip_for(fa, q);
             acc[q >> 3][q & 7] = Mfma16<T>::run(fa.b[q & 7], fa.a[q >> 3], acc[q >> 3][q & 7]);
             if ((q & 3) == 3) rd16(fb, base, 1, q >> 2);
             __builtin_amdgcn_sched_barrier(0);
@@ -351,10 +384,36 @@ __global__ void __launch_bounds__(256, 1)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int q = 0; q < 64; ++q) {
+            flip_for(fb, q);
             acc[q >> 3][q & 7] = Mfma16<T>::run(fb.b[q & 7], fb.a[q >> 3], acc[q >> 3][q & 7]);
             if ((q & 3) == 1) rd16(fa, next, 0, q >> 2);
             if ((q & 3) == 3) dma(q >> 2, st, kofs2);
             __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    if constexpr (U8) {
+        // full sums: the four 16-lane groups hold the four 16-byte quarters of every k-step
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            ra[i] += __shfl_xor(ra[i], 16, 64);
+            ra[i] += __shfl_xor(ra[i], 32, 64);
+            rb[i] += __shfl_xor(rb[i], 16, 64);
+            rb[i] += __shfl_xor(rb[i], 32, 64);
+        }
+        // acc[i][j] register r: row 16 i + lane % 16 (this lane's ra[i]), column 16 j + 4 (lane / 16) + r
+        // (rb[j] of lane 4 (lane / 16) + r)
+        const uint32_t kconst = 16384u * (uint32_t)ktiles * (uint32_t)TN_KB;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t cb[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cb[r] = (uint32_t)__shfl(rb[j], 4 * (lane >> 4) + r, 64);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[i][j][r] = (int32_t)((uint32_t)acc[i][j][r] + 128u * ((uint32_t)ra[i] + cb[r]) + kconst);
         }
     }
 
@@ -501,7 +560,7 @@ int tn_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int
     return M * N >= (int64_t)TN_TILE * TN_TILE ? TN_RAGGED : TN_NO;
 }
 
-template <typename T, typename OutT, bool EPI, bool AK, bool BK>
+template <typename T, typename OutT, bool EPI, bool AK, bool BK, bool U8 = false>
 int launch_gemm_tn_layout(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                           int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged) {
     const int tiles_m = (int)((M + TN_TILE - 1) / TN_TILE), tiles_n = (int)((N + TN_TILE - 1) / TN_TILE);
@@ -514,10 +573,10 @@ int launch_gemm_tn_layout(const T* A, const T* B, OutT* C, int64_t M, int64_t N,
     bnd.cvec = ldc % 4 == 0 && aligned(C, 4 * sizeof(OutT));
     const int64_t lda_b = lda * (int64_t)sizeof(T), ldb_b = ldb * (int64_t)sizeof(T);
     if (ragged)
-        hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, true, AK, BK>), dim3((unsigned)(tiles_m * tiles_n)),
+        hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, true, AK, BK, U8>), dim3((unsigned)(tiles_m * tiles_n)),
                            dim3(256), 0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
     else
-        hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, false, AK, BK>), dim3((unsigned)(tiles_m * tiles_n)),
+        hipLaunchKernelGGL((gemm_tn16_kernel<T, OutT, EPI, false, AK, BK, U8>), dim3((unsigned)(tiles_m * tiles_n)),
                            dim3(256), 0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
     LAVA_LAUNCH_CHECK("gemm_tn_kernel");
     return LAVA_HIP_OK;
@@ -531,6 +590,15 @@ int launch_gemm_tn_layout(const T* A, const T* B, OutT* C, int64_t M, int64_t N,
     extern template int launch_gemm_tn_layout<T, O, E, AK, BK>(const T*, const T*, O*, int64_t, int64_t, int64_t,   \
                                                                int64_t, int64_t, int64_t, hipStream_t,                \
                                                                const Epilogue&, bool);
+// The unsigned 8-bit instance of one operand form (bytes in int8_t storage, uint32 product in int32).
+#define LAVA_TN_LAYOUT_U8_INST(AK, BK)                                                                              \
+    template int launch_gemm_tn_layout<int8_t, int32_t, false, AK, BK, true>(                                     \
+        const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, hipStream_t, \
+        const Epilogue&, bool);
+#define LAVA_TN_LAYOUT_U8_EXTERN(AK, BK)                                                                            \
+    extern template int launch_gemm_tn_layout<int8_t, int32_t, false, AK, BK, true>(                              \
+        const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, hipStream_t, \
+        const Epilogue&, bool);
 // The 16-bit set of one operand form: plain fp32 output, and the epilogue to fp32 / fp16 / bf16.
 #define LAVA_TN_LAYOUT_16BIT(M, AK, BK) \
     M(f16, float, false, AK, BK)        \

@@ -5,5 +5,6 @@ namespace lava {
 
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_INST, false, true)
 LAVA_TN_LAYOUT_INST(int8_t, int32_t, false, false, true)
+LAVA_TN_LAYOUT_U8_INST(false, true)
 
 }  // namespace lava

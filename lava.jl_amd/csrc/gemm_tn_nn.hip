@@ -5,5 +5,6 @@ namespace lava {
 
 LAVA_TN_LAYOUT_16BIT(LAVA_TN_LAYOUT_INST, false, false)
 LAVA_TN_LAYOUT_INST(int8_t, int32_t, false, false, false)
+LAVA_TN_LAYOUT_U8_INST(false, false)
 
 }  // namespace lava

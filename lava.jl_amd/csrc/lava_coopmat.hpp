@@ -39,7 +39,9 @@
 //                         with 0-based row/col (src/device/coopmat_intrinsics.jl:535-678)
 //   reduce                OpCooperativeMatrixReduceNV: combine along Row (1), Column
 //                         (2) or both (3); the result is smeared over the reduced
-//                         axis, not a vector (src/device/coopmat_intrinsics.jl:685-755)
+//                         axis, not a vector (src/device/coopmat_intrinsics.jl:685-755);
+//                         reduce_into: the same into a destination of another extent,
+//                         and the TwoByTwo (4) block form
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -73,7 +75,7 @@ static_assert(sizeof(f32x4) == 16 && alignof(f32x4) == 16, "<4 x float> in LDS: 
 enum Use { MatrixA = 0, MatrixB = 1, Accumulator = 2 };
 
 // CoopMatReduce masks (src/vocabulary/coopmat.jl:292-297)
-enum ReduceMask : uint32_t { ReduceRow = 1u, ReduceColumn = 2u, ReduceRowAndColumn = 3u };
+enum ReduceMask : uint32_t { ReduceRow = 1u, ReduceColumn = 2u, ReduceRowAndColumn = 3u, ReduceTwoByTwo = 4u };
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
@@ -108,6 +110,27 @@ struct Layout<16, 16, Accumulator> {
     static constexpr int len = 4;
     __host__ __device__ static constexpr int row(int lane, int j) { return 4 * (lane / 16) + j; }
     __host__ __device__ static constexpr int col(int lane, int) { return lane % 16; }
+};
+
+// Accumulators of other extents (coopmat2's flexible dimensions, used by a reduce into a
+// destination of another shape): R x C with R and C multiples of 16, as (R / 16) x (C / 16)
+// sub-tiles of the 16 x 16 map in row-major order -- slot j is sub-tile j / 4, row
+// 4 (lane / 16) + j % 4 and column lane % 16 within it.  (32 x 32 keeps the 32x32x16 MFMA's map.)
+template <int R, int C>
+struct Layout<R, C, Accumulator> {
+    static_assert(R % 16 == 0 && C % 16 == 0 && R >= 16 && C >= 16, "Accumulator extents are multiples of 16");
+    static constexpr int tc = C / 16;
+    static constexpr int len = R * C / 64;
+    __host__ __device__ static constexpr int row(int lane, int j) { return 16 * ((j / 4) / tc) + 4 * (lane / 16) + j % 4; }
+    __host__ __device__ static constexpr int col(int lane, int j) { return 16 * ((j / 4) % tc) + lane % 16; }
+};
+
+// The 8 x 8 result of a TwoByTwo reduce of a 16 x 16 tile: one element per lane.
+template <>
+struct Layout<8, 8, Accumulator> {
+    static constexpr int len = 1;
+    __host__ __device__ static constexpr int row(int lane, int) { return lane / 8; }
+    __host__ __device__ static constexpr int col(int lane, int) { return lane % 8; }
 };
 
 template <>
@@ -316,6 +339,53 @@ __device__ __forceinline__ Frag<T, R, C, Accumulator> reduce(F f, Frag<T, R, C, 
         for (int j = 0; j < Frag<T, R, C, Accumulator>::len; ++j) m.v[j] = acc;
     }
     return m;
+}
+
+// coopmat_reduce into a destination of another extent (OpCooperativeMatrixReduceNV with coopmat2
+// flexible dimensions; src/device/coopmat_intrinsics.jl:685-720: the reference's smearReduce
+// resizes a Br x Bc matrix to Br x HSV_pad).  Row: Dst has m's rows and any number of columns,
+// every column of row r holding row r's combination; Column: m's columns, any rows; RowAndColumn:
+// any extent, every element the combination of all of m; TwoByTwo: Dst is (R / 2) x (C / 2),
+// element (i, j) = f(f(m[2i][2j], m[2i][2j+1]), f(m[2i+1][2j], m[2i+1][2j+1])) -- the 2 x 2 block
+// reduce of the published SPV_NV_cooperative_matrix2 extension (the reference ships the mask bit
+// unverified), combined in that order.  The values cross lanes through `lds` (R * C elements of
+// the calling wavefront's workgroup memory); every lane of the wavefront calls it.
+template <uint32_t MASK, int RD, int CD, typename F, typename T, int R, int C>
+__device__ __forceinline__ Frag<T, RD, CD, Accumulator> reduce_into(F f, const Frag<T, R, C, Accumulator>& m,
+                                                                     T* lds) {
+    using LS = Layout<R, C, Accumulator>;
+    using LD = Layout<RD, CD, Accumulator>;
+    const int lane = lane_id();
+    Frag<T, RD, CD, Accumulator> d;
+    if constexpr (MASK == ReduceTwoByTwo) {
+        static_assert(2 * RD == R && 2 * CD == C, "a TwoByTwo reduce halves both extents");
+#pragma unroll
+        for (int j = 0; j < LS::len; ++j) lds[LS::row(lane, j) * C + LS::col(lane, j)] = m.v[j];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < LD::len; ++j) {
+            const int i = LD::row(lane, j), k = LD::col(lane, j);
+            const T* b = lds + (2 * i) * C + 2 * k;
+            d.v[j] = f(f(b[0], b[1]), f(b[C], b[C + 1]));
+        }
+    } else {
+        static_assert(MASK >= 1u && MASK <= 3u, "Row, Column, RowAndColumn or TwoByTwo");
+        static_assert((MASK & ReduceRow) == 0 || (MASK & ReduceColumn) != 0 || RD == R,
+                      "a Row reduce keeps the rows");
+        static_assert((MASK & ReduceColumn) == 0 || (MASK & ReduceRow) != 0 || CD == C,
+                      "a Column reduce keeps the columns");
+        const auto sm = reduce<MASK>(f, m);   // same shape, smeared
+#pragma unroll
+        for (int j = 0; j < LS::len; ++j) lds[LS::row(lane, j) * C + LS::col(lane, j)] = sm.v[j];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < LD::len; ++j) {
+            const int r = MASK == ReduceRow ? LD::row(lane, j) : 0;
+            const int c = MASK == ReduceColumn ? LD::col(lane, j) : 0;
+            d.v[j] = lds[r * C + c];
+        }
+    }
+    return d;
 }
 
 // ---------------------------------------------------------------------------

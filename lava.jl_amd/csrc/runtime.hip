@@ -102,6 +102,33 @@ __global__ void copy_bytes_kernel(uint8_t* __restrict__ dst, const uint8_t* __re
     }
 }
 
+// Reads [src, src + 16 n16) once -- 16-byte loads with the nontemporal hint, UNROLL of them in
+// flight per thread, the threads of a workgroup on adjacent 16-byte words in each load -- and
+// stores the XOR of everything a thread read to sink[thread], so that no load is dropped.  The
+// read bandwidth the part sustains (lava_hip_read_stream).
+typedef uint32_t rs_u32x4 __attribute__((ext_vector_type(4)));
+
+template <int UNROLL>
+__global__ void __launch_bounds__(256) read_stream_kernel(const rs_u32x4* __restrict__ src, size_t n16,
+                                                          uint32_t* __restrict__ sink) {
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t nth = (size_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
+    size_t i = tid;
+    for (; i + (UNROLL - 1) * nth < n16; i += UNROLL * nth) {
+        rs_u32x4 v[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) v[u] = __builtin_nontemporal_load(src + i + u * nth);
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += nth) {
+        const rs_u32x4 v = src[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    sink[tid] = acc;
+}
+
 }  // namespace lava
 
 using namespace lava;
@@ -267,6 +294,24 @@ int lava_hip_event_elapsed_ms(float* ms, void* start, void* stop) {
     LAVA_ARG(ms != nullptr && start != nullptr && stop != nullptr, "event_elapsed_ms: null argument");
     LAVA_HIP_TRY(hipEventSynchronize(reinterpret_cast<hipEvent_t>(stop)));
     LAVA_HIP_TRY(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(stop)));
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_read_stream(const void* src, size_t bytes, uint32_t* sink, int blocks, int unroll, void* stream) {
+    LAVA_ARG(src != nullptr && sink != nullptr, "read_stream: null pointer");
+    LAVA_ARG(aligned(src, 16) && bytes % 16 == 0, "read_stream: src must be 16-byte aligned and bytes a multiple of 16");
+    LAVA_ARG(blocks >= 1 && blocks <= 65536, "read_stream: blocks = %d outside [1, 65536]", blocks);
+    LAVA_ARG(unroll == 4 || unroll == 8 || unroll == 16, "read_stream: unroll = %d is not 4, 8 or 16", unroll);
+    const rs_u32x4* s4 = static_cast<const rs_u32x4*>(src);
+    const size_t n16 = bytes / 16;
+    hipStream_t s = as_stream(stream);
+    if (unroll == 4)
+        hipLaunchKernelGGL(read_stream_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, s4, n16, sink);
+    else if (unroll == 8)
+        hipLaunchKernelGGL(read_stream_kernel<8>, dim3((unsigned)blocks), dim3(256), 0, s, s4, n16, sink);
+    else
+        hipLaunchKernelGGL(read_stream_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, s, s4, n16, sink);
+    LAVA_LAUNCH_CHECK("read_stream_kernel");
     return LAVA_HIP_OK;
 }
 

@@ -126,6 +126,63 @@ static void launch_reduce_mask(uint32_t mask, int combine, const float* in, floa
     else launch_reduce<T, 3u>(combine, in, out, n, s);
 }
 
+// reduce into a destination of another extent: one wavefront per tile, column-major tiles in
+// memory like the same-shape form
+template <int T, uint32_t MASK, int RD, int CD, typename F>
+__global__ void __launch_bounds__(64) reduce_into_kernel(const float* in, float* out) {
+    __shared__ float lds[T * T];
+    auto m = load<Frag<float, T, T, Accumulator>>(in + (int64_t)blockIdx.x * T * T, T, false);
+    const auto d = reduce_into<MASK, RD, CD>(F{}, m, lds);
+    store(out + (int64_t)blockIdx.x * RD * CD, RD, false, d);
+}
+
+template <int T, uint32_t MASK, int RD, int CD>
+static void launch_reduce_into(int combine, const float* in, float* out, int64_t n, hipStream_t s) {
+    if (combine == LAVA_HIP_COMBINE_ADD)
+        hipLaunchKernelGGL((reduce_into_kernel<T, MASK, RD, CD, CombineAdd>), dim3((unsigned)n), dim3(64), 0, s, in, out);
+    else if (combine == LAVA_HIP_COMBINE_MAX)
+        hipLaunchKernelGGL((reduce_into_kernel<T, MASK, RD, CD, CombineMax>), dim3((unsigned)n), dim3(64), 0, s, in, out);
+    else
+        hipLaunchKernelGGL((reduce_into_kernel<T, MASK, RD, CD, CombineMin>), dim3((unsigned)n), dim3(64), 0, s, in, out);
+}
+
+// The destination extents the entry instantiates: 16, 32 or 64 along a free axis.
+template <int T, uint32_t MASK, int RD>
+static bool reduce_into_cols(int cd, int combine, const float* in, float* out, int64_t n, hipStream_t s) {
+    switch (cd) {
+    case 16: launch_reduce_into<T, MASK, RD, 16>(combine, in, out, n, s); return true;
+    case 32: launch_reduce_into<T, MASK, RD, 32>(combine, in, out, n, s); return true;
+    case 64: launch_reduce_into<T, MASK, RD, 64>(combine, in, out, n, s); return true;
+    default: return false;
+    }
+}
+
+template <int T>
+static bool launch_reduce_into_mask(uint32_t mask, int rd, int cd, int combine, const float* in, float* out, int64_t n,
+                                    hipStream_t s) {
+    if (mask == 4u) {
+        if (rd != T / 2 || cd != T / 2) return false;
+        launch_reduce_into<T, 4u, T / 2, T / 2>(combine, in, out, n, s);
+        return true;
+    }
+    if (mask == 1u) return rd == T && reduce_into_cols<T, 1u, T>(cd, combine, in, out, n, s);
+    if (mask == 2u) {
+        if (cd != T) return false;
+        switch (rd) {
+        case 16: launch_reduce_into<T, 2u, 16, T>(combine, in, out, n, s); return true;
+        case 32: launch_reduce_into<T, 2u, 32, T>(combine, in, out, n, s); return true;
+        case 64: launch_reduce_into<T, 2u, 64, T>(combine, in, out, n, s); return true;
+        default: return false;
+        }
+    }
+    switch (rd) {
+    case 16: return reduce_into_cols<T, 3u, 16>(cd, combine, in, out, n, s);
+    case 32: return reduce_into_cols<T, 3u, 32>(cd, combine, in, out, n, s);
+    case 64: return reduce_into_cols<T, 3u, 64>(cd, combine, in, out, n, s);
+    default: return false;
+    }
+}
+
 // ---- convert -------------------------------------------------------------------
 template <typename To>
 __global__ void __launch_bounds__(64) convert_kernel(const float* in, To* out) {
@@ -352,7 +409,7 @@ int lava_hip_coopmat_reduce(const float* in, float* out, int tile, uint32_t mask
                             void* stream) {
     LAVA_ARG(tile == 16 || tile == 32, "coopmat_reduce: tile = %d is not 16 or 32", tile);
     LAVA_REQUIRE(mask != LAVA_HIP_REDUCE_TWO_BY_TWO, LAVA_HIP_ERR_UNSUPPORTED,
-                 "coopmat_reduce: the TwoByTwo mask is not supported (the reference marks it unverified)");
+                 "coopmat_reduce: a TwoByTwo reduce halves both extents; use lava_hip_coopmat_reduce_into");
     LAVA_ARG(mask >= 1u && mask <= 3u, "coopmat_reduce: mask %u is not Row, Column or RowAndColumn", mask);
     LAVA_ARG(combine >= LAVA_HIP_COMBINE_ADD && combine <= LAVA_HIP_COMBINE_MIN, "coopmat_reduce: combine %d unknown",
              combine);
@@ -364,6 +421,34 @@ int lava_hip_coopmat_reduce(const float* in, float* out, int tile, uint32_t mask
     if (tile == 16) launch_reduce_mask<16>(mask, combine, in, out, ntiles, as_stream(stream));
     else launch_reduce_mask<32>(mask, combine, in, out, ntiles, as_stream(stream));
     LAVA_LAUNCH_CHECK("reduce_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_coopmat_reduce_into(const float* in, float* out, int tile, int dst_rows, int dst_cols, uint32_t mask,
+                                 int combine, int64_t ntiles, void* stream) {
+    LAVA_ARG(tile == 16 || tile == 32, "coopmat_reduce_into: tile = %d is not 16 or 32", tile);
+    LAVA_ARG(mask >= 1u && mask <= 4u, "coopmat_reduce_into: mask %u is not Row, Column, RowAndColumn or TwoByTwo",
+             mask);
+    LAVA_ARG(combine >= LAVA_HIP_COMBINE_ADD && combine <= LAVA_HIP_COMBINE_MIN,
+             "coopmat_reduce_into: combine %d unknown", combine);
+    LAVA_ARG(ntiles >= 0 && ntiles <= 0x7fffffff, "coopmat_reduce_into: ntiles out of range");
+    const bool shape_ok =
+        mask == 4u ? dst_rows == tile / 2 && dst_cols == tile / 2
+                   : (mask == 1u ? dst_rows == tile : (dst_rows == 16 || dst_rows == 32 || dst_rows == 64)) &&
+                         (mask == 2u ? dst_cols == tile : (dst_cols == 16 || dst_cols == 32 || dst_cols == 64));
+    LAVA_ARG(shape_ok,
+             "coopmat_reduce_into: destination %d x %d does not fit mask %u on %d x %d tiles (Row keeps the rows, "
+             "Column the columns, a free extent is 16, 32 or 64; TwoByTwo halves both)",
+             dst_rows, dst_cols, mask, tile, tile);
+    if (ntiles == 0) return LAVA_HIP_OK;
+    LAVA_ARG(in && out, "coopmat_reduce_into: null pointer");
+    int rc = lava_hip_init();
+    if (rc != LAVA_HIP_OK) return rc;
+    const bool ok = tile == 16
+                        ? launch_reduce_into_mask<16>(mask, dst_rows, dst_cols, combine, in, out, ntiles, as_stream(stream))
+                        : launch_reduce_into_mask<32>(mask, dst_rows, dst_cols, combine, in, out, ntiles, as_stream(stream));
+    LAVA_REQUIRE(ok, LAVA_HIP_ERR_UNSUPPORTED, "coopmat_reduce_into: no instance for this shape");
+    LAVA_LAUNCH_CHECK("reduce_into_kernel");
     return LAVA_HIP_OK;
 }
 

@@ -11,7 +11,7 @@ from .device import Event, Graph, HIPDeviceArray, Stream, device_count, synchron
 from .kernels import (coopmat_accinit_muladd, coopmat_convert, coopmat_convert_use, coopmat_convert_use_muladd,
                       coopmat_elementwise, coopmat_foreach_act, coopmat_gemm_tiles, coopmat_length,
                       coopmat_muladd_16x16x16, coopmat_perelement_pair, coopmat_perelement_rowcol,
-                      coopmat_perelement_scale, coopmat_reduce, coopmat_workgroup_gemm, dot4x8, fill_i8, fill_normal,
+                      coopmat_perelement_scale, coopmat_reduce, coopmat_reduce_into, coopmat_workgroup_gemm, dot4x8, fill_i8, fill_normal,
                       fill_uniform, flash_attn_fwd, flash_attn_fwd_raw, gemm, gemm_ex, gemm_ex_raw, gemm_raw, w8a16,
                       w8a16_noalloc, w8a16_raw)
 from .tensor import (TENSOR_CLAMP_CONSTANT, TENSOR_CLAMP_TO_EDGE, TENSOR_CLAMP_UNDEFINED, TensorLayout, TensorView,

@@ -86,6 +86,7 @@ PROTOTYPES: dict[str, tuple] = {
     "lava_hip_coopmat_perelement_rowcol": (ci, [vp, vp, ci, i64, vp]),
     "lava_hip_coopmat_perelement_pair": (ci, [vp, vp, vp, ci, i64, vp]),
     "lava_hip_coopmat_reduce": (ci, [vp, vp, ci, u32, ci, i64, vp]),
+    "lava_hip_coopmat_reduce_into": (ci, [vp, vp, ci, ci, ci, u32, ci, i64, vp]),
     "lava_hip_coopmat_convert": (ci, [vp, vp, ci, i64, vp]),
     "lava_hip_dot4x8": (ci, [vp, vp, vp, i64, vp]),
     "lava_hip_coopmat_convert_use": (ci, [vp, vp, ci, ci, ci, i64, vp]),
@@ -100,6 +101,7 @@ PROTOTYPES: dict[str, tuple] = {
     "lava_hip_gemm_f16_f32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_gemm_bf16_f32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_gemm_i8_i32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
+    "lava_hip_gemm_u8_u32": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_coopmat_gemm_f16_tiles": (ci, [vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp]),
     "lava_hip_gemm_ex": (ci, [ci, ci, vp, vp, vp, i64, i64, i64, i64, i64, i64, u32, vp, vp, i64, ci, vp]),
     "lava_hip_tensor_load_tile": (ci, [ci, ci, vp, vp, ci, vp, vp, vp]),
@@ -111,6 +113,7 @@ PROTOTYPES: dict[str, tuple] = {
     "lava_hip_flash_attn_fwd_f16": (ci, [vp, vp, vp, vp, i64, i64, i64, i64, C.POINTER(i64),
                                          C.POINTER(i64), C.c_float, ci, vp]),
     "lava_hip_release_workspaces": (ci, []),
+    "lava_hip_read_stream": (ci, [vp, C.c_size_t, vp, ci, ci, vp]),
     "lava_hip_graph_capture_begin": (ci, [vp]),
     "lava_hip_graph_capture_end": (ci, [vp, C.POINTER(vp)]),
     "lava_hip_graph_launch": (ci, [vp, vp]),

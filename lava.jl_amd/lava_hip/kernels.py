@@ -15,7 +15,7 @@ from . import _lib
 from .device import HIPDeviceArray
 
 _GEMM_ENTRY = {("f16", "f32"): "lava_hip_gemm_f16_f32", ("bf16", "f32"): "lava_hip_gemm_bf16_f32",
-               ("i8", "i32"): "lava_hip_gemm_i8_i32"}
+               ("i8", "i32"): "lava_hip_gemm_i8_i32", ("u8", "u32"): "lava_hip_gemm_u8_u32"}
 
 
 def _ld(a: HIPDeviceArray) -> int:
@@ -196,6 +196,15 @@ def coopmat_reduce(inp: int, out: int, tile: int, mask: int, combine: str, ntile
                    stream: Optional[int] = None) -> None:
     comb = {"add": _lib.COMBINE_ADD, "max": _lib.COMBINE_MAX, "min": _lib.COMBINE_MIN}[combine]
     _lib.call("lava_hip_coopmat_reduce", inp, out, tile, mask, comb, ntiles, stream)
+
+
+def coopmat_reduce_into(inp: int, out: int, tile: int, dst_rows: int, dst_cols: int, mask: int, combine: str,
+                        ntiles: int, stream: Optional[int] = None) -> None:
+    """coopmat_reduce into a destination of another extent (Row, Column, RowAndColumn smeared
+    into dst_rows x dst_cols), or the TwoByTwo block reduce into tile/2 x tile/2; column-major
+    fp32 tiles, ntiles of each."""
+    comb = {"add": _lib.COMBINE_ADD, "max": _lib.COMBINE_MAX, "min": _lib.COMBINE_MIN}[combine]
+    _lib.call("lava_hip_coopmat_reduce_into", inp, out, tile, dst_rows, dst_cols, mask, comb, ntiles, stream)
 
 
 def coopmat_convert(inp: int, out: int, out_dtype: str, n: int, stream: Optional[int] = None) -> None:

@@ -175,7 +175,9 @@ def supports_coopmat_reduce(backend=None) -> bool:
 
 
 def supports_flexible_coopmat_shapes(backend=None) -> bool:
-    """Subgroup fragments are exactly the MFMA shapes in the table."""
+    """Subgroup fragments are the MFMA shapes in the table.  The one place another extent is
+    taken is the destination of a reduce (lava_hip_coopmat_reduce_into: 16, 32 or 64 along a
+    free axis, half the extents for TwoByTwo), which is not the general capability this names."""
     return False
 
 

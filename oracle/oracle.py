@@ -231,6 +231,42 @@ def reduce_smear(m: np.ndarray, mask: int, combine: str) -> np.ndarray:
     return np.array(x)
 
 
+def reduce_into(m: np.ndarray, mask: int, combine: str, dst_rows: int, dst_cols: int) -> np.ndarray:
+    """coopmat_reduce into a dst_rows x dst_cols destination (coopmat2 flexible dimensions,
+    src/device/coopmat_intrinsics.jl:685-720): Row (1) keeps m's rows and repeats each row's
+    combination across the destination's columns, Column (2) the transpose of that, RowAndColumn
+    (3) fills the destination with the combination of all of m.  fp32 values, combined in fp64
+    (exact for the integer-valued tiles the tests use, and for max / min)."""
+    R, C = m.shape
+    f = {"add": np.sum, "max": np.max, "min": np.min}[combine]
+    x = m.astype(np.float64)
+    if mask == 1:
+        assert dst_rows == R
+        return np.repeat(f(x, axis=1)[:, None], dst_cols, axis=1)
+    if mask == 2:
+        assert dst_cols == C
+        return np.repeat(f(x, axis=0)[None, :], dst_rows, axis=0)
+    assert mask == 3
+    return np.full((dst_rows, dst_cols), f(x))
+
+
+def reduce_2x2(m: np.ndarray, combine: str) -> np.ndarray:
+    """The TwoByTwo reduce (the 2 x 2 block form of SPV_NV_cooperative_matrix2; the reference
+    declares the mask bit, src/vocabulary/coopmat.jl:289-297): element (i, j) of the
+    (R / 2) x (C / 2) result is f(f(m[2i, 2j], m[2i, 2j+1]), f(m[2i+1, 2j], m[2i+1, 2j+1])), in fp32
+    in that order."""
+    x = np.asarray(m, dtype=np.float32)
+    f = {"add": np.add, "max": np.maximum, "min": np.minimum}[combine]
+    R, C = x.shape
+    out = np.empty((R // 2, C // 2), dtype=np.float32)
+    for i in range(R // 2):
+        for j in range(C // 2):
+            top = f(x[2 * i, 2 * j], x[2 * i, 2 * j + 1])
+            bot = f(x[2 * i + 1, 2 * j], x[2 * i + 1, 2 * j + 1])
+            out[i, j] = f(np.float32(top), np.float32(bot))
+    return out
+
+
 def load_tile(buf: np.ndarray, off: int, stride: int, rowmajor: bool, R: int, C: int) -> np.ndarray:
     """coopmat_load of an R x C tile at 0-based element offset `off`: element (r, c) at
     off + r*stride + c (RowMajor) or off + c*stride + r (ColumnMajor, the default); a

@@ -1,0 +1,111 @@
+"""uint8 x uint8 -> uint32 GEMM (the unsigned coopmat product of test/spirv/test_coopmat_int8.jl:71-98,
+whose operands carry no signed-component bits) at matrix scale, against the oracle, bit for bit.
+
+The tile kernel runs it as a signed int8 product of the bytes flipped by 128 plus a row-sum and
+column-sum correction; the tests pin the identity where it can go wrong: every operand layout,
+ragged M, N and K (the zero padding of a ragged K enters the identity), the extremes 0 and 255,
+a K long enough that the 32-bit sum wraps, and the one-thread-per-element kernel for the shapes
+the tile kernel does not take.  Each test checks through the kernel log which kernel ran."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import lava_hip as lh_mod
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(lh, M, N, K, layout, seed):
+    A = lh.HIPDeviceArray("u8", (M, K), order="C" if layout & 1 else "F")
+    B = lh.HIPDeviceArray("u8", (K, N), order="C" if layout & 2 else "F")
+    lh.fill_i8(A, lh_mod.seed(seed, 0))   # the generator's bytes: uniform over 0..255 as uint8
+    lh.fill_i8(B, lh_mod.seed(seed, 1))
+    return A, B
+
+
+def _check(oracle, A, B, C, M, N, K, layout, rows):
+    lda = K if layout & 1 else M
+    ldb = N if layout & 2 else K
+    ref = oracle.gemm_u8_rows(A.to_numpy().ravel(order=A.order), B.to_numpy().ravel(order=B.order), N, K, lda, ldb,
+                              layout & 3, rows)
+    np.testing.assert_array_equal(C.to_numpy()[rows], ref)
+
+
+@pytest.mark.parametrize("layout", range(8))
+@pytest.mark.parametrize("shape", [(512, 768, 1024), (1008, 784, 528), (256, 256, 16)])
+def test_gemm_u8_tile_kernel(gpu, oracle, layout, shape):
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm u8 tile kernel layout={layout} M={M} N={N} K={K}")
+    A, B = _inputs(lh, M, N, K, layout, 60 + layout)
+    C = lh.HIPDeviceArray("u32", (M, N), order="C" if layout & 4 else "F")
+    C.fill_bytes(0xFF)
+    lh.kernel_log_clear()
+    lh.gemm(C, A, B)
+    assert "gemm_tn_kernel" in lh.kernel_log(), lh.kernel_log()
+    rows = np.unique(np.concatenate([np.arange(0, M, 11), [r for r in (1, 15, 16, 255, 256, M - 1) if r < M]]))
+    _check(oracle, A, B, C, M, N, K, layout, rows)
+
+
+def test_gemm_u8_full_size(gpu, oracle):
+    """4096^3 (the int8 configuration's shape, unsigned): sampled rows bit for bit, and every
+    element through the sum of C modulo 2^32 against the closed form (row sums of A) . (column
+    sums of B)."""
+    lh = gpu
+    M = N = K = 4096
+    announce("gemm u8 4096^3")
+    A, B = _inputs(lh, M, N, K, 1, 62)
+    C = lh.HIPDeviceArray("u32", (M, N), order="C")
+    lh.gemm(C, A, B)
+    rows = np.array([0, 1, 777, 2048, 4095])
+    _check(oracle, A, B, C, M, N, K, 1, rows)
+    a = A.to_numpy().astype(np.uint64)
+    b = B.to_numpy().astype(np.uint64)
+    want = int((a.sum(axis=0) * b.sum(axis=1)).sum()) % (1 << 32)   # sum_mn C = sum_k colsum_A(k) rowsum_B(k)
+    got = int(C.to_numpy().astype(np.uint64).sum()) % (1 << 32)
+    assert got == want
+
+
+@pytest.mark.parametrize("value", [0, 255])
+def test_gemm_u8_extremes_and_wrap(gpu, oracle, value):
+    """Every byte 0 or 255 (the extremes of the flipped encoding: -128 and 127) with K = 66064,
+    where 255^2 K = 4295811600 passes 2^32: C must hold the product modulo 2^32."""
+    lh = gpu
+    M, N, K = 256, 256, 66064
+    announce(f"gemm u8 extremes value={value} K={K}")
+    A = lh.HIPDeviceArray("u8", (M, K), order="C")
+    B = lh.HIPDeviceArray("u8", (K, N), order="F")
+    A.fill_bytes(value)
+    B.fill_bytes(value)
+    C = lh.HIPDeviceArray("u32", (M, N), order="C")
+    lh.kernel_log_clear()
+    lh.gemm(C, A, B)
+    assert "gemm_tn_kernel" in lh.kernel_log(), lh.kernel_log()
+    want = (value * value * K) % (1 << 32)
+    assert np.all(C.to_numpy() == np.uint32(want))
+
+
+@pytest.mark.parametrize("layout", [0, 3, 5, 7])
+@pytest.mark.parametrize("shape", [(100, 70, 50), (16, 16, 16), (300, 257, 33), (5, 1, 7)])
+def test_gemm_u8_generic_kernel(gpu, oracle, layout, shape):
+    """Shapes the tile kernel does not take (fewer than 256 x 256 outputs, or a K-contiguous K not
+    a multiple of 16) on the one-thread-per-element kernel, including the reference's 16x16x16
+    tile with a[l] = l % 7, b[l] = l % 5."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm u8 generic layout={layout} M={M} N={N} K={K}")
+    A, B = _inputs(lh, M, N, K, layout, 70 + layout)
+    if shape == (16, 16, 16):
+        l = np.arange(256)
+        A = lh.HIPDeviceArray.from_numpy((l % 7).astype(np.uint8).reshape(16, 16, order="F" if not layout & 1 else "C"),
+                                         "u8", order="C" if layout & 1 else "F")
+        B = lh.HIPDeviceArray.from_numpy((l % 5).astype(np.uint8).reshape(16, 16, order="F" if not layout & 2 else "C"),
+                                         "u8", order="C" if layout & 2 else "F")
+    C = lh.HIPDeviceArray("u32", (M, N), order="C" if layout & 4 else "F")
+    C.fill_bytes(0xFF)
+    lh.kernel_log_clear()
+    lh.gemm(C, A, B)
+    assert lh.kernel_log() == ["gemm_u8_generic_kernel"], lh.kernel_log()
+    _check(oracle, A, B, C, M, N, K, layout, np.arange(M))

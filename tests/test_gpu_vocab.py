@@ -162,6 +162,44 @@ def test_reduce_smears(gpu, oracle, tile, mask, combine):
     np.testing.assert_array_equal(got, oracle.reduce_smear(m, mask, combine).astype(np.float32))
 
 
+@pytest.mark.parametrize("tile", [16, 32])
+@pytest.mark.parametrize("mask,dst", [(1, (None, 16)), (1, (None, 64)), (2, (32, None)), (2, (64, None)),
+                                      (3, (16, 64)), (3, (64, 32)), (4, "half")])
+@pytest.mark.parametrize("combine", ["add", "max", "min"])
+def test_reduce_into_other_extent(gpu, oracle, tile, mask, dst, combine):
+    """coopmat_reduce into a destination of another extent (Row keeps the rows, Column the
+    columns, RowAndColumn any extent; the value smeared over the destination) and the TwoByTwo
+    block reduce into tile/2 x tile/2, against the oracle, bit for bit (small integers: every
+    fp32 sum exact).  Two tiles per call, each with its own values."""
+    lh = gpu
+    if dst == "half":
+        rd = cd = tile // 2
+    else:
+        rd = tile if dst[0] is None else dst[0]
+        cd = tile if dst[1] is None else dst[1]
+    announce(f"reduce_into tile={tile} mask={mask} dst={rd}x{cd} {combine}")
+    rng = np.random.default_rng(mask * 100 + tile + rd + cd)
+    ms = [rng.integers(-50, 50, (tile, tile)).astype(np.float32) for _ in range(2)]
+    din = flat(lh, np.concatenate([m.ravel(order="F") for m in ms]), "f32")
+    dout = flat(lh, np.full(2 * rd * cd, np.nan, np.float32), "f32")
+    lh.coopmat_reduce_into(din.ptr, dout.ptr, tile, rd, cd, mask, combine, 2)
+    got = dout.to_numpy()
+    for t, m in enumerate(ms):
+        g = got[t * rd * cd:(t + 1) * rd * cd].reshape(rd, cd, order="F")
+        want = oracle.reduce_2x2(m, combine) if mask == 4 else oracle.reduce_into(m, mask, combine, rd, cd)
+        np.testing.assert_array_equal(g, want.astype(np.float32))
+
+
+def test_reduce_into_shape_errors(gpu):
+    lh = gpu
+    announce("reduce_into shape errors")
+    for tile, rd, cd, mask in [(16, 32, 16, 1), (16, 16, 32, 2), (16, 16, 16, 4), (32, 16, 128, 3), (16, 16, 8, 1)]:
+        with pytest.raises(lh.InvalidArgument):
+            lh.coopmat_reduce_into(8, 8, tile, rd, cd, mask, "add", 1)
+    with pytest.raises(lh.Unsupported):
+        lh.coopmat_reduce(8, 8, 16, 4, "add", 1)   # the same-shape form has no TwoByTwo
+
+
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 def test_convert_rne(gpu, oracle, golden, dt):
     lh = gpu

@@ -278,6 +278,27 @@ def test_perelement_and_reduce_definitions(oracle, golden):
     assert p[2, 5] == max(m[2, 5], m[5, 2]) + 2 - 5
 
 
+def test_reduce_into_and_two_by_two_definitions(oracle):
+    """The reduce into another extent against closed forms of an arange tile (row r of m is
+    16 r + [0, 16): its max is 16 r + 15, its sum 256 r + 120), and the TwoByTwo block reduce
+    against an independent formulation (a reshape to (R/2, 2, C/2, 2) reduced over the block
+    axes); a transposed operand or a swapped block index fails both."""
+    m = np.arange(16 * 16, dtype=np.float32).reshape(16, 16)
+    r = oracle.reduce_into(m, 1, "max", 16, 64)
+    assert r.shape == (16, 64) and np.all(r == (16 * np.arange(16) + 15)[:, None])
+    c = oracle.reduce_into(m, 2, "add", 32, 16)
+    assert c.shape == (32, 16) and np.all(c == (16 * 120 + 16 * np.arange(16))[None, :])
+    s = oracle.reduce_into(m, 3, "min", 64, 32)
+    assert s.shape == (64, 32) and np.all(s == 0)
+    rng = np.random.default_rng(3)
+    x = rng.integers(-100, 100, (32, 32)).astype(np.float32)
+    for comb, f in (("add", np.sum), ("max", np.max), ("min", np.min)):
+        want = f(x.reshape(16, 2, 16, 2), axis=(1, 3))
+        np.testing.assert_array_equal(oracle.reduce_2x2(x, comb), want)
+    # a mistake a block reduce can make: pairing rows 2i and 2i+1 of the transposed tile
+    assert not np.array_equal(oracle.reduce_2x2(x.T, "max"), oracle.reduce_2x2(x, "max"))
+
+
 # ---------------------------------------------------------------- GEMM epilogue
 def test_gelu_closed_forms(oracle):
     """erf form: gelu(x) = x Phi(x) -- Phi(1) = 0.8413447460685429 (standard normal
