@@ -132,9 +132,10 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
     constexpr int JR = 64 / EV;               // 16-byte chunks across the 64 rows of an M/N-contiguous chunk
     constexpr bool A_TR = !AROW && sizeof(T) == 2;   // A read through transposing LDS reads
     constexpr bool B_TR = BROW && sizeof(T) == 2;
-    constexpr int SBYTES = (64 * PITCH > KC * PTR) ? 64 * PITCH : KC * PTR;
-    __shared__ __attribute__((aligned(16))) uint8_t As[SBYTES];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[SBYTES];
+    // each operand's staging sized for its own layout ([k][row] only for a transposed 16-bit operand):
+    // int8 needs 2 x 33 KB, so two workgroups share a CU
+    __shared__ __attribute__((aligned(16))) uint8_t As[A_TR ? KC * PTR : 64 * PITCH];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[B_TR ? KC * PTR : 64 * PITCH];
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
@@ -338,13 +339,14 @@ bool small_gemm_preferred(int64_t M, int64_t N, int64_t) {
     if (tiles256 <= SMALL_GEMM_MAX_TILES) return true;
     // Rate estimates (measured on shape lists): the tile kernel ~1500 TFLOP/s (bf16; int8 ~3000
     // TOP/s) times the share of the 256 CUs its tiles occupy times the useful share of the tile
-    // area, the small kernel ~450 (int8 ~400) times the share of 512 workgroups its 64 x 64
-    // tiles fill.  E.g. bf16 64 x 14336 x 4096: 94 -> 234 TFLOP/s; 1536^2 x 8192: 275 -> 342;
-    // 2048 x 4096 x 4096 stays on the tile kernel (898 against 494); int8 64 x 14336 x 4096:
-    // 166 -> 388 TOP/s, while 128 x 28672 x 8192 (723 against 517) and 2048^3 (651 against 507)
-    // stay on the tile kernel.
+    // area, the small kernel ~450 (int8 ~800, two workgroups per CU) times the share of 512
+    // workgroups its 64 x 64 tiles fill.  E.g. bf16 64 x 14336 x 4096: 94 -> 234 TFLOP/s; 1536^2
+    // x 8192: 275 -> 342; 2048 x 4096 x 4096 stays on the tile kernel (898 against 494); int8
+    // (tile kernel against small kernel, TOP/s): 64 x 14336 x 4096 166 / 383, 128 x 28672 x 8192
+    // 727 / 755, 2048^3 653 / 681, 1536^2 x 8192 515 / 637 take the small kernel, 2048 x 4096 x
+    // 4096 (1558 / 916) the tile kernel.
     const double tile_rate = sizeof(T) == 1 ? 3000.0 : 1500.0;
-    const double small_rate = sizeof(T) == 1 ? 400.0 : 450.0;
+    const double small_rate = sizeof(T) == 1 ? 800.0 : 450.0;
     const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
     const double occ256 = tiles256 >= 256 ? 1.0 : (double)tiles256 / 256.0;
     const double useful = (double)M * (double)N / ((double)tiles256 * 65536.0);

@@ -359,13 +359,20 @@ __global__ void __launch_bounds__(256, 1)
         sum = __builtin_amdgcn_sdot4((int)v.z, 0x01010101, sum, false);
         sum = __builtin_amdgcn_sdot4((int)v.w, 0x01010101, sum, false);
     };
-    // before MFMA q of a k-step: the fragments it reads first (b[q] for q < 8, a[q / 8] at q % 8 == 0)
-    auto flip_for = [&](F16& f, int q) __attribute__((always_inline)) {
+    // fragment t in read order (a[0], b[0..7], a[1..7]).  Each is flipped two reads after its own
+    // read was issued, well before its first MFMA, so that neither the LDS latency nor the
+    // VALU-to-MFMA wait sits in front of an MFMA; the last two of a k-step are flipped early in
+    // the next one (their first MFMAs come at 48 and 56).  Fragments read past the last k-tile
+    // are never flipped, so they do not enter the sums.
+    auto flip_t = [&](F16& f, int t) __attribute__((always_inline)) {
         if constexpr (U8) {
-            if (q < 8) flip(f.b[q], rb[q]);
-            if ((q & 7) == 0) flip(f.a[q >> 3], ra[q >> 3]);
+            if (t == 0) flip(f.a[0], ra[0]);
+            else if (t <= 8) flip(f.b[t - 1], rb[t - 1]);
+            else flip(f.a[t - 8], ra[t - 8]);
         }
     };
+#pragma unroll
+    for (int t = 0; t < 16; ++t) flip_t(fa, t);
 
     for (int kt = 0; kt < ktiles; ++kt) {
         const int st = kt & 1;
@@ -374,9 +381,10 @@ __global__ void __launch_bounds__(256, 1)
         const uint32_t kofs2 = (uint32_t)(kt + 2 < ktiles ? kt + 2 : ktiles - 1) * TN_KB;
 #pragma unroll
         for (int q = 0; q < 64; ++q) {
-            flip_for(fa, q);
             acc[q >> 3][q & 7] = Mfma16<T>::run(fa.b[q & 7], fa.a[q >> 3], acc[q >> 3][q & 7]);
             if ((q & 3) == 3) rd16(fb, base, 1, q >> 2);
+            if ((q == 2 || q == 6) && kt > 0) flip_t(fa, 14 + (q >> 2));
+            if ((q & 3) == 3 && (q >> 2) >= 2) flip_t(fb, (q >> 2) - 2);
             __builtin_amdgcn_sched_barrier(0);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's part of tile kt + 1 landed
@@ -384,14 +392,26 @@ __global__ void __launch_bounds__(256, 1)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int q = 0; q < 64; ++q) {
-            flip_for(fb, q);
             acc[q >> 3][q & 7] = Mfma16<T>::run(fb.b[q & 7], fb.a[q >> 3], acc[q >> 3][q & 7]);
             if ((q & 3) == 1) rd16(fa, next, 0, q >> 2);
             if ((q & 3) == 3) dma(q >> 2, st, kofs2);
+            if (q == 2 || q == 6) flip_t(fb, 14 + (q >> 2));
+            if ((q & 3) == 3 && (q >> 2) >= 2 && kt + 1 < ktiles) flip_t(fa, (q >> 2) - 2);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
 
+    // ---- epilogue through LDS, so that global stores are whole 512-byte row runs.
+    // acc[I][j] register r of lane l is C[m][n] with m = 128 wm + 16 I + l % 16 and
+    // n = 128 wn + 16 j + 4 (l / 16) + r within the tile (the 16x16 MFMA accumulator
+    // map, I and j = 0..7).  Each wave stages 32 rows x 128 columns at a time (a row
+    // quarter i: I = 2 i, 2 i + 1) in its own 16.5 KB of the idle stage buffers (4 waves:
+    // 66 KB of the 128 KB), rows padded to 528 bytes so the 32 rows of one column group
+    // land on distinct banks; then reads whole rows back: lanes 0..31 and 32..63 each
+    // cover one 512-byte row per instruction.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    constexpr int EP_PITCH = 128 * 4 + 16;
     if constexpr (U8) {
         // full sums: the four 16-lane groups hold the four 16-byte quarters of every k-step
 #pragma unroll
@@ -417,17 +437,6 @@ __global__ void __launch_bounds__(256, 1)
         }
     }
 
-    // ---- epilogue through LDS, so that global stores are whole 512-byte row runs.
-    // acc[I][j] register r of lane l is C[m][n] with m = 128 wm + 16 I + l % 16 and
-    // n = 128 wn + 16 j + 4 (l / 16) + r within the tile (the 16x16 MFMA accumulator
-    // map, I and j = 0..7).  Each wave stages 32 rows x 128 columns at a time (a row
-    // quarter i: I = 2 i, 2 i + 1) in its own 16.5 KB of the idle stage buffers (4 waves:
-    // 66 KB of the 128 KB), rows padded to 528 bytes so the 32 rows of one column group
-    // land on distinct banks; then reads whole rows back: lanes 0..31 and 32..63 each
-    // cover one 512-byte row per instruction.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    constexpr int EP_PITCH = 128 * 4 + 16;
     const int rr = lane & 31;
     uint8_t* ep = smem + w * (32 * EP_PITCH);
     typedef Acc Acc4 __attribute__((ext_vector_type(4)));
