@@ -11,7 +11,7 @@ before timing starts.
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
                               gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|gemm_shapes|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy|
-                              hbm_read|gemm_u8]
+                              hbm_read|gemm_u8|mfma_loop]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -84,6 +84,8 @@ def timed(lh, launch, steps: int, warmup: int, stream, group: int = 1):
 
 # mean of the per-launch kernel times of the last timed() call (reported beside the median)
 TIMED_MEAN_MS = [0.0]
+# the two operand arrays of the last GEMM or attention workload (for the MFMA-loop ceiling)
+LAST_INPUTS = []
 # seconds of untimed load before each workload's warmup (--settle)
 SETTLE_S = [1.0]
 # launches per timed step for the kernels of a few tens of microseconds (W8A16, the 256^3 GEMM)
@@ -115,6 +117,30 @@ def roofline(bound, achieved, peak, unit, traffic):
             "frac": round(achieved / peak, 4), "traffic": traffic}
 
 
+# lava_hip_mfma_loop forms: (id, depth K of one MFMA, name)
+MFMA_FORMS = {"f16_16x16x32": (0, 32), "bf16_16x16x32": (1, 32), "i8_16x16x64": (2, 64),
+              "f16_32x32x16": (3, 16), "bf16_32x32x16": (4, 16), "i8_32x32x32": (5, 32)}
+
+
+def mfma_loop_rate(lh, form, a, b, waves, stream, iters=4096, steps=5, warmup=2):
+    """T(FL)OP/s of a loop of MFMAs of `form` with no memory access, its operands read once from
+    the device arrays a and b (the workload's own inputs), 256 workgroups (one per CU) of
+    `waves` waves per SIMD: what the matrix cores sustain on that data at the clock the power
+    budget allows."""
+    op, depth = MFMA_FORMS[form]
+    nbytes = min(a.nbytes, b.nbytes) // 16 * 16
+    sink = lh.HIPDeviceArray("f32", (256 * 256 * waves,))
+    kms, _ = timed(lh, lambda: lh._lib.call("lava_hip_mfma_loop", op, a.ptr, b.ptr, nbytes, 256, waves, iters,
+                                            sink.ptr, stream), steps, warmup, stream)
+    return 256 * 4 * waves * iters * 8192.0 * depth / (kms * 1e-3) / 1e12
+
+
+def with_loop_ceiling(roof, rate, what):
+    """Adds the MFMA-loop ceiling (mfma_loop_rate) beside the published peak of a roofline."""
+    roof["loop_ceiling"] = {"value": round(rate, 1), "frac": round(roof["achieved"] / rate, 4), "what": what}
+    return roof
+
+
 # ---------------------------------------------------------------- workloads
 def bench_gemm(lh, dt, n, steps, warmup, stream, cfg, shape=None):
     M, N, Kd = shape if shape is not None else (n, n, n)
@@ -131,6 +157,7 @@ def bench_gemm(lh, dt, n, steps, warmup, stream, cfg, shape=None):
     lh.synchronize()
     kern_ms, wall_ms = timed(lh, lambda: lh.gemm(C, A, B, stream=stream), steps, warmup, stream)
     flop = 2.0 * M * N * Kd
+    LAST_INPUTS[:] = [A, B]
     return flop, kern_ms, wall_ms
 
 
@@ -186,6 +213,7 @@ def bench_attn(lh, steps, warmup, stream, B=4, H=32, S=4096, D=128):
     kern_ms, wall_ms = timed(lh, lambda: lh.flash_attn_fwd(O, Q, K, V, scale=sc, causal=True, stream=stream),
                              steps, warmup, stream)
     flop = 0.5 * 4.0 * B * H * S * S * D   # causal: half of 4*B*H*S^2*D
+    LAST_INPUTS[:] = [Q, K]
     return flop, kern_ms, wall_ms
 
 
@@ -330,7 +358,8 @@ def main():
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96", "attn_d256",
-                             "copy", "hbm_read", "vendor_bf16", "w8a16_wrow", "w8a16_julia", "gemm_shapes", "gemm_u8"])
+                             "copy", "hbm_read", "vendor_bf16", "w8a16_wrow", "w8a16_julia", "gemm_shapes", "gemm_u8",
+                             "mfma_loop"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -374,6 +403,8 @@ def main():
                                            "and output (BASELINE configs[1])", "M": 8192, "N": 8192, "K": 8192},
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(gemm_mean, 4),
                     "roofline": roofline("mfma", achieved, PEAK_BF16_TFLOPS, "TFLOP/s", load_traffic("gemm_bf16_8192"))})
+        with_loop_ceiling(out["roofline"], mfma_loop_rate(lh, "bf16_16x16x32", *LAST_INPUTS, 1, stream),
+                          "bf16 16x16x32 MFMAs alone on the GEMM's A and B, 1 wave per SIMD as in the kernel")
         if args.workload == "headline":
             aflop, akms, awms = bench_attn(lh, K, W, stream)
             a_ach = aflop / (akms * 1e-3) / 1e12
@@ -383,8 +414,11 @@ def main():
                                "config": {"workload": "causal flash-attention forward B=4 H=32 S=4096 D=128 fp16, "
                                                       "fp32 softmax state (BASELINE configs[4]); FLOP = "
                                                       "0.5*4*B*H*S^2*D"},
-                               "roofline": roofline("mfma", a_ach, PEAK_FP16_TFLOPS, "TFLOP/s",
-                                                    load_traffic("flash_fwd_causal"))}
+                               "roofline": with_loop_ceiling(
+                                   roofline("mfma", a_ach, PEAK_FP16_TFLOPS, "TFLOP/s", load_traffic("flash_fwd_causal")),
+                                   mfma_loop_rate(lh, "f16_32x32x16", *LAST_INPUTS, 2, stream),
+                                   "f16 32x32x16 MFMAs alone on the attention's Q and K, 2 waves per SIMD as in "
+                                   "the kernel")}
     elif args.workload == "gemm_bf16_4096":
         flop, kms, wms = bench_gemm(lh, "bf16", 4096, K, W, stream, 1)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
@@ -547,6 +581,38 @@ def main():
                     "w8a16_size": {"bytes": wb, "copies": 6, "us": round(wms_k * 1e3, 2),
                                    "GBs": round(wb / (wms_k * 1e-3) / 1e9, 1), "launch": "448 x 256 threads"},
                     "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s", nbytes)})
+    elif args.workload == "mfma_loop":
+        # the matrix cores alone: MFMA loops with no memory access, on each workload's own data
+        # (the GEMM's uniform[-1,1] bf16, the attention's normal(0,1) fp16, the int8 GEMM's bytes)
+        # and on constant data (every fp16 operand the same), at 1, 2 and 4 waves per SIMD
+        n = 4096
+        A = lh.HIPDeviceArray("bf16", (n, n))
+        B = lh.HIPDeviceArray("bf16", (n, n))
+        lh.fill_uniform(A, lh.seed(1, 0), -1.0, 1.0)
+        lh.fill_uniform(B, lh.seed(1, 1), -1.0, 1.0)
+        Q = lh.HIPDeviceArray("f16", (n, n))
+        Kt = lh.HIPDeviceArray("f16", (n, n))
+        lh.fill_normal(Q, lh.seed(4, 0))
+        lh.fill_normal(Kt, lh.seed(4, 1))
+        Ai = lh.HIPDeviceArray("i8", (n, n))
+        Bi = lh.HIPDeviceArray("i8", (n, n))
+        lh.fill_i8(Ai, lh.seed(2, 0))
+        lh.fill_i8(Bi, lh.seed(2, 1))
+        ones = lh.HIPDeviceArray("f16", (n, n))
+        ones.fill_bytes(0x3C)   # every operand 0x3C3C = 1.0586
+        lh.synchronize()
+        rates = {}
+        for form, a, b in (("bf16_16x16x32", A, B), ("bf16_32x32x16", A, B), ("f16_16x16x32", Q, Kt),
+                           ("f16_32x32x16", Q, Kt), ("i8_16x16x64", Ai, Bi), ("i8_32x32x32", Ai, Bi),
+                           ("f16_16x16x32 constant", ones, ones)):
+            for waves in (1, 2, 4):
+                rates[f"{form}, {waves} wave(s)/SIMD"] = round(
+                    mfma_loop_rate(lh, form.split()[0], a, b, waves, stream, steps=K, warmup=W), 1)
+        top = rates["bf16_16x16x32, 1 wave(s)/SIMD"]
+        out.update({"value": top, "unit": "TFLOP/s", "ms_per_step": None, "dtype": "bf16",
+                    "config": {"workload": "MFMA loops without memory access, 256 workgroups (one per CU), "
+                                           "4096 rounds; value: bf16 16x16x32 at 1 wave/SIMD on uniform[-1,1]"},
+                    "rates": rates, "roofline": roofline("mfma", top, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "copy":
         # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain 1 GiB device copy
         nbytes = 1 << 30

@@ -149,6 +149,25 @@ void lava_hip_kernel_log_clear(void);
  * of 16. */
 int lava_hip_read_stream(const void* src, size_t bytes, uint32_t* sink, int blocks, int unroll, void* stream);
 
+/* MFMA forms for lava_hip_mfma_loop. */
+#define LAVA_HIP_MFMA_F16_16X16X32 0
+#define LAVA_HIP_MFMA_BF16_16X16X32 1
+#define LAVA_HIP_MFMA_I8_16X16X64 2
+#define LAVA_HIP_MFMA_F16_32X32X16 3
+#define LAVA_HIP_MFMA_BF16_32X32X16 4
+#define LAVA_HIP_MFMA_I8_32X32X32 5
+/* Issues MFMAs of form `op` with no memory access in the loop: `blocks` workgroups of
+ * 256 * waves_per_simd (1, 2 or 4) threads, one workgroup per CU at a time, each lane holding four (a, b) operand pairs of 16
+ * bytes read once from a and b (lane i takes 16-byte words 4i .. 4i+3, modulo bytes / 16), then
+ * `iters` rounds of 16 independent MFMAs of a 16x16 form or 4 of a 32x32 form.  Writes a hash of
+ * each thread's accumulators to sink[thread] (blocks * 256 * waves_per_simd floats).  Each wave
+ * does iters rounds of 8192 * K FLOP (integer ops for int8; K the form's depth: 32 or 64 for the
+ * 16x16 forms, 16 or 32 for the 32x32 forms), blocks * 4 * waves_per_simd waves: the matrix-core
+ * rate the part sustains on that data at the clock its power budget allows.  a, b 16-byte
+ * aligned, bytes a positive multiple of 16. */
+int lava_hip_mfma_loop(int op, const void* a, const void* b, size_t bytes, int blocks, int waves_per_simd,
+                       int iters, float* sink, void* stream);
+
 #define LAVA_HIP_FAMILY_ATTN 1
 #define LAVA_HIP_FAMILY_GEMM 2
 int lava_hip_set_kernel_override(int family, int choice);

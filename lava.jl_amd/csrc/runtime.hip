@@ -129,6 +129,75 @@ __global__ void __launch_bounds__(256) read_stream_kernel(const rs_u32x4* __rest
     sink[tid] = acc;
 }
 
+// MFMA issue loop (lava_hip_mfma_loop): each lane reads four (a, b) operand pairs of 16 bytes
+// from the caller's buffers once, then issues `iters` rounds of independent MFMAs -- 16 of a 16x16
+// form on 16 accumulators, or 4 of a 32x32 form on 4 -- with operand pair t % 4 for accumulator t
+// and no memory access in the loop.  The matrix-core rate the part sustains on that data at the
+// clock its power budget allows, the ceiling beside the published peak.
+typedef float ml_f32x4 __attribute__((ext_vector_type(4)));
+typedef float ml_f32x16 __attribute__((ext_vector_type(16)));
+typedef int ml_i32x4 __attribute__((ext_vector_type(4)));
+typedef int ml_i32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 ml_f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 ml_bf16x8 __attribute__((ext_vector_type(8)));
+
+template <int OP>
+__global__ void __launch_bounds__(1024, 1) mfma_loop_kernel(const rs_u32x4* __restrict__ a,
+                                                           const rs_u32x4* __restrict__ b, size_t n16,
+                                                           int iters, float* __restrict__ sink) {
+    // 81 KB of LDS (never touched: the entry rejects iters < 1) hold the part to one workgroup
+    // per CU, so that waves per SIMD is blockDim / 256 as asked
+    __shared__ float one_per_cu[81 * 256];
+    if (iters < 0) one_per_cu[threadIdx.x] = 0.f;
+    const size_t tid = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    ml_i32x4 op[8];
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+        op[2 * o] = (ml_i32x4)a[(tid * 4 + o) % n16];
+        op[2 * o + 1] = (ml_i32x4)b[(tid * 4 + o) % n16];
+    }
+    constexpr bool WIDE = (OP == LAVA_HIP_MFMA_F16_32X32X16 || OP == LAVA_HIP_MFMA_BF16_32X32X16 ||
+                           OP == LAVA_HIP_MFMA_I8_32X32X32);
+    ml_f32x4 c4[WIDE ? 1 : 16];
+    ml_f32x16 c16[WIDE ? 4 : 1];
+    for (int t = 0; t < (WIDE ? 1 : 16); ++t) c4[t] = ml_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < (WIDE ? 4 : 1); ++t)
+        for (int r = 0; r < 16; ++r) c16[t][r] = 0.f;
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int t = 0; t < (WIDE ? 4 : 16); ++t) {
+            const ml_i32x4 x = op[2 * (t & 3)], y = op[2 * (t & 3) + 1];
+            if constexpr (OP == LAVA_HIP_MFMA_F16_16X16X32)
+                c4[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16((ml_f16x8)x, (ml_f16x8)y, c4[t], 0, 0, 0);
+            else if constexpr (OP == LAVA_HIP_MFMA_BF16_16X16X32)
+                c4[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16((ml_bf16x8)x, (ml_bf16x8)y, c4[t], 0, 0, 0);
+            else if constexpr (OP == LAVA_HIP_MFMA_I8_16X16X64)
+                c4[t] = (ml_f32x4)__builtin_amdgcn_mfma_i32_16x16x64_i8(x, y, (ml_i32x4)c4[t], 0, 0, 0);
+            else if constexpr (OP == LAVA_HIP_MFMA_F16_32X32X16)
+                c16[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16((ml_f16x8)x, (ml_f16x8)y, c16[t], 0, 0, 0);
+            else if constexpr (OP == LAVA_HIP_MFMA_BF16_32X32X16)
+                c16[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16((ml_bf16x8)x, (ml_bf16x8)y, c16[t], 0, 0, 0);
+            else
+                c16[t] = (ml_f32x16)__builtin_amdgcn_mfma_i32_32x32x32_i8(x, y, (ml_i32x16)c16[t], 0, 0, 0);
+        }
+    }
+    // the accumulators' bits, folded by multiply-add (accumulators that hold equal values do not
+    // cancel, as they would under XOR) so that no MFMA is dropped
+    uint32_t h = 0;
+    for (int t = 0; t < (WIDE ? 1 : 16); ++t)
+        for (int r = 0; r < 4; ++r) h = h * 0x9E3779B1u + __float_as_uint(c4[t][r]);
+    for (int t = 0; t < (WIDE ? 4 : 1); ++t)
+        for (int r = 0; r < 16; ++r) h = h * 0x9E3779B1u + __float_as_uint(c16[t][r]);
+    sink[tid] = __uint_as_float(h);
+}
+
+template <int OP>
+static void launch_mfma_loop(int blocks, int threads, hipStream_t s, const rs_u32x4* a, const rs_u32x4* b,
+                             size_t n16, int iters, float* sink) {
+    hipLaunchKernelGGL(mfma_loop_kernel<OP>, dim3((unsigned)blocks), dim3((unsigned)threads), 0, s, a, b, n16, iters,
+                       sink);
+}
+
 }  // namespace lava
 
 using namespace lava;
@@ -312,6 +381,45 @@ int lava_hip_read_stream(const void* src, size_t bytes, uint32_t* sink, int bloc
     else
         hipLaunchKernelGGL(read_stream_kernel<16>, dim3((unsigned)blocks), dim3(256), 0, s, s4, n16, sink);
     LAVA_LAUNCH_CHECK("read_stream_kernel");
+    return LAVA_HIP_OK;
+}
+
+int lava_hip_mfma_loop(int op, const void* a, const void* b, size_t bytes, int blocks, int waves_per_simd,
+                       int iters, float* sink, void* stream) {
+    LAVA_ARG(a != nullptr && b != nullptr && sink != nullptr, "mfma_loop: null pointer");
+    LAVA_ARG(aligned(a, 16) && aligned(b, 16) && bytes >= 16 && bytes % 16 == 0,
+             "mfma_loop: a and b must be 16-byte aligned and bytes a positive multiple of 16");
+    LAVA_ARG(op >= LAVA_HIP_MFMA_F16_16X16X32 && op <= LAVA_HIP_MFMA_I8_32X32X32, "mfma_loop: unknown form %d", op);
+    LAVA_ARG(blocks >= 1 && blocks <= 65536, "mfma_loop: blocks = %d outside [1, 65536]", blocks);
+    LAVA_ARG(waves_per_simd == 1 || waves_per_simd == 2 || waves_per_simd == 4,
+             "mfma_loop: waves_per_simd = %d is not 1, 2 or 4", waves_per_simd);
+    LAVA_ARG(iters >= 1, "mfma_loop: iters = %d < 1", iters);
+    const rs_u32x4* a4 = static_cast<const rs_u32x4*>(a);
+    const rs_u32x4* b4 = static_cast<const rs_u32x4*>(b);
+    const size_t n16 = bytes / 16;
+    const int threads = 256 * waves_per_simd;
+    hipStream_t s = as_stream(stream);
+    switch (op) {
+        case LAVA_HIP_MFMA_F16_16X16X32:
+            launch_mfma_loop<LAVA_HIP_MFMA_F16_16X16X32>(blocks, threads, s, a4, b4, n16, iters, sink);
+            break;
+        case LAVA_HIP_MFMA_BF16_16X16X32:
+            launch_mfma_loop<LAVA_HIP_MFMA_BF16_16X16X32>(blocks, threads, s, a4, b4, n16, iters, sink);
+            break;
+        case LAVA_HIP_MFMA_I8_16X16X64:
+            launch_mfma_loop<LAVA_HIP_MFMA_I8_16X16X64>(blocks, threads, s, a4, b4, n16, iters, sink);
+            break;
+        case LAVA_HIP_MFMA_F16_32X32X16:
+            launch_mfma_loop<LAVA_HIP_MFMA_F16_32X32X16>(blocks, threads, s, a4, b4, n16, iters, sink);
+            break;
+        case LAVA_HIP_MFMA_BF16_32X32X16:
+            launch_mfma_loop<LAVA_HIP_MFMA_BF16_32X32X16>(blocks, threads, s, a4, b4, n16, iters, sink);
+            break;
+        default:
+            launch_mfma_loop<LAVA_HIP_MFMA_I8_32X32X32>(blocks, threads, s, a4, b4, n16, iters, sink);
+            break;
+    }
+    LAVA_LAUNCH_CHECK("mfma_loop_kernel");
     return LAVA_HIP_OK;
 }
 

@@ -114,6 +114,7 @@ PROTOTYPES: dict[str, tuple] = {
                                          C.POINTER(i64), C.c_float, ci, vp]),
     "lava_hip_release_workspaces": (ci, []),
     "lava_hip_read_stream": (ci, [vp, C.c_size_t, vp, ci, ci, vp]),
+    "lava_hip_mfma_loop": (ci, [ci, vp, vp, C.c_size_t, ci, ci, ci, vp, vp]),
     "lava_hip_graph_capture_begin": (ci, [vp]),
     "lava_hip_graph_capture_end": (ci, [vp, C.POINTER(vp)]),
     "lava_hip_graph_launch": (ci, [vp, vp]),
