@@ -531,7 +531,7 @@ def main():
                                                           "(signed MFMA on bytes flipped by 128, row/column-sum "
                                                           "correction)"},
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
-                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_INT8_TOPS, "TOP/s", None)})
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_INT8_TOPS, "TOP/s", load_traffic("gemm_u8_4096"))})
     elif args.workload in W8A16_WORKLOADS:
         xo, wo, yo, what, traffic_key = W8A16_WORKLOADS[args.workload]
         nbytes, kms, wms = bench_w8a16(lh, K, W, stream, x_order=xo, w_order=wo, y_order=yo)
@@ -580,7 +580,7 @@ def main():
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "w8a16_size": {"bytes": wb, "copies": 6, "us": round(wms_k * 1e3, 2),
                                    "GBs": round(wb / (wms_k * 1e-3) / 1e9, 1), "launch": "448 x 256 threads"},
-                    "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s", nbytes)})
+                    "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s", load_traffic("hbm_read_4g"))})
     elif args.workload == "mfma_loop":
         # the matrix cores alone: MFMA loops with no memory access, on each workload's own data
         # (the GEMM's uniform[-1,1] bf16, the attention's normal(0,1) fp16, the int8 GEMM's bytes)
