@@ -11,7 +11,7 @@ before timing starts.
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
                               gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|gemm_shapes|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy|
-                              hbm_read|gemm_u8|mfma_loop]
+                              hbm_read|gemm_u8|mfma_loop|gemm_bf16_pad64]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -359,7 +359,7 @@ def main():
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96", "attn_d256",
                              "copy", "hbm_read", "vendor_bf16", "w8a16_wrow", "w8a16_julia", "gemm_shapes", "gemm_u8",
-                             "mfma_loop"])
+                             "mfma_loop", "gemm_bf16_pad64"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -430,6 +430,23 @@ def main():
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16", "config": {"workload": "bf16 GEMM M=N=K=8000 (not a tile multiple: "
                                                             "zero-clamped loads, bounds-checked store)"},
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "gemm_bf16_pad64":
+        # the headline product with A's and B's rows 8192 + 64 elements apart (not 16 KiB): the
+        # L2-set aliasing check for the tile kernel's LDS-DMA row pattern
+        n, ld = 8192, 8192 + 64
+        A = lh.HIPDeviceArray("bf16", (n, ld), order="C")
+        B = lh.HIPDeviceArray("bf16", (ld, n), order="F")
+        C = lh.HIPDeviceArray("f32", (n, n), order="C")
+        lh.fill_uniform(A, lh.seed(1, 0), -1.0, 1.0)
+        lh.fill_uniform(B, lh.seed(1, 1), -1.0, 1.0)
+        lh.synchronize()
+        kms, wms = timed(lh, lambda: lh.gemm_raw("bf16", "f32", A.ptr, B.ptr, C.ptr, n, n, n, ld, ld, n, 1 | 4, stream),
+                         K, W, stream)
+        flop = 2.0 * n ** 3
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "bf16", "config": {"workload": "bf16 GEMM 8192^3 as the headline, lda = ldb = 8256"},
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_shapes":

@@ -12,6 +12,7 @@
 // kernel.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
 #include <utility>
 
 #include "gemm_kernels.hpp"
@@ -21,9 +22,13 @@ using namespace lava;
 
 namespace {
 
-template <typename T, typename OutT = typename Mfma16<T>::acc_elem, bool EPI = false>
+// U8: int8 storage read as unsigned bytes, uint32 results (the int32 words' bits); the same
+// kernel choice, with each kernel's unsigned form and a one-thread-per-element kernel in the
+// staged kernel's place.
+template <typename T, typename OutT = typename Mfma16<T>::acc_elem, bool EPI = false, bool U8 = false>
 int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                int64_t ldb, int64_t ldc, uint32_t layout, void* stream, Epilogue epi = Epilogue{}) {
+    static_assert(!U8 || (std::is_same<T, int8_t>::value && !EPI), "unsigned: int8 storage, no epilogue");
     using Acc = OutT;
     LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative extent (M=%lld N=%lld K=%lld)", name, (long long)M,
              (long long)N, (long long)K);
@@ -79,60 +84,28 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
             const SmallSplit sp = pin == 2 ? SmallSplit{} : small_gemm_splits<T>(M, N, K);
             // under graph capture, split only within the workspace the stream already has
             if (sp.splits > 1 && small_splitk_bytes<T>(M, N, sp) <= stream_workspace_cap(stream))
-                return launch_gemm_small_splitk<T>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, stream, sp);
+                return launch_gemm_small_splitk<T, U8>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, stream, sp);
         }
-        return launch_gemm_small<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
+        if constexpr (U8)
+            return launch_gemm_small_u8(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s);
+        else
+            return launch_gemm_small<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
     }
-    if (fit != TN_NO && pin != 3)
-        return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, fit == TN_RAGGED, arow, !brow);
+    if (fit != TN_NO && pin != 3) {
+        if constexpr (U8)
+            return launch_gemm_tn_u8(a, b, c, M, N, K, lda, ldb, ldc, s, fit == TN_RAGGED, arow, !brow);
+        else
+            return launch_gemm_tn<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, fit == TN_RAGGED, arow, !brow);
+    }
+    if constexpr (U8) {
+        LAVA_REQUIRE((M * N + 255) / 256 <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "%s: problem too large", name);
+        return launch_gemm_u8_generic(reinterpret_cast<const uint8_t*>(a), reinterpret_cast<const uint8_t*>(b),
+                                      reinterpret_cast<uint32_t*>(c), M, N, K, lda, ldb, ldc,
+                                      (arow ? 1u : 0u) | (brow ? 2u : 0u) | 4u, s);
+    }
     LAVA_REQUIRE((N + 63) / 64 <= 0x7fffffff && (M + 63) / 64 <= 65535, LAVA_HIP_ERR_UNSUPPORTED,
                  "%s: too many 64-row tiles for the staged kernel (M=%lld N=%lld)", name, (long long)M, (long long)N);
     return launch_gemm_staged<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, arow, brow, s, epi);
-}
-
-// C = A B over unsigned bytes, uint32 accumulate (wrapping): the tile kernel in its U8 mode for
-// the shapes it takes, otherwise one thread per element of C.
-int gemm_u8_entry(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
-                  int64_t ldc, uint32_t layout, void* stream) {
-    const char* name = "gemm_u8_u32";
-    LAVA_ARG(M >= 0 && N >= 0 && K >= 0, "%s: negative extent (M=%lld N=%lld K=%lld)", name, (long long)M,
-             (long long)N, (long long)K);
-    LAVA_ARG(layout <= 7u, "%s: layout %u has bits beyond A/B/C row-major", name, layout);
-    if (M == 0 || N == 0) return LAVA_HIP_OK;
-    LAVA_ARG(C != nullptr, "%s: null C", name);
-    LAVA_ARG(K == 0 || (A != nullptr && B != nullptr), "%s: null A or B", name);
-    bool arow = layout & 1u, brow = layout & 2u;
-    const bool crow = layout & 4u;
-    const int64_t k1 = K > 0 ? K : 1;
-    LAVA_ARG(lda >= (arow ? k1 : M), "%s: lda = %lld is smaller than %s", name, (long long)lda, arow ? "K" : "M");
-    LAVA_ARG(ldb >= (brow ? N : k1), "%s: ldb = %lld is smaller than %s", name, (long long)ldb, brow ? "N" : "K");
-    LAVA_ARG(ldc >= (crow ? N : M), "%s: ldc = %lld is smaller than %s", name, (long long)ldc, crow ? "N" : "M");
-    LAVA_ARG(aligned(C, 4), "%s: C not aligned to 4 bytes", name);
-    LAVA_REQUIRE((M * N + 255) / 256 <= 0x7fffffff, LAVA_HIP_ERR_UNSUPPORTED, "%s: problem too large", name);
-    int rc = lava_hip_init();
-    if (rc != LAVA_HIP_OK) return rc;
-    hipStream_t s = as_stream(stream);
-    if (K > 0) {
-        const int8_t* a = static_cast<const int8_t*>(A);
-        const int8_t* b = static_cast<const int8_t*>(B);
-        int64_t m = M, n = N, la = lda, lb = ldb;
-        bool ar = arow, br = brow;
-        if (!crow) {   // C^T = B^T A^T, row-major
-            std::swap(a, b);
-            std::swap(m, n);
-            std::swap(la, lb);
-            const bool t = ar;
-            ar = !br;
-            br = !t;
-        }
-        const int fit = kernel_override(LAVA_HIP_FAMILY_GEMM) == 3
-                            ? TN_NO
-                            : tn_gemm_eligible<int8_t>(a, b, C, m, n, K, la, lb, ldc, sizeof(int32_t), ar, !br);
-        if (fit != TN_NO)
-            return launch_gemm_tn_u8(a, b, static_cast<int32_t*>(C), m, n, K, la, lb, ldc, s, fit == TN_RAGGED, ar, !br);
-    }
-    return launch_gemm_u8_generic(static_cast<const uint8_t*>(A), static_cast<const uint8_t*>(B),
-                                  static_cast<uint32_t*>(C), M, N, K, lda, ldb, ldc, layout, s);
 }
 
 template <typename T, typename OutT>
@@ -174,7 +147,7 @@ int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64
 
 int lava_hip_gemm_u8_u32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream) {
-    return gemm_u8_entry(A, B, C, M, N, K, lda, ldb, ldc, layout, stream);
+    return gemm_entry<int8_t, int32_t, false, true>("gemm_u8_u32", A, B, C, M, N, K, lda, ldb, ldc, layout, stream);
 }
 
 int lava_hip_gemm_ex(int ab_dtype, int d_dtype, const void* A, const void* B, void* D, int64_t M, int64_t N,

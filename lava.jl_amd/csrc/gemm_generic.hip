@@ -117,11 +117,17 @@ __global__ void __launch_bounds__(256) gemm_staged_kernel(const T* __restrict__ 
 // outside ones read as zero.
 // Split K: workgroup z multiplies K elements [z kspan, min(K, (z + 1) kspan)) and writes its
 // product at C + z zstride (kspan a multiple of the 512-byte chunk; one split: kspan = K).
-template <typename T, bool AROW, bool BROW, typename OutT, bool EPI>
+// U8 (int8 storage, no epilogue): the bytes are unsigned.  They are flipped to s = u - 128 (XOR
+// 0x80) on their way into LDS, multiplied by the signed MFMA, and each C element gets
+// 128 (RA + CB) + 16384 Kp added, RA / CB the sums of its row's / column's flipped bytes over the
+// Kp k-values the workgroup multiplied (K padded to the 64-byte k-step: a padded byte reads 0,
+// flips to -128 in both operands, and its terms cancel), all modulo 2^32.
+template <typename T, bool AROW, bool BROW, typename OutT, bool EPI, bool U8 = false>
 __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A, const T* __restrict__ B,
                                                          OutT* __restrict__ C, int64_t M, int64_t N, int64_t K,
                                                          int64_t lda, int64_t ldb, int64_t ldc, Epilogue epi,
                                                          int64_t kspan, int64_t zstride) {
+    static_assert(!U8 || (sizeof(T) == 1 && !EPI), "the unsigned form is int8 storage without an epilogue");
     using Acc = typename Mfma16<T>::acc_elem;
     using AccV = typename Mfma16<T>::acc_t;
     constexpr int EV = 16 / (int)sizeof(T);   // elements per 16-byte chunk
@@ -168,13 +174,20 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int e = tid + 256 * i;
+            uint4 x = reg[i];
+            if constexpr (U8) {
+                x.x ^= 0x80808080u;
+                x.y ^= 0x80808080u;
+                x.z ^= 0x80808080u;
+                x.w ^= 0x80808080u;
+            }
             if constexpr (decltype(kcont)::value) {
-                *reinterpret_cast<uint4*>(S + (e >> 5) * PITCH + 16 * (e & 31)) = reg[i];
+                *reinterpret_cast<uint4*>(S + (e >> 5) * PITCH + 16 * (e & 31)) = x;
             } else if constexpr (decltype(tr)::value) {
-                *reinterpret_cast<uint4*>(S + (e / JR) * PTR + 16 * (e % JR)) = reg[i];
+                *reinterpret_cast<uint4*>(S + (e / JR) * PTR + 16 * (e % JR)) = x;
             } else {
                 const int k = e / JR, j = e % JR;
-                const T* v = reinterpret_cast<const T*>(&reg[i]);
+                const T* v = reinterpret_cast<const T*>(&x);
 #pragma unroll
                 for (int t = 0; t < EV; ++t) *reinterpret_cast<T*>(S + (EV * j + t) * PITCH + k * (int)sizeof(T)) = v[t];
             }
@@ -209,6 +222,16 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = AccV{0, 0, 0, 0};
+    // U8: this lane's sums of the flipped bytes of its fragment rows (A) and columns (B), and the
+    // k-steps multiplied
+    uint32_t usa[2] = {0u, 0u}, usb[2] = {0u, 0u};
+    int64_t usteps = 0;
+    auto bytesum = [](uint4 v, uint32_t acc) __attribute__((always_inline)) {
+        int s = __builtin_amdgcn_sdot4((int)v.x, 0x01010101, (int)acc, false);
+        s = __builtin_amdgcn_sdot4((int)v.y, 0x01010101, s, false);
+        s = __builtin_amdgcn_sdot4((int)v.z, 0x01010101, s, false);
+        return (uint32_t)__builtin_amdgcn_sdot4((int)v.w, 0x01010101, s, false);
+    };
     uint4 ra[8], rb[8];
     load(A, AK{}, lda, m0, M, kb, ra);
     load(B, BK{}, ldb, n0, N, kb, rb);
@@ -221,6 +244,7 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
             load(B, BK{}, ldb, n0, N, k0 + KC, rb);
         }
         const int64_t nks = min((int64_t)(KC / KE), (ke - k0 + KE - 1) / KE);
+        if constexpr (U8) usteps += nks;
 #pragma unroll
         for (int ks = 0; ks < KC / KE; ++ks) {
             if (ks < nks) {
@@ -230,6 +254,13 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
                     af[t] = frag(As, ATR{}, wm * 32 + t * 16, ks);
                     bf[t] = frag(Bs, BTR{}, wn * 32 + t * 16, ks);
                 }
+                if constexpr (U8) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        usa[t] = bytesum(af[t], usa[t]);
+                        usb[t] = bytesum(bf[t], usb[t]);
+                    }
+                }
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -237,6 +268,27 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
             }
         }
         __syncthreads();
+    }
+    if constexpr (U8) {
+        // lane (r, g) summed fragment row / column r over k slice g: add the four slices, so every
+        // lane holds the full sum of row (column) lane % 16 of each fragment
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            usa[t] += (uint32_t)__shfl_xor((int)usa[t], 16);
+            usa[t] += (uint32_t)__shfl_xor((int)usa[t], 32);
+            usb[t] += (uint32_t)__shfl_xor((int)usb[t], 16);
+            usb[t] += (uint32_t)__shfl_xor((int)usb[t], 32);
+        }
+        const uint32_t kconst = 16384u * (uint32_t)(usteps * KE);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t rsum = (uint32_t)__shfl((int)usa[i], 4 * (lane >> 4) + q);
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j][q] = (Acc)((uint32_t)acc[i][j][q] + 128u * (rsum + usb[j]) + kconst);
+            }
     }
     // lane holds column lane % 16 and rows 4 * (lane / 16) + q of each 16x16 tile
 #pragma unroll
@@ -372,27 +424,33 @@ LAVA_SMALL_RULE_INST(int8_t)
 #undef LAVA_SMALL_RULE_INST
 
 namespace {
-template <typename T, typename OutT, bool EPI>
+template <typename T, typename OutT, bool EPI, bool U8 = false>
 int launch_small_grid(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                       int64_t ldc, bool arow, bool brow, hipStream_t s, const Epilogue& epi, int splits,
                       int64_t kspan, int64_t zstride) {
     const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64), (unsigned)splits);
     if (arow && brow)
-        hipLaunchKernelGGL((gemm_small_kernel<T, true, true, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
-                           ldb, ldc, epi, kspan, zstride);
-    else if (arow)
-        hipLaunchKernelGGL((gemm_small_kernel<T, true, false, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
-                           ldb, ldc, epi, kspan, zstride);
-    else if (brow)
-        hipLaunchKernelGGL((gemm_small_kernel<T, false, true, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K, lda,
-                           ldb, ldc, epi, kspan, zstride);
-    else
-        hipLaunchKernelGGL((gemm_small_kernel<T, false, false, OutT, EPI>), grid, dim3(256), 0, s, A, B, C, M, N, K,
+        hipLaunchKernelGGL((gemm_small_kernel<T, true, true, OutT, EPI, U8>), grid, dim3(256), 0, s, A, B, C, M, N, K,
                            lda, ldb, ldc, epi, kspan, zstride);
-    LAVA_LAUNCH_CHECK("gemm_small_kernel");
+    else if (arow)
+        hipLaunchKernelGGL((gemm_small_kernel<T, true, false, OutT, EPI, U8>), grid, dim3(256), 0, s, A, B, C, M, N, K,
+                           lda, ldb, ldc, epi, kspan, zstride);
+    else if (brow)
+        hipLaunchKernelGGL((gemm_small_kernel<T, false, true, OutT, EPI, U8>), grid, dim3(256), 0, s, A, B, C, M, N, K,
+                           lda, ldb, ldc, epi, kspan, zstride);
+    else
+        hipLaunchKernelGGL((gemm_small_kernel<T, false, false, OutT, EPI, U8>), grid, dim3(256), 0, s, A, B, C, M, N,
+                           K, lda, ldb, ldc, epi, kspan, zstride);
+    LAVA_LAUNCH_CHECK(U8 ? "gemm_small_kernel<u8>" : "gemm_small_kernel");
     return LAVA_HIP_OK;
 }
 }  // namespace
+
+int launch_gemm_small_u8(const int8_t* A, const int8_t* B, int32_t* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                         int64_t ldb, int64_t ldc, bool arow, bool brow, hipStream_t s) {
+    return launch_small_grid<int8_t, int32_t, false, true>(A, B, C, M, N, K, lda, ldb, ldc, arow, brow, s, Epilogue{},
+                                                           1, K > 0 ? K : 1, 0);
+}
 
 template <typename T, typename OutT, bool EPI>
 int launch_gemm_small(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
@@ -427,7 +485,7 @@ template size_t small_splitk_bytes<f16>(int64_t, int64_t, const SmallSplit&);
 template size_t small_splitk_bytes<bf16>(int64_t, int64_t, const SmallSplit&);
 template size_t small_splitk_bytes<int8_t>(int64_t, int64_t, const SmallSplit&);
 
-template <typename T>
+template <typename T, bool U8>
 int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
                              int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, void* stream,
                              const SmallSplit& sp) {
@@ -435,8 +493,10 @@ int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_ele
     hipStream_t s = as_stream(stream);
     return with_stream_workspace(small_splitk_bytes<T>(M, N, sp), stream, [&](void* ws) {
         Acc* P = reinterpret_cast<Acc*>(static_cast<uint8_t*>(ws) + STREAM_WS_RESERVED);
-        int rc = launch_small_grid<T, Acc, false>(A, B, P, M, N, K, lda, ldb, N, arow, brow, s, Epilogue{}, sp.splits,
-                                                 sp.kspan, M * N);
+        // unsigned: each split's partial carries its own correction, so the wrapped sum of the
+        // partials is the product
+        int rc = launch_small_grid<T, Acc, false, U8>(A, B, P, M, N, K, lda, ldb, N, arow, brow, s, Epilogue{},
+                                                     sp.splits, sp.kspan, M * N);
         if (rc != LAVA_HIP_OK) return rc;
         if (N % 4 == 0)
             hipLaunchKernelGGL((splitk_sum_kernel<Acc, 4>), dim3((unsigned)((N + 1023) / 1024), (unsigned)M), dim3(256),
@@ -451,12 +511,14 @@ int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_ele
 template SmallSplit small_gemm_splits<f16>(int64_t, int64_t, int64_t);
 template SmallSplit small_gemm_splits<bf16>(int64_t, int64_t, int64_t);
 template SmallSplit small_gemm_splits<int8_t>(int64_t, int64_t, int64_t);
-template int launch_gemm_small_splitk<f16>(const f16*, const f16*, float*, int64_t, int64_t, int64_t, int64_t, int64_t,
-                                           int64_t, bool, bool, void*, const SmallSplit&);
-template int launch_gemm_small_splitk<bf16>(const bf16*, const bf16*, float*, int64_t, int64_t, int64_t, int64_t,
-                                            int64_t, int64_t, bool, bool, void*, const SmallSplit&);
-template int launch_gemm_small_splitk<int8_t>(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t,
-                                              int64_t, int64_t, int64_t, bool, bool, void*, const SmallSplit&);
+template int launch_gemm_small_splitk<f16, false>(const f16*, const f16*, float*, int64_t, int64_t, int64_t, int64_t,
+                                                  int64_t, int64_t, bool, bool, void*, const SmallSplit&);
+template int launch_gemm_small_splitk<bf16, false>(const bf16*, const bf16*, float*, int64_t, int64_t, int64_t,
+                                                   int64_t, int64_t, int64_t, bool, bool, void*, const SmallSplit&);
+template int launch_gemm_small_splitk<int8_t, false>(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t,
+                                                     int64_t, int64_t, int64_t, bool, bool, void*, const SmallSplit&);
+template int launch_gemm_small_splitk<int8_t, true>(const int8_t*, const int8_t*, int32_t*, int64_t, int64_t, int64_t,
+                                                    int64_t, int64_t, int64_t, bool, bool, void*, const SmallSplit&);
 
 #define LAVA_STAGED_INST(T, O, E)                                                                              \
     template int launch_gemm_staged<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t, \

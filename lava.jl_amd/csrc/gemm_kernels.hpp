@@ -41,10 +41,14 @@ SmallSplit small_gemm_splits(int64_t M, int64_t N, int64_t K);
 // Workspace bytes of a split plan: the W8A16 counter region, then one M x N partial per split.
 template <typename T>
 size_t small_splitk_bytes(int64_t M, int64_t N, const SmallSplit& sp);
-template <typename T>
+// U8: int8 storage read as unsigned bytes (uint32 results in the int32 words).
+template <typename T, bool U8 = false>
 int launch_gemm_small_splitk(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
                              int64_t lda, int64_t ldb, int64_t ldc, bool arow, bool brow, void* stream,
                              const SmallSplit& sp);
+// Unsigned bytes on the small kernel, unsplit (flipped bytes, signed MFMAs, row / column sums).
+int launch_gemm_small_u8(const int8_t* A, const int8_t* B, int32_t* C, int64_t M, int64_t N, int64_t K, int64_t lda,
+                         int64_t ldb, int64_t ldc, bool arow, bool brow, hipStream_t s);
 
 // The 16x16x16 vocabulary-tile GEMM (fp16 -> fp32); M, N, K multiples of 16.
 int launch_coopmat_tiles(const f16* A, const f16* B, float* C, int64_t M, int64_t N, int64_t K, int64_t lda,
