@@ -180,6 +180,12 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
                 x.y ^= 0x80808080u;
                 x.z ^= 0x80808080u;
                 x.w ^= 0x80808080u;
+            } else if constexpr (sizeof(T) == 1 && !decltype(kcont)::value) {
+                // an opaque use of the loaded words before their byte stores: without it the
+                // compiler holds the bytes of all 8 loads apart (256-304 VGPRs, one workgroup per
+                // CU); with it 180-192, two workgroups (int8 A column-major 64 x 14336 x 4096:
+                // 146 -> 226 TOP/s; both operands M/N-contiguous at 2048^3: 116 -> 228)
+                asm volatile("; keep" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
             }
             if constexpr (decltype(kcont)::value) {
                 *reinterpret_cast<uint4*>(S + (e >> 5) * PITCH + 16 * (e & 31)) = x;
