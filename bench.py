@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the cooperative-matrix path on one MI355X.
 
-Headline (BASELINE.json metric): the bf16 GEMM at M=N=K=8192 (A row-major,
+Headline metric: the bf16 GEMM at M=N=K=8192 (A row-major,
 B column-major, fp32 C) -- `value` is its TFLOP/s -- and the causal
 flash-attention forward at B=4, H=32, S=4096, D=128 (fp16), reported beside it
 in the same JSON line with its own roofline.  Inputs are the seeded synthetic
@@ -315,7 +315,7 @@ def cpu_baseline_gemm(n=8192, budget_s=20.0):
                       f"includes decoding B), oracle/lava_oracle.c oracle_gemm_f32acc, {dt:.1f} s"}
 
 
-# what the CPU figures are (BASELINE.md asks for the Lava/lavapipe path, which cannot run on the box)
+# what the CPU figures are: the reference's own CPU path (Lava on lavapipe) cannot run on the box
 CPU_NOTE = ("lavapipe baseline unavailable (no Julia, Mantle or Lavapipe_jll on the GPU box); not the Lava path: "
             "the build's own CPU restatement (oracle/lava_oracle.c, OpenMP over all host threads)")
 

@@ -9,7 +9,8 @@
 // would run on few CUs or mostly empty tiles (small_gemm_preferred's rate estimate), take
 // the 64 x 64 small-product kernel (with K split over the stream's workspace where its tiles
 // alone would leave CUs idle: small_gemm_splits); the rest (extents that split a 16-byte chunk) the staged
-// kernel.
+// kernel.  Unsigned bytes (lava_hip_gemm_u8_u32) take the same choice among the tile and small
+// kernels' unsigned forms, and a one-thread-per-element kernel where the staged kernel would run.
 #include <hip/hip_runtime.h>
 
 #include <type_traits>

@@ -7,7 +7,7 @@
 //    src/vocabulary/tensor.jl:46-51).  It is the fallback behind the fast TN
 //    kernel and the path for small problems.
 //  * gemm_small_kernel: the products too small to fill the chip with 256 x 256
-//    tiles (16 or fewer of them, e.g. BASELINE's 256^3 fp16 case): 64 x 64 tiles,
+//    tiles (16 or fewer of them, e.g. the 256^3 fp16 configuration): 64 x 64 tiles,
 //    K in chunks of 512 bytes loaded with 16-byte loads, all in flight at once, the
 //    next chunk arriving in registers while this one is multiplied.
 //  * coopmat_tiles_kernel: the 16x16x16 subgroup-tile GEMM written in the

@@ -1,11 +1,11 @@
 """GEMM kernels on the GPU against the oracle.
 
   * fp16/bf16: relative Frobenius error <= 1e-3 against the fp64 product of the
-    same rounded inputs (the tolerance BASELINE.json states);
+    same rounded inputs (the path's stated tolerance for 16-bit inputs);
   * int8 -> int32: bit-exact;
   * every layout combination and ragged extents through the staged kernel, and the
     small-product kernel (at most 16 tiles of 256 x 256) in every layout;
-  * the BASELINE configs at full size: 256^3 fp16 (A, B row-major), 4096^3 and
+  * the benchmark configurations at full size: 256^3 fp16 (A, B row-major), 4096^3 and
     8192^3 bf16 (A row-major, B column-major), 4096^3 int8.  At full size the
     oracle checks sampled rows exactly and a size-independent property checks
     every element: sum_ij C_ij = sum_k (sum_i A_ik)(sum_j B_kj).

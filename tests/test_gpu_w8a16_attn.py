@@ -1,5 +1,5 @@
 """W8A16 decode GEMM and causal flash-attention forward on the GPU, against the
-oracle (rel-Frobenius <= 1e-3 and <= 2e-3, the tolerances BASELINE.json states).
+oracle (rel-Frobenius <= 1e-3 and <= 2e-3, the path's stated tolerances).
 """
 from __future__ import annotations
 
