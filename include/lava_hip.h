@@ -50,6 +50,7 @@ extern "C" {
 #define LAVA_HIP_U8 4
 #define LAVA_HIP_I32 5
 #define LAVA_HIP_U32 6
+#define LAVA_HIP_F64 7
 
 /* ---- GEMM layout flags ---------------------------------------------------
  * bit0: A row-major, bit1: B row-major, bit2: C row-major; a clear bit means
@@ -215,7 +216,9 @@ int lava_hip_fill_i8(void* dst, int64_t n, uint64_t seed, int symmetric, void* s
  * A, B, C, D row-major.  `ntiles` independent tiles are processed, tile t
  * reading at offsets + t * tile_step (elements).
  * Type pairs (ab_dtype, acc_dtype): (F16, F32), (I8, I32) signed, (U8, U32)
- * unsigned (test/spirv/test_coopmat_int8.jl:25-98). */
+ * unsigned (test/spirv/test_coopmat_int8.jl:25-98), and the wide component types of the
+ * reference's coopmat table (src/device/coopmat_intrinsics.jl:16-19): (F32, F32) on four
+ * v_mfma_f32_16x16x4_f32 and (F64, F64) on four v_mfma_f64_16x16x4_f64 per tile. */
 int lava_hip_coopmat_muladd_16x16x16(int ab_dtype, int acc_dtype, const void* A, int64_t offA, int64_t strideA,
                                      const void* B, int64_t offB, int64_t strideB, const void* C, int64_t offC,
                                      int64_t strideC, void* D, int64_t offD, int64_t strideD, uint32_t layout,

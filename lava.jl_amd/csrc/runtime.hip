@@ -463,6 +463,7 @@ static const int32_t kShapes[][5] = {
     {LAVA_HIP_I8, LAVA_HIP_I32, 16, 16, 32},  {LAVA_HIP_I8, LAVA_HIP_I32, 16, 16, 64},
     {LAVA_HIP_I8, LAVA_HIP_I32, 32, 32, 16},  {LAVA_HIP_I8, LAVA_HIP_I32, 32, 32, 32},
     {LAVA_HIP_F32, LAVA_HIP_F32, 16, 16, 4},  {LAVA_HIP_F32, LAVA_HIP_F32, 32, 32, 2},
+    {LAVA_HIP_F64, LAVA_HIP_F64, 16, 16, 4},
 };
 
 int lava_hip_matrix_shapes(int32_t* out, int max_rows, int* count) {

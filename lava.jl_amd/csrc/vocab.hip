@@ -59,6 +59,39 @@ __global__ void __launch_bounds__(64) muladd_tile_u8_kernel(const uint8_t* A, in
     store(D + t * tile_step, strideD, (layout & 8u) != 0, c);
 }
 
+// fp32 and fp64 operands: a 16x16x16 tile is four 16x16x4 MFMAs.  Lane (r, g) = (lane % 16,
+// lane / 16) supplies A[r][4 s + g] and B[4 s + g][r] to step s.  Its accumulator element i is
+// C[4 g + i][r] for fp32 (the layout of the other 16x16 MFMAs) but C[g + 4 i][r] for fp64 (the
+// 16x16x4 fp64 MFMA interleaves its rows; measured, and pinned by the identity-product tests).
+template <typename T>
+__global__ void __launch_bounds__(64) muladd_tile_wide_kernel(const T* A, int64_t strideA, const T* B,
+                                                              int64_t strideB, const T* C, int64_t strideC, T* D,
+                                                              int64_t strideD, uint32_t layout, int64_t tile_step) {
+    typedef T v4 __attribute__((ext_vector_type(4)));
+    const int64_t t = blockIdx.x;
+    const T* a_p = A + t * tile_step;
+    const T* b_p = B + t * tile_step;
+    const T* c_p = C + t * tile_step;
+    T* d_p = D + t * tile_step;
+    const int lane = lane_id(), r = lane & 15, g = lane >> 4;
+    const bool arow = layout & 1u, brow = layout & 2u, crow = layout & 4u, drow = layout & 8u;
+    v4 acc;
+    auto row = [&](int i) { return sizeof(T) == 8 ? g + 4 * i : 4 * g + i; };
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = c_p[tile_index(row(i), r, strideC, crow)];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const T a = a_p[tile_index(r, 4 * st + g, strideA, arow)];
+        const T b = b_p[tile_index(4 * st + g, r, strideB, brow)];
+        if constexpr (sizeof(T) == 8)
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc, 0, 0, 0);
+        else
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) d_p[tile_index(row(i), r, strideD, drow)] = acc[i];
+}
+
 // ---- per-element callbacks ---------------------------------------------------
 // The known-answer callback of test/spirv/test_coopmat_perelement_inline.jl:20,
 // which depends on both indices and is not symmetric under swapping them.
@@ -317,6 +350,7 @@ static size_t dtype_size(int dt) {
     case LAVA_HIP_BF16: return 2;
     case LAVA_HIP_I8:
     case LAVA_HIP_U8: return 1;
+    case LAVA_HIP_F64: return 8;
     default: return 4;
     }
 }
@@ -334,9 +368,11 @@ int lava_hip_coopmat_muladd_16x16x16(int ab_dtype, int acc_dtype, const void* A,
     const bool is_f16 = ab_dtype == LAVA_HIP_F16 && acc_dtype == LAVA_HIP_F32;
     const bool is_i8 = ab_dtype == LAVA_HIP_I8 && acc_dtype == LAVA_HIP_I32;
     const bool is_u8 = ab_dtype == LAVA_HIP_U8 && acc_dtype == LAVA_HIP_U32;
-    LAVA_REQUIRE(is_f16 || is_i8 || is_u8, LAVA_HIP_ERR_UNSUPPORTED,
-                 "coopmat_muladd_16x16x16: type pair (%d, %d) is not (F16,F32), (I8,I32) or (U8,U32)", ab_dtype,
-                 acc_dtype);
+    const bool is_f32 = ab_dtype == LAVA_HIP_F32 && acc_dtype == LAVA_HIP_F32;
+    const bool is_f64 = ab_dtype == LAVA_HIP_F64 && acc_dtype == LAVA_HIP_F64;
+    LAVA_REQUIRE(is_f16 || is_i8 || is_u8 || is_f32 || is_f64, LAVA_HIP_ERR_UNSUPPORTED,
+                 "coopmat_muladd_16x16x16: type pair (%d, %d) is not (F16,F32), (I8,I32), (U8,U32), (F32,F32) or "
+                 "(F64,F64)", ab_dtype, acc_dtype);
     LAVA_ARG(ntiles >= 0 && ntiles <= 0x7fffffff, "coopmat_muladd_16x16x16: ntiles = %lld out of range",
              (long long)ntiles);
     if (ntiles == 0) return LAVA_HIP_OK;
@@ -362,6 +398,14 @@ int lava_hip_coopmat_muladd_16x16x16(int ab_dtype, int acc_dtype, const void* A,
         hipLaunchKernelGGL((muladd_tile_kernel<int8_t, int32_t>), dim3((unsigned)ntiles), dim3(64), 0, s,
                            (const int8_t*)a, strideA, (const int8_t*)b, strideB, (const int32_t*)c, strideC,
                            (int32_t*)d, strideD, layout, tile_step);
+    else if (is_f32)
+        hipLaunchKernelGGL(muladd_tile_wide_kernel<float>, dim3((unsigned)ntiles), dim3(64), 0, s, (const float*)a,
+                           strideA, (const float*)b, strideB, (const float*)c, strideC, (float*)d, strideD, layout,
+                           tile_step);
+    else if (is_f64)
+        hipLaunchKernelGGL(muladd_tile_wide_kernel<double>, dim3((unsigned)ntiles), dim3(64), 0, s, (const double*)a,
+                           strideA, (const double*)b, strideB, (const double*)c, strideC, (double*)d, strideD, layout,
+                           tile_step);
     else
         hipLaunchKernelGGL(muladd_tile_u8_kernel, dim3((unsigned)ntiles), dim3(64), 0, s, (const uint8_t*)a, strideA,
                            (const uint8_t*)b, strideB, (const uint32_t*)c, strideC, (uint32_t*)d, strideD, layout,

@@ -18,7 +18,7 @@ ERR_HIP = -3
 ERR_NO_DEVICE = -4
 
 # element type codes
-F16, BF16, F32, I8, U8, I32, U32 = 0, 1, 2, 3, 4, 5, 6
+F16, BF16, F32, I8, U8, I32, U32, F64 = 0, 1, 2, 3, 4, 5, 6, 7
 ACT_NONE, ACT_RELU, ACT_GELU_TANH, ACT_GELU_ERF = 0, 1, 2, 3
 
 A_ROWMAJOR, B_ROWMAJOR, C_ROWMAJOR = 1, 2, 4

@@ -29,6 +29,7 @@ DTYPES = {
     "u8": (_lib.U8, np.dtype(np.uint8)),
     "i32": (_lib.I32, np.dtype(np.int32)),
     "u32": (_lib.U32, np.dtype(np.uint32)),
+    "f64": (_lib.F64, np.dtype(np.float64)),
 }
 
 
@@ -85,7 +86,8 @@ class HIPDeviceArray:
     def from_numpy(cls, a: np.ndarray, dtype: str | None = None, order: str = "F") -> "HIPDeviceArray":
         if dtype is None:
             dtype = {np.dtype(np.float16): "f16", np.dtype(np.float32): "f32", np.dtype(np.int8): "i8",
-                     np.dtype(np.uint8): "u8", np.dtype(np.int32): "i32", np.dtype(np.uint32): "u32"}.get(a.dtype)
+                     np.dtype(np.uint8): "u8", np.dtype(np.int32): "i32", np.dtype(np.uint32): "u32",
+                     np.dtype(np.float64): "f64"}.get(a.dtype)
             if dtype is None:
                 raise ValueError(f"pass dtype= for numpy dtype {a.dtype}")
         out = cls(dtype, a.shape, order)

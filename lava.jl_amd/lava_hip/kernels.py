@@ -179,7 +179,8 @@ def coopmat_muladd_16x16x16(ab: str, acc: str, A: int, offA: int, strideA: int, 
                             ntiles: int = 1, tile_step: int = 0, stream: Optional[int] = None) -> None:
     """`copyto!(D, offD, strideD, muladd(a, b, c))` over 1-based offsets and element
     strides; layout bits 0..3 mark A, B, C, D row-major."""
-    codes = {"f16": _lib.F16, "f32": _lib.F32, "i8": _lib.I8, "i32": _lib.I32, "u8": _lib.U8, "u32": _lib.U32}
+    codes = {"f16": _lib.F16, "f32": _lib.F32, "i8": _lib.I8, "i32": _lib.I32, "u8": _lib.U8, "u32": _lib.U32,
+             "f64": _lib.F64}
     _lib.call("lava_hip_coopmat_muladd_16x16x16", codes[ab], codes[acc], A, offA, strideA, B, offB, strideB, Cp,
               offC, strideC, D, offD, strideD, layout, ntiles, tile_step, stream)
 

@@ -65,7 +65,7 @@ class CoopMatReduce:
 
 
 # dtype names <-> liblava_hip.so codes
-_CODE_NAMES = {0: "f16", 1: "bf16", 2: "f32", 3: "i8", 4: "u8", 5: "i32", 6: "u32"}
+_CODE_NAMES = {0: "f16", 1: "bf16", 2: "f32", 3: "i8", 4: "u8", 5: "i32", 6: "u32", 7: "f64"}
 
 
 # ---- MatrixShape (src/vocabulary/matrix.jl:88-113) -----------------------------

@@ -48,6 +48,24 @@ def test_muladd_i8_golden_tile(gpu, golden):
     np.testing.assert_array_equal(d.to_numpy().reshape(16, 16, order="F"), golden["i8_min_c"])
 
 
+@pytest.mark.parametrize("dt", ["f32", "f64"])
+def test_muladd_wide_identity_pins_layouts(gpu, dt):
+    """fp32 / fp64 tiles: A . I + C and I . B + C are exact (every product is by 1 or 0), so they
+    pin A's and B's lane layouts independently, bit for bit: a transposed operand read would give
+    the transpose, a wrong k slot a zero column.  A non-symmetric M (16 r + c) is used for both."""
+    lh = gpu
+    announce(f"muladd_16x16x16 {dt} identity products")
+    ft = np.float32 if dt == "f32" else np.float64
+    m = (16 * np.arange(16)[:, None] + np.arange(16)[None, :]).astype(ft)   # m[r][c] = 16 r + c
+    eye = np.eye(16, dtype=ft)
+    c = (np.arange(256).reshape(16, 16) * 0.5).astype(ft)
+    for a, b, want in ((m, eye, m + c), (eye, m, m + c)):
+        da, db, dc = flat(lh, a.ravel(order="F"), dt), flat(lh, b.ravel(order="F"), dt), flat(lh, c.ravel(order="F"), dt)
+        dd = flat(lh, np.zeros(256, ft), dt)
+        lh.coopmat_muladd_16x16x16(dt, dt, da.ptr, 1, 16, db.ptr, 1, 16, dc.ptr, 1, 16, dd.ptr, 1, 16, layout=0)
+        np.testing.assert_array_equal(dd.to_numpy().reshape(16, 16, order="F"), want)
+
+
 def test_muladd_u8_is_unsigned(gpu, golden):
     lh = gpu
     announce("muladd_16x16x16 u8")
@@ -63,7 +81,7 @@ def test_muladd_u8_is_unsigned(gpu, golden):
 
 
 @pytest.mark.parametrize("layout", range(16))
-@pytest.mark.parametrize("ab,acc", [("f16", "f32"), ("i8", "i32"), ("u8", "u32")])
+@pytest.mark.parametrize("ab,acc", [("f16", "f32"), ("i8", "i32"), ("u8", "u32"), ("f32", "f32"), ("f64", "f64")])
 def test_muladd_layouts_offsets_strides(gpu, oracle, layout, ab, acc):
     """Tiles read at 1-based offsets inside larger arrays with padded strides, in
     every row/column-major combination of A, B, C, D, several tiles per call."""
@@ -73,11 +91,12 @@ def test_muladd_layouts_offsets_strides(gpu, oracle, layout, ab, acc):
     ntiles, stride, off = 3, 24, 5
     step = stride * 16 + 7
     total = off + step * ntiles + stride * 16
-    if ab == "f16":
-        A = rng.uniform(-1, 1, total).astype(np.float16)
-        B = rng.uniform(-1, 1, total).astype(np.float16)
-        Cin = rng.uniform(-1, 1, total).astype(np.float32)
-        outdt = np.float32
+    if ab in ("f16", "f32", "f64"):
+        ft = {"f16": np.float16, "f32": np.float32, "f64": np.float64}[ab]
+        A = rng.uniform(-1, 1, total).astype(ft)
+        B = rng.uniform(-1, 1, total).astype(ft)
+        outdt = np.float64 if ab == "f64" else np.float32
+        Cin = rng.uniform(-1, 1, total).astype(outdt)
     elif ab == "i8":
         A = rng.integers(-128, 128, total).astype(np.int8)
         B = rng.integers(-128, 128, total).astype(np.int8)
@@ -105,9 +124,12 @@ def test_muladd_layouts_offsets_strides(gpu, oracle, layout, ab, acc):
         b = tile(B, off + t * step, layout & 2)
         c = tile(Cin, off + 1 + t * step, layout & 4)
         d = tile(D, off + 2 + t * step, layout & 8)
-        if ab == "f16":
+        if ab in ("f16", "f32"):
             ref = a.astype(np.float64) @ b.astype(np.float64) + c.astype(np.float64)
             np.testing.assert_allclose(d, ref, rtol=1e-5, atol=1e-5)
+        elif ab == "f64":
+            ref = a @ b + c
+            np.testing.assert_allclose(d, ref, rtol=1e-13, atol=1e-13)
         else:
             ref = (a.astype(np.int64) @ b.astype(np.int64) + c.astype(np.int64)).astype(outdt)
             np.testing.assert_array_equal(d, ref)

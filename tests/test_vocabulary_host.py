@@ -58,6 +58,8 @@ def test_gfx950_table_answers():
     assert lh.bestshape(table, "bf16", "f32") == S("bf16", "f32", 16, 16, 16)
     assert lh.bestshape(table, "i8", "i32") == S("i8", "i32", 32, 32, 32)
     assert lh.bestshape(table, "u8", "u32") is None   # CDNA4 has no unsigned MFMA
+    assert lh.bestshape(table, "f64", "f64") == S("f64", "f64", 16, 16, 4)
+    assert lh.bestshape(table, "f32", "f32") == S("f32", "f32", 16, 16, 4)
     assert lh.supports_coopmat_perelement() and lh.supports_coopmat_reduce()
     assert lh.CoopMatReduce.Row == 1 and lh.CoopMatReduce.RowAndColumn == 3
 
