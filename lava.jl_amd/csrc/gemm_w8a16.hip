@@ -30,6 +30,7 @@
 #include <map>
 #include <mutex>
 #include <set>
+#include <type_traits>
 #include <vector>
 
 #include "lava_coopmat.hpp"
@@ -253,17 +254,19 @@ __global__ void __launch_bounds__(64 * W8_WAVES) w8a16_kernel(const f16* __restr
 // kernel cannot stage is copied row-major by the host first).  Each column's dot product streams
 // contiguous memory, so a workgroup takes whole columns over all of K -- no split across
 // workgroups, no exchange:
-//  * a workgroup owns KM_COLS = 32 columns (two 16 x 16 MFMA tiles) of one 16-row block of X;
-//    its KM_KSPLIT = 2 wavefronts take half of K each and are added through LDS at the end;
+//  * a workgroup owns KM_COLS = 32 columns (two 16 x 16 MFMA tiles) of MB = 1, 2 or 4 16-row
+//    blocks of X (MB by M: each dequantized W fragment feeds MB MFMAs, so W is streamed once per
+//    16 MB rows); its KM_KSPLIT = 2 wavefronts take half of K each and are added through LDS at the end;
 //  * a wavefront streams its 32 columns in stages of KM_SEG = 128 k: W (32 columns x 128 bytes)
-//    and X (16 rows x 256 bytes) go straight into the wavefront's own LDS ring of KM_BUFS = 4
+//    and X (16 MB rows x 256 bytes) go straight into the wavefront's own LDS ring of 4, 3 or 2
 //    stages (LDS DMA, one 128-byte run of a column per 8 lanes -- HBM serves 128-byte runs of a
 //    column at ~4.8 TB/s against ~3.4 for the 64-byte runs a direct MFMA-layout load would
 //    make), waited for with vmcnt: no barriers between wavefronts.  A stage's buffer is refilled
 //    as soon as its fragments are in registers, before its MFMAs.  W's DMA carries the
 //    nontemporal hint (W is read once; ~7 % faster);
-//  * 68 KB of LDS per workgroup holds the chip to two workgroups per CU, which spreads a grid
-//    of a few hundred workgroups evenly (a third per CU, from a shallower ring, measured slower);
+//  * 64, 72 or 80 KB of LDS per workgroup holds the chip to two workgroups per CU, which spreads
+//    a grid of a few hundred workgroups evenly (a third per CU, from a shallower ring, measured
+//    slower at MB = 1);
 //  * LDS rows are XOR-swizzled (16-byte slot = chunk ^ row) so the fragment reads of 16 rows hit
 //    distinct banks;
 //  * per 64 k, lane (n, g) = (lane % 16, lane / 16) reads 16 bytes of column n0 + 16 t + n at
@@ -280,12 +283,20 @@ constexpr int KM_KSPLIT = 2;                      // wavefronts side by side in 
 constexpr int KM_WAVES = KM_CG * KM_KSPLIT;
 constexpr int KM_WCOLS = 16 * KM_TILES;           // columns per wavefront
 constexpr int KM_COLS = KM_WCOLS * KM_CG;         // columns per workgroup
-constexpr int KM_BUFS = 4;                        // stage ring per wavefront
-static_assert(KM_BUFS >= 1 && KM_BUFS <= 6, "the vmcnt waits cover up to 5 later stages");
 constexpr int KM_SEG = 128;                       // k per stage
 constexpr int KM_W_INSTR = KM_WCOLS / 8;          // W DMA instructions per stage (8 columns each)
-constexpr int KM_X_INSTR = 16 / 4;                // X DMA instructions per stage (4 rows each)
-constexpr int KM_STAGE_BYTES = KM_WCOLS * KM_SEG + 16 * KM_SEG * 2;
+// MB 16-row blocks of X per workgroup (1, 2 or 4): each dequantized W fragment feeds MB MFMAs, so
+// W is streamed once per 16 MB rows.  The stage ring is shallower as X's share of a stage grows,
+// keeping two workgroups per CU (64, 72, 80 KB of LDS).
+template <int MB>
+struct KmCfg {
+    static_assert(MB == 1 || MB == 2 || MB == 4, "1, 2 or 4 row blocks");
+    static constexpr int BUFS = MB == 1 ? 4 : (MB == 2 ? 3 : 2);          // stage ring per wavefront
+    static constexpr int X_INSTR = 4 * MB;                                 // X DMA instructions (4 rows each)
+    static constexpr int STAGE = KM_WCOLS * KM_SEG + 16 * MB * KM_SEG * 2;  // W, then X
+    static_assert(BUFS >= 1 && BUFS <= 6, "the vmcnt waits cover up to 5 later stages");
+    static_assert(BUFS * STAGE >= MB * KM_TILES * 64 * 16, "the K-range sums reuse a wavefront's ring");
+};
 
 // 8 int8 weights (two dwords, k ascending) -> the 8 fp16 values of a B operand
 __device__ __forceinline__ f16x8 km_dequant(uint32_t lo, uint32_t hi) {
@@ -310,21 +321,23 @@ __device__ __forceinline__ int km_xline(int L) { return L ^ ((L >> 2) & 4); }
 typedef short km_s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) km_s16x4 km_lds_s16x4;
 
-template <bool XROW, bool YROW>
+template <bool XROW, bool YROW, int MB>
 __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* __restrict__ X,
                                                                       const int8_t* __restrict__ W,
                                                                       const f16* __restrict__ scale,
                                                                       float* __restrict__ Y, int M, int N, int K,
                                                                       int64_t ldx, int64_t ldw, int64_t ldy) {
-    // per wavefront: a ring of stage buffers, each W [32 columns][128 bytes] then X (4 KB)
-    __shared__ __attribute__((aligned(16))) uint8_t stage_buf[KM_WAVES][KM_BUFS][KM_STAGE_BYTES];
-    __shared__ __attribute__((aligned(16))) f32x4 red[KM_KSPLIT][KM_CG * KM_TILES][64];
+    using Cfg = KmCfg<MB>;
+    constexpr int KM_BUFS = Cfg::BUFS;
+    // per wavefront: a ring of stage buffers, each W [32 columns][128 bytes] then X (4 KB per
+    // 16-row block)
+    __shared__ __attribute__((aligned(16))) uint8_t stage_buf[KM_WAVES][KM_BUFS][Cfg::STAGE];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int cg = w % KM_CG, ks = w / KM_CG;         // column group, K range
     const int q = lane & 15, g = lane >> 4;
     // this wavefront's columns start at n0 (the last block may pass N)
     const int n0 = blockIdx.x * KM_COLS + cg * KM_WCOLS;
-    const int m0 = blockIdx.y * 16;
+    const int m0 = blockIdx.y * 16 * MB;
     const int stages = (K + KM_SEG - 1) / KM_SEG;
     const int per = (stages + KM_KSPLIT - 1) / KM_KSPLIT;
     const int s_begin = min(stages, ks * per), s_end = min(stages, s_begin + per);
@@ -335,15 +348,16 @@ __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* 
     const v4i w_rs = make_rsrc(W + (int64_t)n0 * ldw, (uint32_t)(max(0, min(KM_WCOLS, N - n0)) * ldw));
     // (X column-major: the host keeps M a multiple of 8, so a 16-byte chunk of 8 rows is wholly
     // inside or wholly past M)
-    const v4i x_rs = XROW ? make_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(16 * ldx * 2))
+    const v4i x_rs = XROW ? make_rsrc(X + (int64_t)m0 * ldx, (uint32_t)(16 * MB * ldx * 2))
                           : make_rsrc(X + m0, (uint32_t)(K * ldx * 2));
     // W instruction i, lane l: column 8 i + l / 8, slot l % 8 holding chunk slot ^ (column % 8)
     // X row-major, instruction j, lane l: row 4 j + l / 16, slot l % 16 holding chunk slot ^ (row % 16)
-    // X column-major, instruction j, lane l: LDS line 32 j + l / 2 (holding k-line km_xline of it),
-    // rows 8 (l % 2) .. + 7
+    // X column-major, instruction j = 4 b + jj, lane l: row block b's LDS line 32 jj + l / 2 (holding
+    // k-line km_xline of it), rows 16 b + 8 (l % 2) .. + 7
+    // (either way instruction j fills the 1 KB at X + 1024 j of the stage: block b at 4 KB b)
     const int wc_lo = lane >> 3, w_slot = lane & 7;
     const int xr_lo = lane >> 4, x_slot = lane & 15;
-    const int rows_ok = min(16, M - m0);
+    const int rows_ok = min(16 * MB, M - m0);
     auto issue = [&](int st, int buf) {
         const int k0 = st * KM_SEG;                   // first k of the stage
         const uint32_t lds0 = lds_addr(&stage_buf[w][buf][0]);
@@ -355,28 +369,30 @@ __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* 
             dma16_stream(w_rs, off, 0, lds0 + 1024 * i);   // W is read once
         }
 #pragma unroll
-        for (int j = 0; j < KM_X_INSTR; ++j) {
+        for (int j = 0; j < Cfg::X_INSTR; ++j) {
             uint32_t off;
             if constexpr (XROW) {
                 const int row = 4 * j + xr_lo;
                 const int kx = k0 + 8 * (x_slot ^ (row & 15));
                 off = (kx < K && row < rows_ok) ? (uint32_t)(row * ldx * 2 + 2 * kx) : OOB_OFS;
             } else {
-                const int kx = k0 + km_xline(32 * j + (lane >> 1));
-                const int row = 8 * (lane & 1);
+                const int kx = k0 + km_xline(32 * (j & 3) + (lane >> 1));
+                const int row = 16 * (j >> 2) + 8 * (lane & 1);
                 off = (kx < K && row < rows_ok) ? (uint32_t)((kx * ldx + row) * 2) : OOB_OFS;
             }
             dma16(x_rs, off, 0, lds0 + KM_WCOLS * KM_SEG + 1024 * j);
         }
     };
 
-    f32x4 acc[KM_TILES];
+    f32x4 acc[MB][KM_TILES];
 #pragma unroll
-    for (int t = 0; t < KM_TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < MB; ++b)
+#pragma unroll
+        for (int t = 0; t < KM_TILES; ++t) acc[b][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int b = 0; b < KM_BUFS; ++b)
         if (b < nst) issue(s_begin + b, b);
-    constexpr int PER_STAGE = KM_W_INSTR + KM_X_INSTR;   // DMA instructions
+    constexpr int PER_STAGE = KM_W_INSTR + Cfg::X_INSTR;   // DMA instructions
     for (int s = 0; s < nst; ++s) {
         // this stage's DMA done; the later stages issued (up to KM_BUFS - 1) may be in flight
         const int later = min(KM_BUFS - 1, nst - 1 - s);
@@ -395,27 +411,33 @@ __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* 
         const int buf = s % KM_BUFS;
         const uint8_t* wb = &stage_buf[w][buf][0];
         const uint8_t* xb = wb + KM_WCOLS * KM_SEG;
-        // the stage's fragments into registers; X row q, k 64 h + 16 g .. + 15 is fp16 chunks
-        // 8 h + 2 g and + 1, W column 16 t + q at k 64 h + 16 g is chunk 4 h + g
-        f16x8 xf[2][2];
+        // the stage's fragments into registers; X row q of block b, k 64 h + 16 g .. + 15 is fp16
+        // chunks 8 h + 2 g and + 1, W column 16 t + q at k 64 h + 16 g is chunk 4 h + g
+        f16x8 xf[MB][2][2];
         uint4 wf[2][KM_TILES];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            if constexpr (XROW) {
-                const int c0 = 8 * h + 2 * g;
-                xf[h][0] = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * (c0 ^ q));
-                xf[h][1] = *reinterpret_cast<const f16x8*>(xb + 256 * q + 16 * ((c0 + 1) ^ q));
-            } else {
-                // lines 64 h + 16 g + 4 p + jj for the p-th group of 4 k-values
-                const int jj = (lane & 15) >> 2, r4 = lane & 3;
-                km_s16x4 v[4];
 #pragma unroll
-                for (int pp = 0; pp < 4; ++pp)
-                    v[pp] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (km_lds_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(
-                            xb + 32 * km_xline(64 * h + 16 * g + 4 * pp + jj) + 8 * r4));
-                xf[h][0] = __builtin_bit_cast(f16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
-                xf[h][1] = __builtin_bit_cast(f16x8, __builtin_shufflevector(v[2], v[3], 0, 1, 2, 3, 4, 5, 6, 7));
+            for (int b = 0; b < MB; ++b) {
+                const uint8_t* xbb = xb + 4096 * b;
+                if constexpr (XROW) {
+                    const int c0 = 8 * h + 2 * g;
+                    xf[b][h][0] = *reinterpret_cast<const f16x8*>(xbb + 256 * q + 16 * (c0 ^ q));
+                    xf[b][h][1] = *reinterpret_cast<const f16x8*>(xbb + 256 * q + 16 * ((c0 + 1) ^ q));
+                } else {
+                    // lines 64 h + 16 g + 4 p + jj for the p-th group of 4 k-values
+                    const int jj = (lane & 15) >> 2, r4 = lane & 3;
+                    km_s16x4 v[4];
+#pragma unroll
+                    for (int pp = 0; pp < 4; ++pp)
+                        v[pp] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (km_lds_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(
+                                xbb + 32 * km_xline(64 * h + 16 * g + 4 * pp + jj) + 8 * r4));
+                    xf[b][h][0] =
+                        __builtin_bit_cast(f16x8, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+                    xf[b][h][1] =
+                        __builtin_bit_cast(f16x8, __builtin_shufflevector(v[2], v[3], 0, 1, 2, 3, 4, 5, 6, 7));
+                }
             }
 #pragma unroll
             for (int t = 0; t < KM_TILES; ++t) {
@@ -432,35 +454,48 @@ __global__ void __launch_bounds__(64 * KM_WAVES) w8a16_kmajor_kernel(const f16* 
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int t = 0; t < KM_TILES; ++t) {
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[h][0], km_dequant(wf[h][t].x, wf[h][t].y), acc[t],
-                                                                0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[h][1], km_dequant(wf[h][t].z, wf[h][t].w), acc[t],
-                                                                0, 0, 0);
+                const f16x8 w0 = km_dequant(wf[h][t].x, wf[h][t].y), w1 = km_dequant(wf[h][t].z, wf[h][t].w);
+#pragma unroll
+                for (int b = 0; b < MB; ++b) {
+                    acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[b][h][0], w0, acc[b][t], 0, 0, 0);
+                    acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xf[b][h][1], w1, acc[b][t], 0, 0, 0);
+                }
             }
     }
-    // the K quarters added in order through LDS; the first wavefront finishes
+    // the K ranges added in order through LDS: every other wavefront leaves its sums in its own
+    // stage ring (its DMAs all landed at its last stage's wait, its reads all returned), and the
+    // first wavefront adds them to its own and finishes
+    auto red = [&](int wave, int b, int t) -> f32x4* {
+        return reinterpret_cast<f32x4*>(&stage_buf[wave][0][0]) + (b * KM_TILES + t) * 64 + lane;
+    };
+    if (ks != 0) {
 #pragma unroll
-    for (int t = 0; t < KM_TILES; ++t) red[ks][cg * KM_TILES + t][lane] = acc[t];
+        for (int b = 0; b < MB; ++b)
+#pragma unroll
+            for (int t = 0; t < KM_TILES; ++t) *red(w, b, t) = acc[b][t];
+    }
     __syncthreads();
     if (ks != 0) return;
-    // acc[t] lane holds column n0 + 16 t + q and rows m0 + 4 g + j: the dequant scale by the
-    // per-element callback with the scale pointer in `extras`
+    // acc[b][t] lane holds column n0 + 16 t + q and rows m0 + 16 b + 4 g + j: the dequant scale by
+    // the per-element callback with the scale pointer in `extras`
 #pragma unroll
-    for (int t = 0; t < KM_TILES; ++t) {
-        f32x4 sum = red[0][cg * KM_TILES + t][lane];
+    for (int b = 0; b < MB; ++b)
 #pragma unroll
-        for (int r = 1; r < KM_KSPLIT; ++r) sum += red[r][cg * KM_TILES + t][lane];
-        Frag<float, 16, 16, Accumulator> f;
+        for (int t = 0; t < KM_TILES; ++t) {
+            f32x4 sum = acc[b][t];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) f.v[j] = sum[j];
-        f = perelement(ScaleStridedBounded<1>{}, f, scale, (uint32_t)(n0 + 16 * t), (uint32_t)N);
-        const int col = n0 + 16 * t + q;
+            for (int r = 1; r < KM_KSPLIT; ++r) sum += *red(r * KM_CG + cg, b, t);
+            Frag<float, 16, 16, Accumulator> f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = m0 + 4 * g + j;
-            if (row < M && col < N) Y[YROW ? (int64_t)row * ldy + col : row + (int64_t)col * ldy] = f.v[j];
+            for (int j = 0; j < 4; ++j) f.v[j] = sum[j];
+            f = perelement(ScaleStridedBounded<1>{}, f, scale, (uint32_t)(n0 + 16 * t), (uint32_t)N);
+            const int col = n0 + 16 * t + q;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = m0 + 16 * b + 4 * g + j;
+                if (row < M && col < N) Y[YROW ? (int64_t)row * ldy + col : row + (int64_t)col * ldy] = f.v[j];
+            }
         }
-    }
 }
 
 // A column-major X (element (m, k) at k ldx + m) copied row-major with leading dimension K,
@@ -508,6 +543,7 @@ struct W8Plan {
     // copied row-major into the workspace, after the counter region
     bool x_copy = false;
     int splits = 1;
+    int mb = 1;                  // W8_KMAJOR: 16-row blocks of X per workgroup
     int ksteps = 0;              // the per-wavefront step count of an unrolled instance, or 0
     // split-K workspace (W8_SPLIT with splits > 1): the arrival counters (one per column and
     // row block, zero between calls) in the first counter_bytes, then the partial blocks
@@ -540,11 +576,15 @@ static W8Plan plan_w8a16(const void* X, const void* W, int64_t M, int64_t N, int
         ldw >= K && ldw <= (int64_t(1) << 31) / KM_WCOLS && aligned(W, 16) && N <= 0x7fffffff && M <= 0x7fffffff &&
         (M + 15) / 16 <= 65535) {
         p.path = W8_KMAJOR;
-        p.mblocks = (M + 15) / 16;
         p.cblocks = (N + KM_COLS - 1) / KM_COLS;
         p.xrow = x_ok ? xrow : true;
         p.yrow = layout & 4u;
         p.kldx = x_ok ? kldx : K;
+        // row blocks per workgroup: W streamed once per 16 mb rows (a row-major X's buffer range,
+        // 32 mb rows of ldx elements, must stay below 4 GB)
+        p.mb = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+        while (p.mb > 1 && p.xrow && 32 * p.mb * p.kldx >= (int64_t(1) << 32)) p.mb /= 2;
+        p.mblocks = (M + 16 * p.mb - 1) / (16 * p.mb);
         if (!x_ok) {
             p.x_copy = true;
             p.counter_bytes = W8_COUNTER_BYTES;
@@ -633,11 +673,20 @@ static int launch_w8a16(const W8Plan& p, const void* X, const void* W, const voi
                                (const int8_t*)W, (const f16*)scale, (float*)Y, (int)M, (int)N, (int)K, p.kldx, ldw,
                                ldy);
         };
+        auto by_mb = [&](auto xr, auto yr) {
+            constexpr bool XR = decltype(xr)::value, YR = decltype(yr)::value;
+            if (p.mb == 4) go(w8a16_kmajor_kernel<XR, YR, 4>);
+            else if (p.mb == 2) go(w8a16_kmajor_kernel<XR, YR, 2>);
+            else go(w8a16_kmajor_kernel<XR, YR, 1>);
+        };
+        typedef std::integral_constant<bool, true> T_;
+        typedef std::integral_constant<bool, false> F_;
         if (p.xrow)
-            p.yrow ? go(w8a16_kmajor_kernel<true, true>) : go(w8a16_kmajor_kernel<true, false>);
+            p.yrow ? by_mb(T_{}, T_{}) : by_mb(T_{}, F_{});
         else
-            p.yrow ? go(w8a16_kmajor_kernel<false, true>) : go(w8a16_kmajor_kernel<false, false>);
-        LAVA_LAUNCH_CHECK("w8a16_kmajor_kernel");
+            p.yrow ? by_mb(F_{}, T_{}) : by_mb(F_{}, F_{});
+        LAVA_LAUNCH_CHECK(p.mb == 1 ? "w8a16_kmajor_kernel" : (p.mb == 2 ? "w8a16_kmajor_kernel<mb2>"
+                                                                          : "w8a16_kmajor_kernel<mb4>"));
         return LAVA_HIP_OK;
     }
     // any layout, any shape

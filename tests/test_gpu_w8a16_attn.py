@@ -211,6 +211,24 @@ def test_w8a16_weights_column_major_orders(gpu, oracle, M, N, K, xo, yo):
     w8a16_column_major_case(gpu, oracle, M, N, K, xo, yo)
 
 
+@pytest.mark.parametrize("M,N,K,xo,yo,kernel", [
+    # two 16-row blocks per workgroup (the second partial); row- and column-major X
+    (17, 2048, 1024, "C", "C", "w8a16_kmajor_kernel<mb2>"), (32, 2048, 4096, "F", "F", "w8a16_kmajor_kernel<mb2>"),
+    # four: a partial group of three blocks, a ragged last stage, the headline N, two and four groups
+    (33, 1024, 1040, "C", "F", "w8a16_kmajor_kernel<mb4>"), (48, 4096, 4096, "F", "C", "w8a16_kmajor_kernel<mb4>"),
+    (64, 14336, 4096, "C", "C", "w8a16_kmajor_kernel<mb4>"), (128, 4096, 4096, "F", "F", "w8a16_kmajor_kernel<mb4>"),
+    (256, 2048, 4096, "C", "C", "w8a16_kmajor_kernel<mb4>"),
+    # M not a multiple of 8 with X column-major: X copied row-major first, a last group of one row
+    (65, 512, 4096, "F", "F", "w8a16_kmajor_kernel<mb4>"), (100, 2048, 2048, "F", "C", "w8a16_kmajor_kernel<mb4>")])
+def test_w8a16_weights_column_major_row_blocks(gpu, oracle, M, N, K, xo, yo, kernel):
+    """Batches above 16 rows: each workgroup multiplies 2 or 4 row blocks of X with every
+    dequantized W fragment, so W streams once per 32 or 64 rows; against the oracle, and through
+    the kernel log, the row-block form that ran."""
+    gpu.kernel_log_clear()
+    w8a16_column_major_case(gpu, oracle, M, N, K, xo, yo)
+    assert kernel in gpu.kernel_log(), gpu.kernel_log()
+
+
 def w8a16_column_major_case(lh, oracle, M, N, K, xo, yo):
     announce(f"w8a16 W column-major M={M} N={N} K={K} X {xo} Y {yo}")
     X = lh.HIPDeviceArray("f16", (M, K), order=xo)

@@ -56,7 +56,9 @@ def test_noalloc_without_split_and_argument_errors(gpu, oracle):
         lh._lib.call("lava_hip_gemm_w8a16_noalloc", 16, 16, 16, 16, 16, 128, 256, 256, 100, 128, 7, None)
 
 
-@pytest.mark.parametrize("M,xo,yo", [(16, "C", "C"), (16, "F", "F"), (5, "F", "C")])
+@pytest.mark.parametrize("M,xo,yo", [(16, "C", "C"), (16, "F", "F"), (5, "F", "C"),
+                                     # several 16-row blocks per workgroup; M = 100 copies X row-major
+                                     (32, "F", "F"), (64, "C", "C"), (100, "F", "C")])
 def test_noalloc_column_major_weights(gpu, oracle, M, xo, yo):
     """W column-major (K contiguous per column): the whole-column kernel (no scratch, or the
     scratch holding a row-major copy of a column-major X whose M is not a multiple of 8); the
