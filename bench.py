@@ -11,7 +11,7 @@ before timing starts.
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
                               gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|gemm_shapes|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy|
-                              hbm_read|gemm_u8|mfma_loop|gemm_bf16_pad64]
+                              hbm_read|gemm_u8|mfma_loop|gemm_bf16_pad64|w8a16_m64]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -359,7 +359,7 @@ def main():
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96", "attn_d256",
                              "copy", "hbm_read", "vendor_bf16", "w8a16_wrow", "w8a16_julia", "gemm_shapes", "gemm_u8",
-                             "mfma_loop", "gemm_bf16_pad64"])
+                             "mfma_loop", "gemm_bf16_pad64", "w8a16_m64"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -559,6 +559,20 @@ def main():
                     "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
                     "roofline": roofline("hbm", nbytes / (kms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s",
                                          load_traffic(traffic_key) if traffic_key else None)})
+    elif args.workload == "w8a16_m64":
+        # batched decode: 64 rows of X, W column-major (each workgroup multiplies 4 row blocks with
+        # every dequantized weight fragment); past the weight stream the kernel is MFMA / L2 work,
+        # so the figure is TFLOP/s, with the HBM rate beside it
+        M = 64
+        nbytes, kms, wms = bench_w8a16(lh, K, W, stream, M=M, x_order="C", w_order="F", y_order="C")
+        flop = 2.0 * M * 4096 * 14336
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 5),
+                    "dtype": "f16", "launches_per_step": SHORT_GROUP,
+                    "config": {"workload": "W8A16 64x4096 . 4096x14336 (batched decode), per-column fp16 scale, "
+                                           "6 rotating weight copies; X row-major, W column-major, Y row-major"},
+                    "kernel_ms": round(kms, 5), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 5),
+                    "hbm_GBs": round(nbytes / (kms * 1e-3) / 1e9, 1),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_FP16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_f16_256":
         flop, kms, wms = bench_gemm_layout(lh, "f16", 256, 3 | 4, K, W, stream, 0, group=SHORT_GROUP)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 3), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
