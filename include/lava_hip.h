@@ -482,7 +482,8 @@ int lava_hip_coopmat_gemm_f16_tiles(const void* A, const void* B, void* C, int64
  * kernels, every call one launch:
  *  - W column-major (K contiguous per output column), X and Y either way: any N, K a
  *    multiple of 16, 16-byte aligned W with a leading dimension a multiple of 16.  Whole
- *    columns per workgroup.  X is read in place when row-major (16-byte aligned, ldx a multiple of 8),
+ *    columns per workgroup, for 1, 2 or 4 16-row blocks of X (M up to 16, 32, or more): W is
+ *    streamed once per 64 rows at most.  X is read in place when row-major (16-byte aligned, ldx a multiple of 8),
  *    or column-major with M a multiple of 8 (or M == 1 with ldx == 1); any other column-major X
  *    is first copied row-major into the workspace (M x K fp16).
  *  - W row-major, X and Y either way: K a multiple of 32, N of 8, 8-byte aligned W with ldw
