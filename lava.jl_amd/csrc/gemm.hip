@@ -79,7 +79,7 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     else if (pin == 3 || (pin == 1 && fit != TN_NO))
         use_small = false;
     else
-        use_small = small_fits && small_gemm_preferred<T>(M, N, K);
+        use_small = small_fits && small_gemm_preferred<T>(M, N, K, !arow || brow);
     if (use_small) {
         if constexpr (!EPI) {
             const SmallSplit sp = pin == 2 ? SmallSplit{} : small_gemm_splits<T>(M, N, K);

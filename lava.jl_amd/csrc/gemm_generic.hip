@@ -392,7 +392,7 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
 }
 
 template <typename T>
-bool small_gemm_preferred(int64_t M, int64_t N, int64_t) {
+bool small_gemm_preferred(int64_t M, int64_t N, int64_t, bool mn_operand) {
     const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
     if (tiles256 <= SMALL_GEMM_MAX_TILES) return true;
     // Rate estimates (measured on shape lists): the tile kernel ~1500 TFLOP/s (bf16; int8 ~3000
@@ -402,9 +402,12 @@ bool small_gemm_preferred(int64_t M, int64_t N, int64_t) {
     // x 8192: 275 -> 342; 2048 x 4096 x 4096 stays on the tile kernel (898 against 494); int8
     // (tile kernel against small kernel, TOP/s): 64 x 14336 x 4096 166 / 383, 128 x 28672 x 8192
     // 727 / 755, 2048^3 653 / 681, 1536^2 x 8192 515 / 637 take the small kernel, 2048 x 4096 x
-    // 4096 (1558 / 916) the tile kernel.
+    // 4096 (1558 / 916) the tile kernel.  An int8 operand that is M/N-contiguous (Julia's
+    // column-major default) is transposed by byte stores on the small kernel, about half its rate
+    // (2048^3 with A column-major: 343 TOP/s against 689), while the tile kernel reads it through
+    // transposing LDS reads at its full rate: ~400.
     const double tile_rate = sizeof(T) == 1 ? 3000.0 : 1500.0;
-    const double small_rate = sizeof(T) == 1 ? 800.0 : 450.0;
+    const double small_rate = sizeof(T) == 1 ? (mn_operand ? 400.0 : 800.0) : 450.0;
     const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
     const double occ256 = tiles256 >= 256 ? 1.0 : (double)tiles256 / 256.0;
     const double useful = (double)M * (double)N / ((double)tiles256 * 65536.0);
@@ -422,7 +425,7 @@ bool small_gemm_fits(const void* A, const void* B, int64_t M, int64_t N, int64_t
            ((arow || !brow) ? K % EV == 0 : true) && (arow || M % EV == 0) && (!brow || N % EV == 0);
 }
 #define LAVA_SMALL_RULE_INST(T)                                                                                      \
-    template bool small_gemm_preferred<T>(int64_t, int64_t, int64_t);                                                 \
+    template bool small_gemm_preferred<T>(int64_t, int64_t, int64_t, bool);                                           \
     template bool small_gemm_fits<T>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool, bool);
 LAVA_SMALL_RULE_INST(f16)
 LAVA_SMALL_RULE_INST(bf16)

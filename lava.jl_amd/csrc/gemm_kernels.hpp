@@ -19,7 +19,7 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
 // arow / brow: A / B row-major).
 constexpr int64_t SMALL_GEMM_MAX_TILES = 16;
 template <typename T>
-bool small_gemm_preferred(int64_t M, int64_t N, int64_t K);
+bool small_gemm_preferred(int64_t M, int64_t N, int64_t K, bool mn_operand);   // mn_operand: A or B M/N-contiguous
 template <typename T>
 bool small_gemm_fits(const void* A, const void* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, bool arow,
                      bool brow);
