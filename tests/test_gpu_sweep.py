@@ -5,7 +5,7 @@ paths were written for; these cases draw shapes, layouts, dtypes, head dimension
 scales from a fixed seed, so that every dispatcher decision (tile kernel, small-product
 kernel, staged kernel, generic kernels; full and ragged tiles; the W8A16 column-major,
 copied-X, split-K and generic kernels; the attention score/output, ping-pong and generic
-kernels) meets shapes nobody chose.  Same bars as everywhere: int8 bit-exact, fp16/bf16
+kernels, and the unsigned GEMM's and the batched W8A16's forms) meets shapes nobody chose.  Same bars as everywhere: int8 bit-exact, fp16/bf16
 GEMM and W8A16 relative Frobenius <= 1e-3, attention <= 2e-3.
 """
 from __future__ import annotations
@@ -147,6 +147,75 @@ def test_sweep_w8a16(gpu, oracle, layout, M, N, K):
     Xh, Wh = np.ascontiguousarray(X.to_numpy()), np.ascontiguousarray(W.to_numpy())
     ref = oracle.w8a16_rows(Xh, Wh, s.to_numpy(), N, K, K, N, np.arange(M))
     assert oracle.rel_frobenius(y1, ref) <= 1e-3
+
+
+def _u8_cases():
+    rng = np.random.default_rng(255255)
+    out = []
+    for _ in range(48):
+        layout = int(rng.integers(0, 8))
+        big = rng.random() < 0.3
+        M = _dim(rng, 1, 700 if big else 300, mults=(16, 64, 256))
+        N = _dim(rng, 1, 700 if big else 300, mults=(16, 64, 256))
+        K = _dim(rng, 1, 2000 if rng.random() < 0.2 else 600, mults=(16, 64, 512))
+        out.append((layout, M, N, K))
+    return out
+
+
+@pytest.mark.parametrize("layout,M,N,K", _u8_cases())
+def test_sweep_gemm_u8(gpu, oracle, layout, M, N, K):
+    """Unsigned bytes: every kernel choice (the tile and small kernels' flipped-byte forms, split
+    K, the one-thread-per-element kernel) on drawn shapes, bit for bit."""
+    lh = gpu
+    announce(f"sweep gemm u8 layout={layout} M={M} N={N} K={K}")
+    A = lh.HIPDeviceArray("u8", (M, K), order="C" if layout & 1 else "F")
+    B = lh.HIPDeviceArray("u8", (K, N), order="C" if layout & 2 else "F")
+    seed = M * 1000003 + N * 1009 + K
+    lh.fill_i8(A, lh_mod.seed(33, seed))
+    lh.fill_i8(B, lh_mod.seed(34, seed))
+    C = lh.HIPDeviceArray("u32", (M, N), order="C" if layout & 4 else "F")
+    C.fill_bytes(0xFF)
+    lh.gemm(C, A, B)
+    lda = K if layout & 1 else M
+    ldb = N if layout & 2 else K
+    rows = np.unique(np.concatenate([np.arange(0, M, 3), [M - 1]]))
+    ref = oracle.gemm_u8_rows(A.to_numpy().ravel(order=A.order), B.to_numpy().ravel(order=B.order), N, K, lda, ldb,
+                              layout & 3, rows)
+    np.testing.assert_array_equal(C.to_numpy()[rows], ref)
+
+
+def _w8_batch_cases():
+    rng = np.random.default_rng(16300)
+    out = []
+    for _ in range(16):
+        layout = int(rng.integers(0, 8))
+        M = int(rng.integers(17, 301))
+        N = _dim(rng, 8, 2048, mult_p=0.7, mults=(8, 32, 128))
+        K = _dim(rng, 16, 2048, mult_p=0.7, mults=(16, 32, 128))
+        out.append((layout, M, N, K))
+    return out
+
+
+@pytest.mark.parametrize("layout,M,N,K", _w8_batch_cases())
+def test_sweep_w8a16_batch(gpu, oracle, layout, M, N, K):
+    """Batches of 17 to 300 rows (2 or 4 row blocks per workgroup for column-major W, several
+    row groups, the row-major copy of X) on drawn shapes; sampled rows against the oracle."""
+    lh = gpu
+    announce(f"sweep w8a16 batch layout={layout} M={M} N={N} K={K}")
+    X = lh.HIPDeviceArray("f16", (M, K), order="C" if layout & 1 else "F")
+    W = lh.HIPDeviceArray("i8", (K, N), order="C" if layout & 2 else "F")
+    s = lh.HIPDeviceArray("f16", (N,))
+    seed = M * 1000003 + N * 1009 + K
+    lh.fill_normal(X, lh_mod.seed(54, seed))
+    lh.fill_i8(W, lh_mod.seed(55, seed), symmetric=True)
+    lh.fill_uniform(s, lh_mod.seed(56, seed), 0.001, 0.02)
+    Y = lh.HIPDeviceArray("f32", (M, N), order="C" if layout & 4 else "F")
+    Y.fill_bytes(0xFF)
+    lh.w8a16(Y, X, W, s)
+    rows = np.unique(np.concatenate([np.arange(0, M, 5), [M - 1]]))
+    Xh, Wh = np.ascontiguousarray(X.to_numpy()), np.ascontiguousarray(W.to_numpy())
+    ref = oracle.w8a16_rows(Xh, Wh, s.to_numpy(), N, K, K, N, rows)
+    assert oracle.rel_frobenius(Y.to_numpy()[rows], ref) <= 1e-3
 
 
 # ---- larger shapes: multi-round grids, XCD orders, K splits; sampled rows against the oracle
