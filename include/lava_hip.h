@@ -424,11 +424,13 @@ int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64
 
 /* uint8 x uint8 -> uint32, all operands unsigned (src/compiler/spirv/coopmat.jl:115-151 emits no
  * signed-component bits for UInt8 coopmats; test/spirv/test_coopmat_int8.jl:71-98), exact with
- * the 32-bit accumulator's wrap; C holds uint32.  The MFMA is signed only: the tile kernel
- * multiplies the bytes flipped by 128 (u - 128) and adds 128 (row sum + column sum) + 16384 K
- * back in its epilogue.  Shapes the tile kernel does not take (fewer than 256 x 256 outputs, a
- * K-contiguous K or an M/N-contiguous M/N not a multiple of 16, 16-byte misaligned operands) run
- * on a one-thread-per-element kernel.  Same layouts and leading-dimension rules as above. */
+ * the 32-bit accumulator's wrap; C holds uint32.  The MFMA is signed only: the tile kernel and
+ * the small-product kernel multiply the bytes flipped by 128 (u - 128) and add 128 (row sum +
+ * column sum) + 16384 K back after their last k-step.  The kernel choice is the signed one's
+ * (tile kernel, small-product kernel with K split through the per-stream workspace, in their
+ * unsigned forms); shapes neither MFMA kernel takes (a K-contiguous K or an M/N-contiguous M/N
+ * not a multiple of 16, 16-byte misaligned operands or leading dimensions) run on a
+ * one-thread-per-element kernel.  Same layouts and leading-dimension rules as above. */
 int lava_hip_gemm_u8_u32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
 
