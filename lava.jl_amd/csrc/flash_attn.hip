@@ -8,10 +8,10 @@
 // and finally O / L, converted to fp16 (RNE).
 //
 // Kernels (the dispatcher at the end of the file picks one):
-//  * flash_fwd5_kernel -- D = 128, the headline shape, any softmax scale: on each SIMD a
-//    score wavefront and an output wavefront share 64 queries (described at the kernel);
-//  * flash_fwd3_kernel -- D = 64 with a positive scale (and D = 128 on request): ping-pong
-//    pairs of 32-query wavefronts;
+//  * flash_fwd5_kernel -- D <= 128 (the headline shape D = 128), any softmax scale: on each SIMD
+//    a score wavefront and an output wavefront share 64 queries (described at the kernel);
+//  * flash_fwd3_kernel -- D = 256 with a positive scale (and D = 64 or 128 on request):
+//    ping-pong pairs of 32-query wavefronts;
 //  * flash_generic_kernel -- any D <= 256, one thread per query (every other case).
 //
 // The common CDNA4 formulation:
@@ -554,14 +554,21 @@ __device__ __forceinline__ void fa_scale_f16(f16x8& q, float c) {
     q = __builtin_bit_cast(f16x8, u);
 }
 
-template <bool CAUSAL>
+// DE: the head dimension the MFMAs cover, 64, 96 or 128 (D rounded up to a multiple of 32).  K, V
+// and Q are staged 128 wide whatever DE is (the chunks past D are DMA-ed as zeros, so the LDS
+// layout, its swizzles and the DMA map stay those of D = 128); a smaller DE only drops the S^T
+// k-steps and the O^T row tiles that would multiply those zero columns.
+template <bool CAUSAL, int DE>
 __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams p) {
-    constexpr int DH = 128;
+    static_assert(DE == 64 || DE == 96 || DE == 128, "the MFMAs cover 64, 96 or 128 of the head dimension");
+    constexpr int DH = 128;                    // staged width
     constexpr int RB = DH * 2;                 // 256 bytes per K / V row
     constexpr int CH = RB / 16;                // 16 chunks
     constexpr int TILE = F5_BK * RB;           // 16 KB
-    constexpr int NKS = DH / 16;               // 8 k-steps of S^T
-    constexpr int NDT = DH / 32;               // 4 O^T row tiles
+    constexpr int NKS = DE / 16;               // k-steps of S^T (8 at DE = 128)
+    constexpr int NDT = DE / 32;               // O^T row tiles (4 at DE = 128)
+    constexpr int NSF = 2 * NKS;               // K fragments per block: (ks, kt)
+    constexpr int NVF = 4 * NDT;               // V fragments per block: (key step kk, dt)
     constexpr int DPT = TILE / (1024 * F5_PAIRS);   // 4 DMA instructions per wavefront per tile
     constexpr int PBUF = 8 * 1024;             // one pair's P^T fragments for one block
     static_assert(DPT == 4, "4 DMA instructions per tile and wavefront");
@@ -718,10 +725,10 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                     st[kt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones, qm[qh], f32x16{}, 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 32; ++i) {   // MFMA i: fragment f = i / 2 (ks = f / 2, kt = f % 2), qh = i % 2
+            for (int i = 0; i < 2 * NSF; ++i) {   // MFMA i: fragment f = i / 2 (ks = f / 2, kt = f % 2), qh = i % 2
                 const int f = i >> 1, qh = i & 1, ks = f >> 1, kt = f & 1;
                 st[kt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[f % F5_PFK], qf[qh][ks], st[kt][qh], 0, 0, 0);
-                if (qh == 1 && f + F5_PFK < 16) fr[f % F5_PFK] = kread(f + F5_PFK);
+                if (qh == 1 && f + F5_PFK < NSF) fr[f % F5_PFK] = kread(f + F5_PFK);
                 __builtin_amdgcn_sched_barrier(0);
             }
             // mask: causal key > query; else keys >= S.  A pair's causal last block is its diagonal
@@ -882,8 +889,8 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                     va[dt] = vb0[dt] + (uint32_t)((j % F5_VST) * TILE);
                     asm("; lds address" : "+v"(va[dt]));
                 }
-                auto vread = [&](int f) __attribute__((always_inline)) -> f16x8 {   // f = 4 kk + dt
-                    const int kk = 16 * (f >> 2), dt = f & 3;
+                auto vread = [&](int f) __attribute__((always_inline)) -> f16x8 {   // f = NDT kk + dt
+                    const int kk = 16 * (f / NDT), dt = f % NDT;
                     const f3_s16x4 lo =
                         __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uintptr_t)(va[dt] + (uint32_t)(kk * RB)));
                     const f3_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -902,13 +909,13 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                 for (int f = 0; f < F5_PFV; ++f) fr[f] = vread(f);
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int i = 0; i < 32; ++i) {   // MFMA i: V fragment f = i / 2 (kk = f / 4, dt = f % 4), qh = i % 2
-                    const int f = i >> 1, qh = i & 1, kk = f >> 2, dt = f & 3;
-                    if (i % 8 == 0 && kk < 3) {   // the next key step's P fragments
+                for (int i = 0; i < 2 * NVF; ++i) {   // MFMA i: V fragment f = i / 2 (kk = f / NDT, dt = f % NDT), qh = i % 2
+                    const int f = i >> 1, qh = i & 1, kk = f / NDT, dt = f % NDT;
+                    if (i % (2 * NDT) == 0 && kk < 3) {   // the next key step's P fragments
                         pp[(kk + 1) & 1][0] = pread(kk + 1, 0);
                         pp[(kk + 1) & 1][1] = pread(kk + 1, 1);
                     }
-                    if (i % 8 == 4) {   // row sums of this key step's P (fp16 values, fp32 sum)
+                    if (i % (2 * NDT) == NDT) {   // row sums of this key step's P (fp16 values, fp32 sum)
 #pragma unroll
                         for (int qq = 0; qq < 2; ++qq)
 #pragma unroll
@@ -918,7 +925,7 @@ __global__ void __launch_bounds__(128 * F5_PAIRS, 1) flash_fwd5_kernel(FaParams 
                     }
                     o[dt][qh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fr[f % F5_PFV], pp[kk & 1][qh], o[dt][qh], 0, 0,
                                                                        0);
-                    if (qh == 1 && f + F5_PFV < 16) fr[f % F5_PFV] = vread(f + F5_PFV);
+                    if (qh == 1 && f + F5_PFV < NVF) fr[f % F5_PFV] = vread(f + F5_PFV);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -1061,12 +1068,14 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     hipStream_t s = as_stream(stream);
 
     // D <= 128 (a multiple of 8) with 16-byte rows, and D = 256: the MFMA kernels.  D <= 128 runs
-    // on flash_fwd5_kernel (score/output wavefront pairs, zero-padded to 128; the scale folds into
-    // Q^T, so any sign), D = 64 and D = 256 with a positive scale on flash_fwd3_kernel (ping-pong
-    // wavefront pairs; its base-2 running maximum assumes one); all take any S (a ragged last
-    // block of queries or keys is zero-filled and masked).  lava_hip_set_kernel_override
-    // (LAVA_HIP_FAMILY_ATTN, 3) pins flash_fwd3_kernel for D = 128 as well, 5 flash_fwd5_kernel for
-    // D = 64 (tests and A/B timing).  Everything else runs on flash_generic_kernel.
+    // on flash_fwd5_kernel (score/output wavefront pairs, rows staged zero-padded to 128, MFMAs over
+    // D rounded up to 64, 96 or 128; the scale folds into Q^T, so any sign; at D = 64 it runs
+    // 1.2x flash_fwd3_kernel, 837 against 682 TFLOP/s causal at B=4 H=32 S=4096), D = 256 with a
+    // positive scale on flash_fwd3_kernel (ping-pong wavefront pairs; its base-2 running maximum
+    // assumes one); all take any S (a ragged last block of queries or keys is zero-filled and
+    // masked).  lava_hip_set_kernel_override(LAVA_HIP_FAMILY_ATTN, 3) pins flash_fwd3_kernel for
+    // D = 64 and 128 with a positive scale (tests and A/B timing).  Everything else runs on
+    // flash_generic_kernel.
     bool lay_ok = D >= 8 && D <= FA_D && D % 8 == 0 && strides[0] == 1 && os[0] == 1;
     for (int i = 1; i < 4; ++i) lay_ok = lay_ok && strides[i] % 8 == 0 && os[i] % 4 == 0;
     lay_ok = lay_ok && aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8) &&
@@ -1074,7 +1083,7 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
     const int64_t blocks3 = ((S + F3_BQ - 1) / F3_BQ) * H * B;
     const int64_t blocks5 = ((S + F5_BQ - 1) / F5_BQ) * H * B;
     const int pin = kernel_override(LAVA_HIP_FAMILY_ATTN);
-    const bool fast3 = lay_ok && scale > 0.f && (D == 64 ? pin != 5 : D == FA_D && pin == 3) && blocks3 <= 0x7fffffff;
+    const bool fast3 = lay_ok && scale > 0.f && (D == 64 || D == FA_D) && pin == 3 && blocks3 <= 0x7fffffff;
     const bool fast5 = lay_ok && !fast3 && blocks5 <= 0x7fffffff;
     // 128 < D <= 256 (a multiple of 8) with a positive scale: the ping-pong kernel over Q/K rows
     // zero-padded to 256, once per 128-column half of V and O (the scores are computed twice)
@@ -1083,11 +1092,17 @@ extern "C" int lava_hip_flash_attn_fwd_f16(const void* Q, const void* K, const v
                    aligned(Q, 16) && aligned(K, 16) && aligned(V, 16) && aligned(O, 8) &&
                    S * strides[1] * 2 < ((int64_t)1 << 31);
     for (int i = 1; i < 4; ++i) fast256 = fast256 && strides[i] % 8 == 0 && os[i] % 4 == 0;
-    if (fast5) {   // any D <= 128, a multiple of 8 (zero-padded to 128)
-        if (p.causal)
-            hipLaunchKernelGGL((flash_fwd5_kernel<true>), dim3((unsigned)blocks5), dim3(128 * F5_PAIRS), 0, s, p);
-        else
-            hipLaunchKernelGGL((flash_fwd5_kernel<false>), dim3((unsigned)blocks5), dim3(128 * F5_PAIRS), 0, s, p);
+    if (fast5) {   // any D <= 128, a multiple of 8 (staged zero-padded to 128; MFMAs over D rounded up to 64, 96, 128)
+        auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, dim3((unsigned)blocks5), dim3(128 * F5_PAIRS), 0, s, p); };
+        if (p.causal) {
+            if (D <= 64) go(flash_fwd5_kernel<true, 64>);
+            else if (D <= 96) go(flash_fwd5_kernel<true, 96>);
+            else go(flash_fwd5_kernel<true, 128>);
+        } else {
+            if (D <= 64) go(flash_fwd5_kernel<false, 64>);
+            else if (D <= 96) go(flash_fwd5_kernel<false, 96>);
+            else go(flash_fwd5_kernel<false, 128>);
+        }
         LAVA_LAUNCH_CHECK("flash_fwd5_kernel");
         return LAVA_HIP_OK;
     }

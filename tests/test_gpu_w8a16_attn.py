@@ -387,17 +387,26 @@ def test_flash_fast_ragged_s(gpu, oracle, so_kernel, causal, L):
     assert not np.isnan(O.to_numpy()).any()
 
 
+@pytest.mark.parametrize("kernel", ["flash_fwd3_kernel", "flash_fwd5_kernel"])
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("L", [64, 256, 777, 2048])
-def test_flash_fast_d64(gpu, oracle, causal, L):
-    """Head dimension 64 on the MFMA kernel (128-byte rows, 4 S^T k-steps, 2 O^T tiles)."""
+def test_flash_fast_d64(gpu, oracle, causal, L, kernel):
+    """Head dimension 64 on both MFMA kernels, each pinned: the ping-pong kernel (128-byte rows,
+    4 S^T k-steps, 2 O^T tiles) and the score/output kernel (rows staged 128 wide, MFMAs over
+    the 64 columns that hold data: 4 S^T k-steps, 2 O^T tiles)."""
     lh = gpu
     E, H, B = 64, 2, 2
-    announce(f"flash fast D=64 S={L} causal={causal}")
+    announce(f"flash fast D=64 S={L} causal={causal} {kernel}")
     Q, K, V = attn_inputs(lh, E, L, H, B)
     O = lh.HIPDeviceArray("f16", (E, L, H, B))
     O.fill_bytes(0xFF)
-    lh.flash_attn_fwd(O, Q, K, V, causal=causal)
+    lh.set_kernel_override(lh.FAMILY_ATTN, 3 if kernel == "flash_fwd3_kernel" else 5)
+    lh.kernel_log_clear()
+    try:
+        lh.flash_attn_fwd(O, Q, K, V, causal=causal)
+        assert kernel in lh.kernel_log(), lh.kernel_log()
+    finally:
+        lh.set_kernel_override(lh.FAMILY_ATTN, 0)
     rng = np.random.default_rng(L + 1)
     rows = np.arange(L) if L <= 256 else np.unique(np.concatenate([[0, 1, 255, 256, L - 1], rng.integers(0, L, 32)]))
     check_heads(oracle, Q, K, V, O, 1 / math.sqrt(E), causal, [(b, h) for b in range(B) for h in range(H)], rows)
@@ -463,9 +472,9 @@ def test_flash_d256_nonpositive_scale(gpu, oracle, causal):
 @pytest.mark.parametrize("E,L,causal", [(32, 200, True), (16, 32, True), (96, 130, False), (48, 100, False),
                                          (8, 257, True), (120, 300, False), (80, 512, True), (96, 1000, True)])
 def test_flash_padded_head_dims(gpu, oracle, so_kernel, E, L, causal):
-    """Head dimensions below 128 (multiples of 8) on the score/output kernel, zero-padded to
-    128: the padding columns of Q and K read zero and add nothing to the scores; those of O
-    are not written."""
+    """Head dimensions below 128 (multiples of 8) on the score/output kernel, staged zero-padded
+    to 128 with MFMAs over D rounded up to 64, 96 or 128: the padding columns of Q and K read
+    zero and add nothing to the scores; those of O are not written."""
     lh = gpu
     announce(f"flash padded D={E} S={L} causal={causal}")
     Q, K, V = attn_inputs(lh, E, L, 2, 1)
@@ -535,8 +544,7 @@ def test_flash_d128_scales(gpu, oracle, so_kernel, causal, scale, L):
 def test_flash_scale_zero_and_negative(gpu, oracle, so_kernel, causal, scale, E):
     """A softmax scale of zero (every visible key weighs the same) or below zero (the
     scores change sign, so the running maximum is taken over negated products): D = 128 and
-    D = 64 (zero-padded to 128) run on the score/output kernels, whose scale folds into Q^T;
-    against the oracle."""
+    D = 64 run on the score/output kernel, whose scale folds into Q^T; against the oracle."""
     lh = gpu
     L, H, B = 256, 2, 1
     announce(f"flash D={E} scale={scale} S={L} causal={causal}")
