@@ -60,17 +60,21 @@ typedef short tn_s16x8 __attribute__((ext_vector_type(8)));
 // The M/N-contiguous swizzle F(r % 4) = {0, 6, 10, 12}, as nibbles.
 __device__ __forceinline__ int tn_mn_swz(int r4) { return (0xCA60 >> (4 * r4)) & 0xF; }
 
-// One operand's staging: DMA offsets and validity, and its fragment reads.
-template <typename T, bool KC>
+// One operand's staging: DMA offsets and validity, and its fragment reads.  TILE: rows (m or n)
+// of the operand per workgroup tile -- 256 for the tile kernel; the K-contiguous form also serves
+// the 128 x 128 mid-size kernel (gemm_mid.hip).
+template <typename T, bool KC, int TILE = TN_TILE>
 struct TnSide;
 
-// K-contiguous: the slice is 256 rows (m or n) x 128 bytes of K.  Row r's logical
+// K-contiguous: the slice is TILE rows (m or n) x 128 bytes of K.  Row r's logical
 // 16-byte chunk c is stored at slot c ^ (r % 8): a 16x16 fragment read (16 consecutive
 // rows, one chunk per 16 lanes) then hits every bank once.  (With an extra ^ (r / 8 % 2),
 // the swizzle a 32-row read needs, the 16-row read costs ~4 conflict cycles; measured with
 // SQ_LDS_BANK_CONFLICT.)
-template <typename T>
-struct TnSide<T, true> {
+template <typename T, int TILE>
+struct TnSide<T, true, TILE> {
+    static constexpr int WROWS = TILE / 4;   // rows one wavefront's DMAs fill
+    static constexpr int HALF = TILE / 2;    // rows one wavefront's fragments read
     v4i rs;
     uint32_t off;      // the lane's row and chunk within an instruction's 8 rows
     uint32_t step;     // soffset per instruction: 8 rows
@@ -81,17 +85,17 @@ struct TnSide<T, true> {
     // rows_in: rows of this tile inside the matrix; w: the wavefront; wx: its 128-row half.
     __device__ __forceinline__ void init(const T* X, int64_t ld_b, int tile, int rows_in, int64_t, int, int w, int wx,
                                          int lane) {
-        rs = make_rsrc(reinterpret_cast<const char*>(X) + (int64_t)tile * TN_TILE * ld_b,
+        rs = make_rsrc(reinterpret_cast<const char*>(X) + (int64_t)tile * TILE * ld_b,
                        (uint32_t)(rows_in * ld_b));
         // DMA: an instruction covers 8 rows; lane l row l / 8, slot l % 8, which holds chunk slot ^ row % 8
         const int lr = lane >> 3;
         const int c = (lane & 7) ^ lr;
-        off = (uint32_t)((64 * w + lr) * ld_b + 16 * c);
+        off = (uint32_t)((WROWS * w + lr) * ld_b + 16 * c);
         step = (uint32_t)(8 * ld_b);
-        lim = rows_in - 64 * w - lr;
+        lim = rows_in - WROWS * w - lr;
         kend = 16 * c + 16;
         // fragments: row 16 t + lane % 16 of the half, chunk 4 u + lane / 16
-        rd16 = (wx * 128 + (lane & 15)) * TN_KB;
+        rd16 = (wx * HALF + (lane & 15)) * TN_KB;
 #pragma unroll
         for (int u = 0; u < 2; ++u) sl16[u] = ((4 * u + (lane >> 4)) ^ (lane & 7)) * 16;
     }
@@ -113,7 +117,7 @@ struct TnSide<T, true> {
 // + 2 (i % 4)), whose 16 k rows (4 groups of 4, 8 apart) x 32 bytes that swizzle spreads
 // over all banks (without the r / 8 term, ~2 conflict cycles per read; SQ_LDS_BANK_CONFLICT).
 template <typename T>
-struct TnSide<T, false> {
+struct TnSide<T, false, TN_TILE> {
     static_assert(sizeof(T) == 2, "M/N-contiguous staging reads 16-bit elements transposed");
     v4i rs;
     uint32_t off[4];   // per instruction variant (i % 2, i / 4): the row's swizzle depends on them
@@ -181,7 +185,7 @@ struct TnSide<T, false> {
 // fragment gives lane group g (bytes 16 g .. 16 g + 15 of the k-step), so the two forms mix.
 // F8 puts the 8 rows one group reads, and the two groups of a 32-lane half, on distinct banks.
 template <>
-struct TnSide<int8_t, false> {
+struct TnSide<int8_t, false, TN_TILE> {
     v4i rs;
     uint32_t off[4];   // per instruction variant (i % 2, i / 4): the row's swizzle depends on them
     uint32_t step;     // soffset per instruction: 4 rows of K

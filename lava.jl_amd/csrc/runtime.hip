@@ -212,7 +212,7 @@ void lava_hip_kernel_log_clear(void) { g_klog[0] = 0; }
 
 int lava_hip_set_kernel_override(int family, int choice) {
     const bool ok = (family == LAVA_HIP_FAMILY_ATTN && (choice == 0 || choice == 3 || choice == 5)) ||
-                    (family == LAVA_HIP_FAMILY_GEMM && choice >= 0 && choice <= 3);
+                    (family == LAVA_HIP_FAMILY_GEMM && choice >= 0 && choice <= 4);
     LAVA_ARG(ok, "set_kernel_override: unknown family %d or choice %d", family, choice);
     g_override[family].store(choice, std::memory_order_relaxed);
     return LAVA_HIP_OK;

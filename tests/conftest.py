@@ -92,3 +92,9 @@ def tile_kernel(gpu):
 def staged_kernel(gpu):
     """As tile_kernel, for the staged (any-layout, bounds-predicated) kernel."""
     yield from _pinned_gemm(gpu, 3, "gemm_staged_kernel")
+
+
+@pytest.fixture
+def mid_kernel(gpu):
+    """As tile_kernel, for the 128 x 128 mid-size kernel (both operands K-contiguous)."""
+    yield from _pinned_gemm(gpu, 4, "gemm_mid_kernel")

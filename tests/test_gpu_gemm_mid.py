@@ -1,0 +1,151 @@
+"""The 128 x 128 mid-size GEMM kernel (gemm_mid_kernel), pinned with lava_hip_set_kernel_override,
+against the oracle: rel. Frobenius <= 1e-3 for f16 / bf16, bit-exact for int8.
+
+Its operands are both K-contiguous (A row-major, B column-major), C row-major or column-major (the
+latter computed as C^T = B^T A^T, whose operands are K-contiguous again); ragged M, N and K take the
+zero-clamped loads (lanes past an extent read zero) and the bounds-checked store, as on the 256 x
+256 tile kernel whose staging it shares.  Checked: whole tiles and ragged extents, a K of one
+16-byte chunk, C row- and column-major, and a C with padded rows and guard rows after the last
+(nothing outside the M x N block changes)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import announce
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+# (M, N, K): whole 128 x 128 tiles; ragged M, N, K; K one chunk; one tile; a tall thin product
+SHAPES_16 = [(2048, 2048, 1024), (128, 128, 64), (1000, 777, 520), (300, 4097, 64), (129, 130, 136),
+             (4095, 257, 8), (640, 1920, 2056)]
+SHAPES_I8 = [(2048, 2048, 2048), (128, 128, 128), (1000, 777, 528), (300, 4097, 64), (129, 130, 144),
+             (4095, 257, 16), (640, 1920, 2064)]
+
+
+def host_flat(a):
+    return a.to_numpy().ravel(order=a.order)
+
+
+def sample_rows(M, rng):
+    edge = [0, 1, 63, 64, 127, 128, 129, M - 2, M - 1]
+    rows = sorted({r for r in edge if 0 <= r < M} | set(rng.integers(0, M, size=min(M, 24)).tolist()))
+    return np.array(rows, dtype=np.int64)
+
+
+def fill(lh, a, dt, seed):
+    if dt == "i8":
+        lh.fill_i8(a, seed)
+    else:
+        lh.fill_uniform(a, seed, -1.0, 1.0)
+
+
+def check(oracle, dt, got, A, B, M, N, K, lda, ldb, rows, layout=1):
+    if dt == "i8":
+        ref = oracle.gemm_i8_rows(host_flat(A), host_flat(B), N, K, lda, ldb, layout, rows)
+        np.testing.assert_array_equal(got, ref)
+    else:
+        ref = oracle.gemm_rows(host_flat(A), dt, host_flat(B), dt, M, N, K, lda, ldb, layout, rows)
+        err = oracle.rel_frobenius(got, ref)
+        assert err <= TOL, err
+
+
+@pytest.mark.parametrize("crow", [True, False])
+@pytest.mark.parametrize("dt,shape", [("f16", s) for s in SHAPES_16] + [("bf16", s) for s in SHAPES_16[:4]]
+                         + [("i8", s) for s in SHAPES_I8])
+def test_mid_kernel(gpu, oracle, mid_kernel, dt, shape, crow):
+    """A row-major, B column-major; C row-major (the kernel as is) or column-major, computed as
+    C^T = B^T A^T with A and B swapped: B^T is row-major, A^T column-major, K-contiguous again."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm mid {dt} M={M} N={N} K={K} C {'row' if crow else 'col'}-major")
+    A = lh.HIPDeviceArray(dt, (M, K), order="C")
+    B = lh.HIPDeviceArray(dt, (K, N), order="F")
+    fill(lh, A, dt, 8000 + M)
+    fill(lh, B, dt, 9000 + N)
+    C = lh.HIPDeviceArray("i32" if dt == "i8" else "f32", (M, N), order="C" if crow else "F")
+    C.fill_bytes(0xFF)
+    lh.gemm(C, A, B)
+    rows = sample_rows(M, np.random.default_rng(M * 7 + N))
+    check(oracle, dt, C.to_numpy()[rows], A, B, M, N, K, K, K, rows)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "i8"])
+def test_mid_kernel_store_stays_inside(gpu, oracle, mid_kernel, dt):
+    """C row-major with ldc = N + 3 (rows not 16-byte aligned: element stores) inside a buffer
+    with two guard rows: the padding columns and the guard rows keep their bytes."""
+    lh = gpu
+    M, N, K = 700, 601, 256 if dt == "bf16" else 512
+    ldc = N + 3
+    announce(f"gemm mid store bounds {dt} M={M} N={N} K={K} ldc={ldc}")
+    A = lh.HIPDeviceArray(dt, (M, K), order="C")
+    B = lh.HIPDeviceArray(dt, (K, N), order="F")
+    fill(lh, A, dt, 8100)
+    fill(lh, B, dt, 8101)
+    acc = "i32" if dt == "i8" else "f32"
+    Cbuf = lh.HIPDeviceArray(acc, (M + 2, ldc), order="C")
+    Cbuf.fill_bytes(0x5A)
+    lh.gemm_raw(dt, acc, A.ptr, B.ptr, Cbuf.ptr, M, N, K, K, K, ldc, 1 | 4)
+    full = Cbuf.to_numpy().view(np.uint32)
+    assert np.all(full[:, N:] == 0x5A5A5A5A), "padding columns written"
+    assert np.all(full[M:, :] == 0x5A5A5A5A), "guard rows written"
+    check(oracle, dt, Cbuf.to_numpy()[:M, :N], A, B, M, N, K, K, K, np.arange(M))
+
+
+def test_mid_kernel_repeatable_and_linear(gpu, oracle, mid_kernel):
+    """bf16 2048 x 2048 x 4096: two calls give the same bits, and C(A1 + A2) = C(A1) + C(A2)
+    exactly (A1, A2, B multiples of 1/64 in [-1, 1], exact in bf16, whose products and partial sums
+    are exact in fp32), so every element of C is checked, not only sampled rows."""
+    lh = gpu
+    M, N, K = 2048, 2048, 4096
+    announce(f"gemm mid repeat/linearity bf16 M={M} N={N} K={K}")
+    rng = np.random.default_rng(8200)
+    a1 = (rng.integers(-32, 33, size=(M, K)) / 64.0).astype(np.float32)
+    a2 = (rng.integers(-32, 33, size=(M, K)) / 64.0).astype(np.float32)
+    b = (rng.integers(-32, 33, size=(K, N)) / 64.0).astype(np.float32)
+
+    def bf16(x):   # exact in bf16: the high half of the fp32 bits (the low half is zero)
+        bits = x.view(np.uint32)
+        assert not (bits & 0xFFFF).any()
+        return (bits >> 16).astype(np.uint16)
+
+    A1 = lh.HIPDeviceArray.from_numpy(bf16(a1), "bf16", order="C")
+    A2 = lh.HIPDeviceArray.from_numpy(bf16(a2), "bf16", order="C")
+    A12 = lh.HIPDeviceArray.from_numpy(bf16(a1 + a2), "bf16", order="C")
+    B = lh.HIPDeviceArray.from_numpy(bf16(b), "bf16", order="F")
+    out = []
+    for A in (A1, A2, A12, A12):
+        C = lh.HIPDeviceArray("f32", (M, N), order="C")
+        lh.gemm(C, A, B)
+        out.append(C.to_numpy().astype(np.float64))
+    np.testing.assert_array_equal(out[2], out[3])
+    # each product is a sum of K exact terms (multiples of 1/4096 below 1): exact in fp32 while
+    # the partial sums stay below 2^24 / 4096 = 4096, so the identity holds exactly
+    np.testing.assert_array_equal(out[0] + out[1], out[2])
+
+
+@pytest.mark.parametrize("dt,shape,kernel", [("bf16", (2048, 2048, 2048), "gemm_mid_kernel"),
+                                             ("i8", (2048, 4096, 4096), "gemm_mid_kernel"),
+                                             ("bf16", (1536, 1536, 8192), "gemm_mid_kernel"),
+                                             ("bf16", (3072, 3072, 3072), "gemm_tn_kernel"),
+                                             ("i8", (4096, 4096, 4096), "gemm_tn_kernel"),
+                                             ("bf16", (1024, 1024, 8192), "splitk_sum_kernel")])
+def test_mid_kernel_automatic_choice(gpu, oracle, dt, shape, kernel):
+    """The automatic choice (A row-major, B column-major): the mid-size kernel from 128 tiles of
+    128 x 128 while there are fewer than 144 of 256 x 256, the tile kernel from there on, the
+    small-product kernel's K split below; each result against the oracle on sampled rows."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm automatic choice {dt} M={M} N={N} K={K}: {kernel}")
+    A = lh.HIPDeviceArray(dt, (M, K), order="C")
+    B = lh.HIPDeviceArray(dt, (K, N), order="F")
+    fill(lh, A, dt, 8300 + M)
+    fill(lh, B, dt, 8400 + N)
+    C = lh.HIPDeviceArray("i32" if dt == "i8" else "f32", (M, N), order="C")
+    lh.kernel_log_clear()
+    lh.gemm(C, A, B)
+    assert kernel in lh.kernel_log(), lh.kernel_log()
+    rows = np.array([0, 1, 127, 128, M // 2, M - 1])
+    check(oracle, dt, C.to_numpy()[rows], A, B, M, N, K, K, K, rows)
