@@ -1,10 +1,11 @@
 // gemm_mid.hip -- the mid-size GEMM kernel (gemm_mid_kernel): 128 x 128 tiles of C, for products
 // whose 256 x 256 tiles would leave most of the 256 CUs idle (2048^3: 64 of them, against 256
 // tiles of 128 x 128) and that the 64 x 64 small-product kernel runs well below the matrix
-// cores' rate.  Both operands K-contiguous (A row-major, B column-major), f16, bf16 or int8, plain
-// fp32 / int32 output.  The staging is the tile kernel's (gemm_tn_kernel.hpp: TnSide<T, true, 128>,
-// LDS-DMA of 128 bytes of K per row, chunk ^ row % 8) on a quarter of its LDS, so that two
-// workgroups share a CU and their wavefronts interleave on each SIMD:
+// cores' rate.  f16, bf16 or int8, each operand K-contiguous (A row-major, B column-major) or
+// M/N-contiguous; plain fp32 / int32 output.  The staging is the tile kernel's at 128 rows
+// (gemm_tn_kernel.hpp: TnSide<T, true, 128>, LDS-DMA of 128 bytes of K per m or n row, chunk ^ row %
+// 8; TnSide<T, false, 128>, 128 bytes of K as rows of 128 m or n, read back transposed) on a quarter
+// of its LDS, so that two workgroups share a CU and their wavefronts interleave on each SIMD:
 //  * 4 wavefronts, each a 64 x 64 sub-tile = 4 x 4 16x16 accumulators (64 registers per lane);
 //  * K advances 128 bytes per k-tile: A and B slices of 16 KB each, double-buffered (64 KB);
 //  * per k-tile, as in the tile kernel: 16 MFMAs of k-step 0 with k-step 1's 8 fragment reads,
@@ -19,7 +20,7 @@ namespace lava {
 constexpr int TM_TILE = 128;
 constexpr int TM_SLICE = TM_TILE * TN_KB;   // 16 KB
 
-template <typename T, bool RAGGED>
+template <typename T, bool RAGGED, bool AK, bool BK>
 __global__ void __launch_bounds__(256, 2)
     gemm_mid_kernel(const T* __restrict__ A, const T* __restrict__ B, typename Mfma16<T>::acc_elem* __restrict__ C,
                     int tiles_m, int tiles_n, int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, TnBounds bnd) {
@@ -40,10 +41,11 @@ __global__ void __launch_bounds__(256, 2)
         b_rows = (int)(bnd.n - (int64_t)tn * TM_TILE < TM_TILE ? bnd.n - (int64_t)tn * TM_TILE : TM_TILE);
     }
     const int kelems = bnd.kb / (int)sizeof(T);
-    TnSide<T, true, TM_TILE> sa, sb;
+    TnSide<T, AK, TM_TILE> sa;
+    TnSide<T, BK, TM_TILE> sb;
     sa.init(A, lda_b, tm, a_rows, bnd.m, kelems, w, wm, lane);
     sb.init(B, ldb_b, tn, b_rows, bnd.n, kelems, w, wn, lane);
-    // wave w fills rows [32 w, 32 w + 32) of each slice (4 KB), instruction i 1 KB of it
+    // wave w fills bytes [4 KB w, 4 KB (w + 1)) of each slice (32 m / n rows, or 16 k rows), instruction i 1 KB of it
     const uint32_t lds0 = lds_addr(smem) + w * (TM_TILE / 4) * TN_KB;
 
     // DMA load q (0..7) of a k-tile into `stage`: q < 4 are A, q >= 4 B.
@@ -168,15 +170,19 @@ __global__ void __launch_bounds__(256, 2)
 
 template <typename T>
 int mid_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
-                      int64_t ldb, int64_t ldc) {
+                      int64_t ldb, int64_t ldc, bool ak, bool bk) {
     const int64_t sz = (int64_t)sizeof(T), ke = TN_KB / sz, chunk = 16 / sz;
-    if (M <= 0 || N <= 0 || K <= 0 || K % chunk) return TN_NO;
+    if (M <= 0 || N <= 0 || K <= 0) return TN_NO;
+    if ((ak || bk) && K % chunk) return TN_NO;           // a K-contiguous chunk wholly in or out
+    if ((!ak && M % chunk) || (!bk && N % chunk)) return TN_NO;
     const int64_t tiles_m = (M + TM_TILE - 1) / TM_TILE, tiles_n = (N + TM_TILE - 1) / TM_TILE;
     if (tiles_m * tiles_n > 0x7fffffff || (K + ke - 1) / ke > 0x7fffffff || K * sz > 0x7fffffff) return TN_NO;
     if ((lda * sz) % 16 || (ldb * sz) % 16 || !aligned(A, 16) || !aligned(B, 16)) return TN_NO;
-    // buffer offsets are 32-bit: a 128-row slab of either operand must span < 2 GiB
+    // buffer offsets are 32-bit: a 128-row K-contiguous slab, or the whole K x ld M/N-contiguous
+    // operand, must span < 2 GiB
     const int64_t lim = (int64_t)1 << 31;
-    if ((int64_t)TM_TILE * lda * sz >= lim || (int64_t)TM_TILE * ldb * sz >= lim) return TN_NO;
+    if ((ak ? (int64_t)TM_TILE * lda * sz : K * lda * sz) >= lim) return TN_NO;
+    if ((bk ? (int64_t)TM_TILE * ldb * sz : K * ldb * sz) >= lim) return TN_NO;
     const size_t c_elem = sizeof(typename Mfma16<T>::acc_elem);
     if (M % TM_TILE == 0 && N % TM_TILE == 0 && K % ke == 0 && ldc % 4 == 0 && aligned(C, 4 * c_elem)) return TN_FULL;
     return TN_RAGGED;
@@ -188,16 +194,34 @@ int mid_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, in
 // 338, 1024 x 4096 x 4096 773 / 471, 512 x 4096 x 4096 412 / 433 and 884 / 721 -- while the 256 x 256
 // tile kernel keeps 3072^3 (948 against 766; 144 tiles) and 4096^3 (1406 against 1164), and the
 // small-product kernel's K split 1024^2 x 8192 (383 against 245; 64 tiles of 128 x 128).  So: at
-// least 128 tiles of 128 x 128, and fewer than 144 of 256 x 256.
-bool mid_gemm_preferred(int64_t M, int64_t N) {
+// least 128 tiles of 128 x 128, and fewer than 144 of 256 x 256.  With M/N-contiguous bf16 operands
+// the same boundaries hold (A and B column-major: 2048^3 620 / 401, 2048 x 4096 x 4096 1104 / 812,
+// 1536^2 x 8192 496 / 322, 3072^3 768 / 866, 1024^2 x 8192 221 / 374; A and B row-major or A
+// column-major and B row-major within 6 % of these).  int8 with an M/N-contiguous operand, which the
+// small-product kernel transposes by byte stores at about half its rate, keeps this kernel down to
+// 64 tiles (TOP/s, A and B column-major: 2048^3 1167 / 627, 1024^2 x 8192 403 / 306, 1024^3 226 /
+// 177; both M/N-contiguous 418 / 215 and 224 / 140).
+bool mid_gemm_preferred(int64_t M, int64_t N, bool i8_mn) {
     const int64_t t128 = ((M + TM_TILE - 1) / TM_TILE) * ((N + TM_TILE - 1) / TM_TILE);
     const int64_t t256 = ((M + TN_TILE - 1) / TN_TILE) * ((N + TN_TILE - 1) / TN_TILE);
-    return t128 >= 128 && t256 < 144;
+    return t128 >= (i8_mn ? 64 : 128) && t256 < 144;
+}
+
+template <typename T, bool AK, bool BK>
+void launch_mid_layout(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int tiles_m, int tiles_n, int ktiles,
+                       int64_t lda_b, int64_t ldb_b, int64_t ldc, const TnBounds& bnd, hipStream_t s, bool ragged) {
+    const dim3 grid((unsigned)(tiles_m * tiles_n));
+    if (ragged)
+        hipLaunchKernelGGL((gemm_mid_kernel<T, true, AK, BK>), grid, dim3(256), 0, s, A, B, C, tiles_m, tiles_n, ktiles,
+                           lda_b, ldb_b, ldc, bnd);
+    else
+        hipLaunchKernelGGL((gemm_mid_kernel<T, false, AK, BK>), grid, dim3(256), 0, s, A, B, C, tiles_m, tiles_n, ktiles,
+                           lda_b, ldb_b, ldc, bnd);
 }
 
 template <typename T>
 int launch_gemm_mid(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int64_t M, int64_t N, int64_t K,
-                    int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, bool ragged) {
+                    int64_t lda, int64_t ldb, int64_t ldc, hipStream_t s, bool ragged, bool ak, bool bk) {
     using Acc = typename Mfma16<T>::acc_elem;
     const int tiles_m = (int)((M + TM_TILE - 1) / TM_TILE), tiles_n = (int)((N + TM_TILE - 1) / TM_TILE);
     const int64_t ke = TN_KB / (int64_t)sizeof(T);
@@ -208,22 +232,23 @@ int launch_gemm_mid(const T* A, const T* B, typename Mfma16<T>::acc_elem* C, int
     bnd.kb = (int)(K * (int64_t)sizeof(T));
     bnd.cvec = ldc % 4 == 0 && aligned(C, 4 * sizeof(Acc));
     const int64_t lda_b = lda * (int64_t)sizeof(T), ldb_b = ldb * (int64_t)sizeof(T);
-    const dim3 grid((unsigned)(tiles_m * tiles_n));
-    if (ragged)
-        hipLaunchKernelGGL((gemm_mid_kernel<T, true>), grid, dim3(256), 0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b,
-                           ldb_b, ldc, bnd);
+    if (!ak && !bk)
+        launch_mid_layout<T, false, false>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, bnd, s, ragged);
+    else if (!ak)
+        launch_mid_layout<T, false, true>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, bnd, s, ragged);
+    else if (!bk)
+        launch_mid_layout<T, true, false>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, bnd, s, ragged);
     else
-        hipLaunchKernelGGL((gemm_mid_kernel<T, false>), grid, dim3(256), 0, s, A, B, C, tiles_m, tiles_n, ktiles, lda_b,
-                           ldb_b, ldc, bnd);
+        launch_mid_layout<T, true, true>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, bnd, s, ragged);
     LAVA_LAUNCH_CHECK("gemm_mid_kernel");
     return LAVA_HIP_OK;
 }
 
 #define LAVA_MID_INST(T)                                                                                          \
     template int mid_gemm_eligible<T>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t, \
-                                      int64_t, int64_t);                                                          \
+                                      int64_t, int64_t, bool, bool);                                              \
     template int launch_gemm_mid<T>(const T*, const T*, typename Mfma16<T>::acc_elem*, int64_t, int64_t, int64_t, \
-                                    int64_t, int64_t, int64_t, hipStream_t, bool);
+                                    int64_t, int64_t, int64_t, hipStream_t, bool, bool, bool);
 LAVA_MID_INST(f16)
 LAVA_MID_INST(bf16)
 LAVA_MID_INST(int8_t)

@@ -175,6 +175,73 @@ struct TnSide<T, false, TN_TILE> {
     }
 };
 
+// M/N-contiguous (16-bit) at 128 columns per tile (the mid-size kernel): the slice is 64 rows of K x
+// 256 bytes, one bank window per row.  Row r's logical 16-byte chunk c is stored at slot c ^ S(r),
+// S(r) = 2 (r % 4) + 8 ((r / 8 + r / 16) % 2).  A fragment's transposing read touches 16 k rows (the
+// 4-row groups 8 g + [0, 4) of the four 16-lane groups g) x 2 adjacent chunks; whether the hardware
+// serves it as lanes 0-31 and 32-63 (rows 8 g, g = 0, 1 or 2, 3: row bits 0, 1 and 3 vary) or as lane
+// groups {0, 2} and {1, 3} (bits 0, 1 and 4), S gives the 8 rows of a pass distinct chunk pairs
+// (bits 1-3 of the slot), so the 16 chunk reads of a pass cover a 256-byte window once.
+template <typename T>
+struct TnSide<T, false, 128> {
+    static_assert(sizeof(T) == 2, "M/N-contiguous staging reads 16-bit elements transposed");
+    v4i rs;
+    uint32_t off[2];   // per instruction variant i / 2: the row's swizzle depends on it
+    uint32_t step;     // soffset per instruction: 4 rows of K
+    uint32_t ld;       // bytes per row of K
+    int klim;          // instruction i's row is inside iff k0 + 4 i < klim
+    bool cin[2];       // the lane's chunk lies inside M (N), per variant
+    int mr16;          // fragment reads: the lane's row and byte offset
+    int c16[4];        // fragment reads: the stored chunk of column block t, times 16
+
+    __device__ __forceinline__ static int swz(int r) { return 2 * (r & 3) + 8 * (((r >> 3) ^ (r >> 4)) & 1); }
+
+    // mn_total: M (N); K: the depth in elements; w: the wavefront; wx: its 64-column half.
+    __device__ __forceinline__ void init(const T* X, int64_t ld_b, int tile, int, int64_t mn_total, int K, int w,
+                                         int wx, int lane) {
+        const int64_t col0 = (int64_t)tile * 128;
+        rs = make_rsrc(reinterpret_cast<const char*>(X) + col0 * (int64_t)sizeof(T),
+                       (uint32_t)((int64_t)K * ld_b - col0 * (int64_t)sizeof(T)));
+        // DMA: instruction i covers k rows 16 w + 4 i + lane / 16, slot lane % 16; that row's
+        // swizzle is S(16 w + 4 i + lane / 16): bits 0, 1 from lane / 16, bit 3 from i / 2, bit 4 from w
+        const int rr = lane >> 4, p = lane & 15;
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const int c = p ^ swz(16 * w + 4 * (2 * v) + rr);
+            off[v] = (uint32_t)((16 * w + rr) * ld_b + 16 * c);
+            cin[v] = col0 + 8 * c < mn_total;
+        }
+        step = (uint32_t)(4 * ld_b);
+        ld = (uint32_t)ld_b;
+        klim = K - 16 * w - rr;
+        // fragments: source lane ss of 16-lane group g points at k row 8 g + 4 r + ss / 4 (+ 32 u),
+        // columns 16 t + 4 (ss % 4) of the half; that row's swizzle is S(8 g + ss / 4) for every
+        // u, t and r (bit 2 and bit 5 do not enter S)
+        const int ss = lane & 15, g = lane >> 4;
+        const int f = swz(8 * g + (ss >> 2));
+        mr16 = (8 * g + (ss >> 2)) * 256 + 8 * (ss & 1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c16[t] = ((8 * wx + 2 * t + ((ss & 3) >> 1)) ^ f) * 16;
+    }
+    __device__ __forceinline__ bool valid(int i, uint32_t kofs, int) const {
+        return (int)(kofs / sizeof(T)) + 4 * i < klim && cin[i >> 1];
+    }
+    __device__ __forceinline__ uint32_t voff(int i) const { return off[i >> 1]; }
+    __device__ __forceinline__ uint32_t soff(int i, uint32_t kofs) const {
+        return (kofs / (uint32_t)sizeof(T)) * ld + i * step;
+    }
+    // fragment t (columns 16 t of the half) of k-step u (32 rows of K): two transposing reads, k rows
+    // 8 g + [0, 4) and 8 g + [4, 8) of the k-step
+    __device__ __forceinline__ uint4 read16(const uint8_t* slice, int u, int t) const {
+        const uint8_t* b = slice + u * 32 * 256 + mr16 + c16[t];
+        const tn_s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) tn_s16x4*)(const __attribute__((address_space(3))) uint8_t*)b);
+        const tn_s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) tn_s16x4*)(const __attribute__((address_space(3))) uint8_t*)(b + 4 * 256));
+        return __builtin_bit_cast(uint4, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+};
+
 // M/N-contiguous int8: the slice is 128 rows of K x 256 bytes (256 m or n).  Row r's logical
 // 16-byte chunk c is stored at slot c ^ F8(r), F8(r) = (r % 8) | 8 (r / 16 % 2).  A fragment is
 // two transposing reads (ds_read_b64_tr_b8: in a 16-lane group, output lane i byte j is the
@@ -233,6 +300,67 @@ struct TnSide<int8_t, false, TN_TILE> {
             (__attribute__((address_space(3))) tn_v2i*)(const __attribute__((address_space(3))) uint8_t*)b);
         const tn_v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
             (__attribute__((address_space(3))) tn_v2i*)(const __attribute__((address_space(3))) uint8_t*)(b + 8 * 256));
+        return make_uint4((uint32_t)lo.x, (uint32_t)lo.y, (uint32_t)hi.x, (uint32_t)hi.y);
+    }
+};
+
+// M/N-contiguous int8 at 128 columns per tile (the mid-size kernel): the slice is 128 rows of K x 128
+// bytes, two rows per 256-byte bank window.  Row r's logical chunk c is stored at slot c ^ F(r),
+// F(r) = (r / 2 % 4) | 4 ((r / 16 + r / 32) % 2).  The transposing reads are the 256-column form's
+// (source lane s of 16-lane group g at k row 64 u + 16 g + 8 h + s / 2, byte 8 (s % 2) of the
+// fragment's chunk); a 32-lane pass reads 16 rows x one chunk, and F gives the rows of each parity
+// distinct slots whether the pass is groups {0, 1} (row bit 4 varies) or {0, 2} / {1, 3} (bit 5), so
+// the pass's 16 chunk reads (row parity x slot) cover the 256-byte window once.
+template <>
+struct TnSide<int8_t, false, 128> {
+    v4i rs;
+    uint32_t off[2];   // per instruction variant i / 2: the row's swizzle depends on it
+    uint32_t step;     // soffset per instruction: 8 rows of K
+    uint32_t ld;       // bytes per row of K
+    int klim;          // instruction i's row is inside iff k0 + 8 i < klim
+    bool cin[2];       // the lane's chunk lies inside M (N), per variant
+    int rd;            // fragment reads: the lane's k row and byte offset
+    int c16[4];        // fragment reads: the stored chunk of column block t, times 16
+
+    __device__ __forceinline__ static int swz(int r) { return ((r >> 1) & 3) | ((((r >> 4) ^ (r >> 5)) & 1) << 2); }
+
+    // mn_total: M (N); K: the depth in elements; w: the wavefront; wx: its 64-column half.
+    __device__ __forceinline__ void init(const int8_t* X, int64_t ld_b, int tile, int, int64_t mn_total, int K, int w,
+                                         int wx, int lane) {
+        const int64_t col0 = (int64_t)tile * 128;
+        rs = make_rsrc(reinterpret_cast<const char*>(X) + col0, (uint32_t)((int64_t)K * ld_b - col0));
+        // DMA: instruction i covers k rows 32 w + 8 i + lane / 8, slot lane % 8; that row's swizzle
+        // is F(32 w + 8 i + lane / 8): bits 1, 2 from lane / 8, bit 4 from i / 2, bit 5 from w
+        const int rr = lane >> 3, p = lane & 7;
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const int c = p ^ swz(32 * w + 16 * v + rr);
+            off[v] = (uint32_t)((32 * w + rr) * ld_b + 16 * c);
+            cin[v] = col0 + 16 * c < mn_total;
+        }
+        step = (uint32_t)(8 * ld_b);
+        ld = (uint32_t)ld_b;
+        klim = K - 32 * w - rr;
+        // fragments: every row a lane reads (16 g + 8 h + s / 2 + 64 u) has F = (s / 4) | 4 (g % 2 ^ g / 2)
+        const int s = lane & 15, g = lane >> 4;
+        const int f = swz(16 * g + (s >> 1));
+        rd = (16 * g + (s >> 1)) * 128 + 8 * (s & 1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c16[t] = ((4 * wx + t) ^ f) * 16;
+    }
+    __device__ __forceinline__ bool valid(int i, uint32_t kofs, int) const {
+        return (int)kofs + 8 * i < klim && cin[i >> 1];
+    }
+    __device__ __forceinline__ uint32_t voff(int i) const { return off[i >> 1]; }
+    __device__ __forceinline__ uint32_t soff(int i, uint32_t kofs) const { return kofs * ld + i * step; }
+    // fragment t (columns 16 t of the half) of k-step u (64 rows of K): two transposing reads,
+    // k rows 16 g + [0, 8) and 16 g + [8, 16) of the k-step
+    __device__ __forceinline__ uint4 read16(const uint8_t* slice, int u, int t) const {
+        const uint8_t* b = slice + u * 64 * 128 + rd + c16[t];
+        const tn_v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) tn_v2i*)(const __attribute__((address_space(3))) uint8_t*)b);
+        const tn_v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (__attribute__((address_space(3))) tn_v2i*)(const __attribute__((address_space(3))) uint8_t*)(b + 8 * 128));
         return make_uint4((uint32_t)lo.x, (uint32_t)lo.y, (uint32_t)hi.x, (uint32_t)hi.y);
     }
 };

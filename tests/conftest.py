@@ -96,5 +96,5 @@ def staged_kernel(gpu):
 
 @pytest.fixture
 def mid_kernel(gpu):
-    """As tile_kernel, for the 128 x 128 mid-size kernel (both operands K-contiguous)."""
+    """As tile_kernel, for the 128 x 128 mid-size kernel."""
     yield from _pinned_gemm(gpu, 4, "gemm_mid_kernel")

@@ -1,12 +1,13 @@
 """The 128 x 128 mid-size GEMM kernel (gemm_mid_kernel), pinned with lava_hip_set_kernel_override,
 against the oracle: rel. Frobenius <= 1e-3 for f16 / bf16, bit-exact for int8.
 
-Its operands are both K-contiguous (A row-major, B column-major), C row-major or column-major (the
-latter computed as C^T = B^T A^T, whose operands are K-contiguous again); ragged M, N and K take the
-zero-clamped loads (lanes past an extent read zero) and the bounds-checked store, as on the 256 x
-256 tile kernel whose staging it shares.  Checked: whole tiles and ragged extents, a K of one
-16-byte chunk, C row- and column-major, and a C with padded rows and guard rows after the last
-(nothing outside the M x N block changes)."""
+Each operand is K-contiguous (A row-major, B column-major) or M/N-contiguous (staged as rows of K
+and read back through transposing LDS reads: 16-bit words or bytes).  C is
+row-major or column-major (the latter computed as C^T = B^T A^T, which swaps the operands and flips
+their layouts); ragged M, N and K take the zero-clamped loads (lanes past an extent read zero) and
+the bounds-checked store, as on the 256 x 256 tile kernel whose staging it shares.  Checked: whole
+tiles and ragged extents, a K of one 16-byte chunk, every operand layout, C row- and column-major,
+and a C with padded rows and guard rows after the last (nothing outside the M x N block changes)."""
 from __future__ import annotations
 
 import numpy as np
@@ -42,6 +43,17 @@ def fill(lh, a, dt, seed):
         lh.fill_uniform(a, seed, -1.0, 1.0)
 
 
+# M/N-contiguous operands: M (N) a multiple of the 8-element chunk; K a multiple of it where the
+# other operand is K-contiguous, anything where both are M/N-contiguous (SHAPES_MN_K)
+SHAPES_MN = [(2048, 2048, 1024), (128, 128, 64), (1000, 776, 520), (296, 4104, 72), (136, 136, 8),
+             (4096, 256, 8), (640, 1920, 2056), (1024, 1536, 104)]
+SHAPES_MN_K = [(136, 136, 1), (1024, 1536, 100), (1000, 776, 33)]
+# int8: M (N) a multiple of 16 for an M/N-contiguous operand, K of 16 for a K-contiguous one
+SHAPES_MN_I8 = [(2048, 2048, 2048), (128, 128, 128), (1008, 784, 528), (304, 4112, 80), (144, 144, 16),
+                (640, 1920, 2064), (1024, 1536, 112)]
+SHAPES_MN_K_I8 = [(144, 144, 1), (1024, 1536, 100), (1008, 784, 33)]
+
+
 def check(oracle, dt, got, A, B, M, N, K, lda, ldb, rows, layout=1):
     if dt == "i8":
         ref = oracle.gemm_i8_rows(host_flat(A), host_flat(B), N, K, lda, ldb, layout, rows)
@@ -70,6 +82,36 @@ def test_mid_kernel(gpu, oracle, mid_kernel, dt, shape, crow):
     lh.gemm(C, A, B)
     rows = sample_rows(M, np.random.default_rng(M * 7 + N))
     check(oracle, dt, C.to_numpy()[rows], A, B, M, N, K, K, K, rows)
+
+
+@pytest.mark.parametrize("crow", [True, False])
+@pytest.mark.parametrize("dt,shape,aorder,border",
+                         [(dt, s, ao, bo) for ao, bo in [("F", "F"), ("C", "C"), ("F", "C")]
+                          for dt, s in [("f16", s) for s in SHAPES_MN] + [("bf16", s) for s in SHAPES_MN[:5]]]
+                         + [("f16", s, "F", "C") for s in SHAPES_MN_K] + [("bf16", SHAPES_MN_K[1], "F", "C")]
+                         + [("i8", s, ao, bo) for ao, bo in [("F", "F"), ("C", "C"), ("F", "C")] for s in SHAPES_MN_I8]
+                         + [("i8", s, "F", "C") for s in SHAPES_MN_K_I8])
+def test_mid_kernel_layouts(gpu, oracle, mid_kernel, dt, shape, aorder, border, crow):
+    """A column-major and / or B row-major: the operand that is M/N-contiguous (in the kernel's
+    row-major C frame: A^T's and B^T's roles swap when C is column-major) is staged as rows of K and
+    read back transposed.  Short K (1, 8, 16, 33, 72, 80, 100, 104, 112) leaves part of the last k-tile
+    outside the matrix; M and N of 1000, 1008, 776, 784, 296, 304, 4104, 4112, 136, 144 end inside a
+    128 x 128 tile."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm mid {dt} M={M} N={N} K={K} A {aorder} B {border} C {'row' if crow else 'col'}-major")
+    A = lh.HIPDeviceArray(dt, (M, K), order=aorder)
+    B = lh.HIPDeviceArray(dt, (K, N), order=border)
+    fill(lh, A, dt, 8500 + M + K)
+    fill(lh, B, dt, 8600 + N + K)
+    C = lh.HIPDeviceArray("i32" if dt == "i8" else "f32", (M, N), order="C" if crow else "F")
+    C.fill_bytes(0xFF)
+    lh.gemm(C, A, B)
+    rows = sample_rows(M, np.random.default_rng(M * 5 + N + K))
+    lda = K if aorder == "C" else M
+    ldb = N if border == "C" else K
+    layout = (1 if aorder == "C" else 0) | (2 if border == "C" else 0)
+    check(oracle, dt, C.to_numpy()[rows], A, B, M, N, K, lda, ldb, rows, layout)
 
 
 @pytest.mark.parametrize("dt", ["bf16", "i8"])
@@ -126,21 +168,31 @@ def test_mid_kernel_repeatable_and_linear(gpu, oracle, mid_kernel):
     np.testing.assert_array_equal(out[0] + out[1], out[2])
 
 
-@pytest.mark.parametrize("dt,shape,kernel", [("bf16", (2048, 2048, 2048), "gemm_mid_kernel"),
-                                             ("i8", (2048, 4096, 4096), "gemm_mid_kernel"),
-                                             ("bf16", (1536, 1536, 8192), "gemm_mid_kernel"),
-                                             ("bf16", (3072, 3072, 3072), "gemm_tn_kernel"),
-                                             ("i8", (4096, 4096, 4096), "gemm_tn_kernel"),
-                                             ("bf16", (1024, 1024, 8192), "splitk_sum_kernel")])
-def test_mid_kernel_automatic_choice(gpu, oracle, dt, shape, kernel):
-    """The automatic choice (A row-major, B column-major): the mid-size kernel from 128 tiles of
-    128 x 128 while there are fewer than 144 of 256 x 256, the tile kernel from there on, the
-    small-product kernel's K split below; each result against the oracle on sampled rows."""
+@pytest.mark.parametrize("dt,shape,kernel,aorder,border",
+                         [("bf16", (2048, 2048, 2048), "gemm_mid_kernel", "C", "F"),
+                          ("i8", (2048, 4096, 4096), "gemm_mid_kernel", "C", "F"),
+                          ("bf16", (1536, 1536, 8192), "gemm_mid_kernel", "C", "F"),
+                          ("bf16", (3072, 3072, 3072), "gemm_tn_kernel", "C", "F"),
+                          ("i8", (4096, 4096, 4096), "gemm_tn_kernel", "C", "F"),
+                          ("bf16", (1024, 1024, 8192), "splitk_sum_kernel", "C", "F"),
+                          ("bf16", (2048, 2048, 2048), "gemm_mid_kernel", "F", "F"),
+                          ("f16", (2048, 4096, 4096), "gemm_mid_kernel", "C", "C"),
+                          ("bf16", (1536, 1536, 8192), "gemm_mid_kernel", "F", "C"),
+                          ("bf16", (3072, 3072, 3072), "gemm_tn_kernel", "F", "F"),
+                          ("i8", (2048, 2048, 2048), "gemm_mid_kernel", "F", "F"),
+                          ("i8", (1024, 1024, 8192), "gemm_mid_kernel", "F", "F"),
+                          ("i8", (1024, 1024, 8192), "splitk_sum_kernel", "C", "F"),
+                          ("i8", (3072, 3072, 3072), "gemm_tn_kernel", "C", "C")])
+def test_mid_kernel_automatic_choice(gpu, oracle, dt, shape, kernel, aorder, border):
+    """The automatic choice, in several operand layouts: the mid-size kernel from 128 tiles of 128 x
+    128 (64 for int8 with an M/N-contiguous operand) while there are fewer than 144 of 256 x 256, the
+    tile kernel from there on, the small-product kernel's K split below; each result against the
+    oracle on sampled rows."""
     lh = gpu
     M, N, K = shape
-    announce(f"gemm automatic choice {dt} M={M} N={N} K={K}: {kernel}")
-    A = lh.HIPDeviceArray(dt, (M, K), order="C")
-    B = lh.HIPDeviceArray(dt, (K, N), order="F")
+    announce(f"gemm automatic choice {dt} M={M} N={N} K={K} A {aorder} B {border}: {kernel}")
+    A = lh.HIPDeviceArray(dt, (M, K), order=aorder)
+    B = lh.HIPDeviceArray(dt, (K, N), order=border)
     fill(lh, A, dt, 8300 + M)
     fill(lh, B, dt, 8400 + N)
     C = lh.HIPDeviceArray("i32" if dt == "i8" else "f32", (M, N), order="C")
@@ -148,4 +200,7 @@ def test_mid_kernel_automatic_choice(gpu, oracle, dt, shape, kernel):
     lh.gemm(C, A, B)
     assert kernel in lh.kernel_log(), lh.kernel_log()
     rows = np.array([0, 1, 127, 128, M // 2, M - 1])
-    check(oracle, dt, C.to_numpy()[rows], A, B, M, N, K, K, K, rows)
+    lda = K if aorder == "C" else M
+    ldb = N if border == "C" else K
+    layout = (1 if aorder == "C" else 0) | (2 if border == "C" else 0)
+    check(oracle, dt, C.to_numpy()[rows], A, B, M, N, K, lda, ldb, rows, layout)

@@ -62,7 +62,24 @@ def _mid_cases():
     return out
 
 
-@pytest.mark.parametrize("dt,layout,M,N,K", _gemm_cases() + _mid_cases())
+def _mid_mn_cases():
+    """Mid-size products with an M/N-contiguous operand (A column-major or B row-major; M and N
+    multiples of 16, K any where both operands are M/N-contiguous): the mid-size kernel's
+    transposing reads under the automatic choice."""
+    rng = np.random.default_rng(20261203)
+    out = []
+    for _ in range(12):
+        dt = str(rng.choice(["f16", "bf16", "i8"]))
+        layout = int(rng.choice([0, 2, 3, 4, 6, 7]))
+        M = 16 * int(rng.integers(57, 188))
+        N = 16 * int(rng.integers(57, 188))
+        both_mn = layout in (2, 6)
+        K = int(rng.integers(64, 2049)) if both_mn else 16 * int(rng.integers(4, 129))
+        out.append((dt, layout, M, N, K))
+    return out
+
+
+@pytest.mark.parametrize("dt,layout,M,N,K", _gemm_cases() + _mid_cases() + _mid_mn_cases())
 def test_sweep_gemm(gpu, oracle, dt, layout, M, N, K):
     lh = gpu
     announce(f"sweep gemm {dt} layout={layout} M={M} N={N} K={K}")
