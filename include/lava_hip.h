@@ -142,7 +142,8 @@ void lava_hip_kernel_log_clear(void);
  *                        (D <= 128, a multiple of 8, any scale);
  *  LAVA_HIP_FAMILY_GEMM: 1 the 256 x 256 tile kernel, 2 the 64 x 64 small-product kernel
  *                        without a K split, 3 the staged kernel, 4 the 128 x 128 mid-size kernel
- *                        (f16 / bf16 / int8, any operand layout, no epilogue).
+ *                        (f16 / bf16 / int8, any operand layout; the fused epilogue for f16 /
+ *                        bf16).
  * Unknown families or choices return LAVA_HIP_ERR_INVALID_ARG. */
 /* Reads [src, src + bytes) once with 16-byte nontemporal loads, `unroll` (4, 8 or 16) in flight
  * per thread, `blocks` workgroups of 256 threads, and writes the XOR of what each thread read to

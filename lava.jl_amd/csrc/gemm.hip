@@ -5,9 +5,9 @@
 // Compute-bound shapes take the 256 x 256 tile kernel (gemm_tn_kernel.hpp) in any
 // operand layout (K-contiguous operands read directly, M/N-contiguous ones through
 // transposing LDS reads, 16- or 8-bit) -- whole tiles, or ragged extents with
-// zero-clamped loads.  Mid-size products with a plain output (at least 128 tiles of 128 x 128 --
-// 64 for int8 with an M/N-contiguous operand -- and fewer than 144 of 256 x 256:
-// mid_gemm_preferred) take the 128 x 128 kernel (gemm_mid.hip).  Other products of at most 16
+// zero-clamped loads.  Mid-size products, plain or with the fused epilogue (at least 128 tiles of
+// 128 x 128 -- 64 for int8 with an M/N-contiguous operand -- and fewer than 144 of 256 x 256:
+// mid_gemm_preferred), take the 128 x 128 kernel (gemm_mid_kernel.hpp).  Other products of at most 16
 // tiles of 256 x 256, and products that the tile kernel would run on few CUs or mostly empty
 // tiles (small_gemm_preferred's rate estimate), take the 64 x 64 small-product kernel (with K
 // split over the stream's workspace where its tiles alone would leave CUs idle:
@@ -75,12 +75,13 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     const int pin = kernel_override(LAVA_HIP_FAMILY_GEMM);
     const bool small_fits = small_gemm_fits<T>(a, b, M, N, K, lda, ldb, arow, brow);
     const int fit = tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
-    // the 128 x 128 mid-size kernel: plain output
-    if constexpr (!EPI && !U8 && std::is_same<OutT, typename Mfma16<T>::acc_elem>::value) {
-        const int mfit = mid_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, arow, !brow);
+    // the 128 x 128 mid-size kernel: plain output, or the fused epilogue (f16 / bf16)
+    if constexpr (!U8 && (EPI || std::is_same<OutT, typename Mfma16<T>::acc_elem>::value)) {
+        const int mfit = mid_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
         const bool i8_mn = sizeof(T) == 1 && (!arow || brow);
         if (mfit != TN_NO && (pin == 4 || (pin == 0 && mid_gemm_preferred(M, N, i8_mn))))
-            return launch_gemm_mid<T>(a, b, c, M, N, K, lda, ldb, ldc, s, mfit == TN_RAGGED, arow, !brow);
+            return launch_gemm_mid<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, mfit == TN_RAGGED, arow,
+                                                 !brow);
     }
     bool use_small;
     if (pin == 2)

@@ -7,13 +7,15 @@ row-major or column-major (the latter computed as C^T = B^T A^T, which swaps the
 their layouts); ragged M, N and K take the zero-clamped loads (lanes past an extent read zero) and
 the bounds-checked store, as on the 256 x 256 tile kernel whose staging it shares.  Checked: whole
 tiles and ragged extents, a K of one 16-byte chunk, every operand layout, C row- and column-major,
-and a C with padded rows and guard rows after the last (nothing outside the M x N block changes)."""
+a C with padded rows and guard rows after the last (nothing outside the M x N block changes), and the
+fused epilogue (bias, residual, activation, fp32 / f16 / bf16 D) against the oracle's."""
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
 from conftest import announce
+from test_gpu_gemm_epilogue import run_case as run_epilogue_case
 
 pytestmark = pytest.mark.gpu
 
@@ -114,6 +116,35 @@ def test_mid_kernel_layouts(gpu, oracle, mid_kernel, dt, shape, aorder, border, 
     check(oracle, dt, C.to_numpy()[rows], A, B, M, N, K, lda, ldb, rows, layout)
 
 
+@pytest.mark.parametrize("act", ["none", "relu", "gelu_tanh", "gelu_erf"])
+@pytest.mark.parametrize("d", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("ab", ["f16", "bf16"])
+def test_mid_kernel_epilogue(gpu, oracle, mid_kernel, ab, d, act):
+    """The fused epilogue (lava_hip_gemm_ex) on the mid-size kernel: D = act(A B + (bias +
+    residual)) narrowed to D's type, every input and output type and activation, against the
+    oracle's fp64 epilogue rounded to D's type (every row)."""
+    announce(f"gemm_ex mid {ab}->{d} act={act} bias+residual")
+    run_epilogue_case(gpu, oracle, ab, d, 384, 256, 320, 1 | 4, act, True, True, 3500)
+
+
+@pytest.mark.parametrize("layout", range(8))
+@pytest.mark.parametrize("shape", [(1000, 776, 520), (256, 1024, 64)])
+def test_mid_kernel_epilogue_layouts(gpu, oracle, mid_kernel, layout, shape):
+    """Every operand and D layout with ragged extents: a column-major D runs as its row-major
+    transpose, where the bias runs along the columns; M, N, K end inside a tile."""
+    M, N, K = shape
+    announce(f"gemm_ex mid layout={layout} M={M} N={N} K={K}")
+    run_epilogue_case(gpu, oracle, "bf16", "bf16", M, N, K, layout, "gelu_erf", True, True, 3600 + layout)
+
+
+@pytest.mark.parametrize("with_bias,with_res", [(False, False), (True, False), (False, True)])
+def test_mid_kernel_epilogue_terms(gpu, oracle, mid_kernel, with_bias, with_res):
+    """Each accumulator-init term alone, and neither; N = 777 makes the residual's rows (ldr = N)
+    unaligned to 16 bytes, so the terms are read by element, and the last column group ragged."""
+    announce(f"gemm_ex mid bias={with_bias} residual={with_res}")
+    run_epilogue_case(gpu, oracle, "f16", "f32", 1000, 777, 256, 1 | 4, "relu", with_bias, with_res, 3700)
+
+
 @pytest.mark.parametrize("dt", ["bf16", "i8"])
 def test_mid_kernel_store_stays_inside(gpu, oracle, mid_kernel, dt):
     """C row-major with ldc = N + 3 (rows not 16-byte aligned: element stores) inside a buffer
@@ -204,3 +235,32 @@ def test_mid_kernel_automatic_choice(gpu, oracle, dt, shape, kernel, aorder, bor
     ldb = N if border == "C" else K
     layout = (1 if aorder == "C" else 0) | (2 if border == "C" else 0)
     check(oracle, dt, C.to_numpy()[rows], A, B, M, N, K, lda, ldb, rows, layout)
+
+
+@pytest.mark.parametrize("shape,kernel", [((2048, 2048, 2048), "gemm_mid_kernel"),
+                                          ((2048, 4096, 1024), "gemm_mid_kernel"),
+                                          ((3072, 3072, 1024), "gemm_tn_kernel")])
+def test_mid_kernel_epilogue_automatic_choice(gpu, oracle, shape, kernel):
+    """lava_hip_gemm_ex (bf16 -> bf16, bias + residual + gelu_tanh) takes the same automatic
+    choice as the plain product; sampled rows against the oracle's fp64 epilogue."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm_ex automatic choice bf16 M={M} N={N} K={K}: {kernel}")
+    A = lh.HIPDeviceArray("bf16", (M, K), order="C")
+    B = lh.HIPDeviceArray("bf16", (K, N), order="F")
+    D = lh.HIPDeviceArray("bf16", (M, N), order="C")
+    bias = lh.HIPDeviceArray("f32", (M,))
+    res = lh.HIPDeviceArray("f32", (M, N), order="C")
+    lh.fill_uniform(A, 8700, -1.0, 1.0)
+    lh.fill_uniform(B, 8701, -1.0, 1.0)
+    lh.fill_uniform(bias, 8702, -1.0, 1.0)
+    lh.fill_uniform(res, 8703, -2.0, 2.0)
+    lh.kernel_log_clear()
+    lh.gemm_ex(D, A, B, bias=bias, residual=res, act="gelu_tanh")
+    assert kernel in lh.kernel_log(), lh.kernel_log()
+    rows = np.array([0, 1, 127, 128, M // 2, M - 1])
+    c = oracle.gemm_rows(host_flat(A), "bf16", host_flat(B), "bf16", M, N, K, K, K, 1, rows)
+    ref = oracle.round_to(oracle.gemm_epilogue(c, bias.to_numpy()[rows], res.to_numpy()[rows], "gelu_tanh"), "bf16")
+    got = oracle.bf16_bits_to_f32(D.to_numpy()[rows]).astype(np.float64)
+    err = oracle.rel_frobenius(got, ref)
+    assert err <= TOL, err
