@@ -6,8 +6,8 @@
 // operand layout (K-contiguous operands read directly, M/N-contiguous ones through
 // transposing LDS reads, 16- or 8-bit) -- whole tiles, or ragged extents with
 // zero-clamped loads.  Mid-size products, plain or with the fused epilogue (at least 128 tiles of
-// 128 x 128 -- 64 for int8 with an M/N-contiguous operand -- and fewer than 144 of 256 x 256:
-// mid_gemm_preferred), take the 128 x 128 kernel (gemm_mid_kernel.hpp).  Other products of at most 16
+// 128 x 128 -- 64 for int8 with an M/N-contiguous operand -- and fewer than 144 of 256 x 256, or
+// 257 to 336 of them: mid_gemm_preferred), take the 128 x 128 kernel (gemm_mid_kernel.hpp).  Other products of at most 16
 // tiles of 256 x 256, and products that the tile kernel would run on few CUs or mostly empty
 // tiles (small_gemm_preferred's rate estimate), take the 64 x 64 small-product kernel (with K
 // split over the stream's workspace where its tiles alone would leave CUs idle:
