@@ -142,8 +142,8 @@ void lava_hip_kernel_log_clear(void);
  *                        (D <= 128, a multiple of 8, any scale);
  *  LAVA_HIP_FAMILY_GEMM: 1 the 256 x 256 tile kernel, 2 the 64 x 64 small-product kernel
  *                        without a K split, 3 the staged kernel, 4 the 128 x 128 mid-size kernel
- *                        (f16 / bf16 / int8, any operand layout; the fused epilogue for f16 /
- *                        bf16).
+ *                        (f16 / bf16 / int8 / unsigned bytes, any operand layout; the fused
+ *                        epilogue for f16 / bf16).
  * Unknown families or choices return LAVA_HIP_ERR_INVALID_ARG. */
 /* Reads [src, src + bytes) once with 16-byte nontemporal loads, `unroll` (4, 8 or 16) in flight
  * per thread, `blocks` workgroups of 256 threads, and writes the XOR of what each thread read to
@@ -426,13 +426,13 @@ int lava_hip_gemm_i8_i32(const void* A, const void* B, void* C, int64_t M, int64
 
 /* uint8 x uint8 -> uint32, all operands unsigned (src/compiler/spirv/coopmat.jl:115-151 emits no
  * signed-component bits for UInt8 coopmats; test/spirv/test_coopmat_int8.jl:71-98), exact with
- * the 32-bit accumulator's wrap; C holds uint32.  The MFMA is signed only: the tile kernel and
- * the small-product kernel multiply the bytes flipped by 128 (u - 128) and add 128 (row sum +
+ * the 32-bit accumulator's wrap; C holds uint32.  The MFMA is signed only: the tile, mid-size
+ * and small-product kernels multiply the bytes flipped by 128 (u - 128) and add 128 (row sum +
  * column sum) + 16384 K back after their last k-step.  The kernel choice is the signed one's
- * (tile kernel, small-product kernel with K split through the per-stream workspace, in their
- * unsigned forms); shapes neither MFMA kernel takes (a K-contiguous K or an M/N-contiguous M/N
- * not a multiple of 16, 16-byte misaligned operands or leading dimensions) run on a
- * one-thread-per-element kernel.  Same layouts and leading-dimension rules as above. */
+ * (tile kernel, 128 x 128 mid-size kernel, small-product kernel with K split through the
+ * per-stream workspace, in their unsigned forms); shapes no MFMA kernel takes (a K-contiguous K or
+ * an M/N-contiguous M/N not a multiple of 16, 16-byte misaligned operands or leading dimensions)
+ * run on a one-thread-per-element kernel.  Same layouts and leading-dimension rules as above. */
 int lava_hip_gemm_u8_u32(const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                          int64_t ldb, int64_t ldc, uint32_t layout, void* stream);
 

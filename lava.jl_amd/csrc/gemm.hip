@@ -75,13 +75,13 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     const int pin = kernel_override(LAVA_HIP_FAMILY_GEMM);
     const bool small_fits = small_gemm_fits<T>(a, b, M, N, K, lda, ldb, arow, brow);
     const int fit = tn_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
-    // the 128 x 128 mid-size kernel: plain output, or the fused epilogue (f16 / bf16)
-    if constexpr (!U8 && (EPI || std::is_same<OutT, typename Mfma16<T>::acc_elem>::value)) {
+    // the 128 x 128 mid-size kernel: plain output, the fused epilogue (f16 / bf16) or unsigned bytes
+    if constexpr (EPI || std::is_same<OutT, typename Mfma16<T>::acc_elem>::value) {
         const int mfit = mid_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
         const bool i8_mn = sizeof(T) == 1 && (!arow || brow);
         if (mfit != TN_NO && (pin == 4 || (pin == 0 && mid_gemm_preferred(M, N, i8_mn))))
-            return launch_gemm_mid<T, OutT, EPI>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, mfit == TN_RAGGED, arow,
-                                                 !brow);
+            return launch_gemm_mid<T, OutT, EPI, U8>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, mfit == TN_RAGGED, arow,
+                                                     !brow);
     }
     bool use_small;
     if (pin == 2)

@@ -72,14 +72,14 @@ int launch_gemm_tn_u8(const int8_t* A, const int8_t* B, int32_t* C, int64_t M, i
                       int64_t ldb, int64_t ldc, hipStream_t s, bool ragged, bool ak, bool bk);
 // The mid-size kernel (gemm_mid_kernel.hpp): 128 x 128 tiles, two workgroups per CU; f16 / bf16 /
 // int8, each operand K- or M/N-contiguous (ak: A row-major, bk: B column-major); fp32 / int32 output,
-// or (EPI, f16 / bf16) the fused epilogue into OutT.  mid_gemm_eligible() gives TN_FULL (whole
+// or (EPI, f16 / bf16) the fused epilogue into OutT, or (U8) unsigned bytes into uint32 words.  mid_gemm_eligible() gives TN_FULL (whole
 // tiles and 128-byte K steps, C rows of 4 c_elem-byte elements aligned), TN_RAGGED (any extents: K
 // a multiple of the 16-byte chunk for a K-contiguous operand, M or N of it for an M/N-contiguous one)
 // or TN_NO.
 template <typename T>
 int mid_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, int64_t N, int64_t K, int64_t lda,
                       int64_t ldb, int64_t ldc, size_t c_elem, bool ak, bool bk);
-template <typename T, typename OutT, bool EPI>
+template <typename T, typename OutT, bool EPI, bool U8 = false>
 int launch_gemm_mid(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                     int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged, bool ak, bool bk);
 // Whether an M x N product takes the mid-size kernel when it fits (the measured choice against the

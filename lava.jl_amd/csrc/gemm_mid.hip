@@ -1,6 +1,6 @@
 // gemm_mid.hip -- the mid-size GEMM kernel's applicability and kernel-choice rule, and its plain
-// (fp32 / int32 output) instances; the kernel is in gemm_mid_kernel.hpp, the fused-epilogue
-// instances in gemm_mid_ex.hip.
+// (fp32 / int32 output) instances; the kernel is in gemm_mid_kernel.hpp, the fused-epilogue and
+// unsigned-byte instances in gemm_mid_ex.hip.
 #include "gemm_mid_kernel.hpp"
 
 namespace lava {
@@ -48,9 +48,9 @@ bool mid_gemm_preferred(int64_t M, int64_t N, bool i8_mn) {
     return t128 >= (i8_mn ? 64 : 128) && (t256 < 144 || (t256 > 256 && t256 <= 336));
 }
 
-LAVA_MID_LAUNCH_INST(f16, float, false)
-LAVA_MID_LAUNCH_INST(bf16, float, false)
-LAVA_MID_LAUNCH_INST(int8_t, int32_t, false)
+LAVA_MID_LAUNCH_INST(f16, float, false, false)
+LAVA_MID_LAUNCH_INST(bf16, float, false, false)
+LAVA_MID_LAUNCH_INST(int8_t, int32_t, false, false)
 template int mid_gemm_eligible<f16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t,
                                     int64_t, size_t, bool, bool);
 template int mid_gemm_eligible<bf16>(const void*, const void*, const void*, int64_t, int64_t, int64_t, int64_t,

@@ -3,8 +3,8 @@
 // (2048^3: 64 of them, against 256 tiles of 128 x 128) and that the 64 x 64 small-product kernel runs
 // well below the matrix cores' rate.  f16, bf16 or int8, each operand K-contiguous (A row-major, B
 // column-major) or M/N-contiguous; fp32 / int32 output, or for f16 / bf16 the fused epilogue (bias,
-// residual, activation, narrowed to fp32 / f16 / bf16).  The staging is the tile kernel's at 128 rows
-// (gemm_tn_kernel.hpp: TnSide<T, true, 128>, LDS-DMA of 128 bytes of K per m or n row, chunk ^ row %
+// residual, activation, narrowed to fp32 / f16 / bf16), or for unsigned bytes the uint32 product.
+// The staging is the tile kernel's at 128 rows (gemm_tn_kernel.hpp: TnSide<T, true, 128>, LDS-DMA of 128 bytes of K per m or n row, chunk ^ row %
 // 8; TnSide<T, false, 128>, 128 bytes of K as rows of 128 m or n, read back transposed) on a quarter
 // of its LDS, so that two workgroups share a CU and their wavefronts interleave on each SIMD:
 //  * 4 wavefronts, each a 64 x 64 sub-tile = 4 x 4 16x16 accumulators (64 registers per lane);
@@ -15,7 +15,7 @@
 //  * the epilogue stages 32 rows x 64 columns per wavefront at a time through LDS and stores whole
 //    row runs (4 rows per instruction), nontemporal; with the fused epilogue the lane's bias and
 //    residual values of a half are requested before its staging, as in the tile kernel.
-// The plain instances live in gemm_mid.hip, the fused-epilogue ones in gemm_mid_ex.hip.
+// The plain instances live in gemm_mid.hip, the fused-epilogue and unsigned ones in gemm_mid_ex.hip.
 #pragma once
 #include "gemm_tn_kernel.hpp"
 
@@ -24,13 +24,18 @@ namespace lava {
 constexpr int TM_TILE = 128;
 constexpr int TM_SLICE = TM_TILE * TN_KB;   // 16 KB
 
-template <typename T, typename OutT, bool EPI, bool RAGGED, bool AK, bool BK>
+// U8 (T = int8_t storage holding unsigned bytes, int32 C holding the uint32 product): the tile
+// kernel's identity (gemm_tn_kernel.hpp) -- signed MFMAs on the bytes flipped by 128, C = A_s B_s +
+// 128 (RA[m] + CB[n]) + 16384 Kp modulo 2^32 with RA, CB the row and column sums of the flipped
+// bytes and Kp the k positions accumulated, zero padding included.
+template <typename T, typename OutT, bool EPI, bool RAGGED, bool AK, bool BK, bool U8 = false>
 __global__ void __launch_bounds__(256, 2)
     gemm_mid_kernel(const T* __restrict__ A, const T* __restrict__ B, OutT* __restrict__ C, int tiles_m, int tiles_n,
                     int ktiles, int64_t lda_b, int64_t ldb_b, int64_t ldc, Epilogue epi, TnBounds bnd) {
     using AccV = typename Mfma16<T>::acc_t;
     typedef typename Mfma16<T>::acc_elem Acc;
     static_assert(EPI || std::is_same<OutT, Acc>::value, "a plain product writes the accumulator type");
+    static_assert(!U8 || (std::is_same<T, int8_t>::value && !EPI), "U8: bytes in int8_t storage, plain int32 output");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * 2 * TM_SLICE];   // [stage][A, B][16 KB]
 
     const int lane = threadIdx.x & 63;
@@ -102,6 +107,34 @@ __global__ void __launch_bounds__(256, 2)
         rd8(fa, smem, 0, t);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // U8: signed-byte sums of this wavefront's A rows (ra[i]: row 16 i + lane % 16 of its 64) and
+    // B columns (rb[j]), over the k bytes of this lane's 16-lane group
+    int32_t ra[4], rb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ra[i] = rb[i] = 0;
+    auto flip = [&](uint4& v, int32_t& sum) __attribute__((always_inline)) {
+        v.x ^= 0x80808080u;
+        v.y ^= 0x80808080u;
+        v.z ^= 0x80808080u;
+        v.w ^= 0x80808080u;
+        sum = __builtin_amdgcn_sdot4((int)v.x, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)v.y, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)v.z, 0x01010101, sum, false);
+        sum = __builtin_amdgcn_sdot4((int)v.w, 0x01010101, sum, false);
+    };
+    // fragment t in read order (a[0], b[0..3], a[1..3]).  Each is flipped two reads after its own
+    // read was issued, before its first MFMA; the last two of a k-step (a[2], a[3], first used by
+    // MFMAs 8 and 12) are flipped at MFMAs 2 and 6 of the next half.  Fragments read past the last
+    // k-tile are never flipped, so they do not enter the sums.
+    auto flip_t = [&](F8& f, int t) __attribute__((always_inline)) {
+        if constexpr (U8) {
+            if (t == 0) flip(f.a[0], ra[0]);
+            else if (t <= 4) flip(f.b[t - 1], rb[t - 1]);
+            else flip(f.a[t - 4], ra[t - 4]);
+        }
+    };
+#pragma unroll
+    for (int t = 0; t < 8; ++t) flip_t(fa, t);
 
     for (int kt = 0; kt < ktiles; ++kt) {
         const int st = kt & 1;
@@ -112,6 +145,8 @@ __global__ void __launch_bounds__(256, 2)
         for (int q = 0; q < 16; ++q) {
             acc[q >> 2][q & 3] = Mfma16<T>::run(fa.b[q & 3], fa.a[q >> 2], acc[q >> 2][q & 3]);
             if (q & 1) rd8(fb, base, 1, q >> 1);
+            if ((q == 2 || q == 6) && kt > 0) flip_t(fa, 6 + (q >> 2));
+            if ((q & 1) && q >= 5) flip_t(fb, (q >> 1) - 2);
             __builtin_amdgcn_sched_barrier(0);
         }
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's part of tile kt + 1 landed
@@ -122,6 +157,8 @@ __global__ void __launch_bounds__(256, 2)
             acc[q >> 2][q & 3] = Mfma16<T>::run(fb.b[q & 3], fb.a[q >> 2], acc[q >> 2][q & 3]);
             if (q & 1) dma(q >> 1, st, kofs2);
             else rd8(fa, next, 0, q >> 1);
+            if (q == 2 || q == 6) flip_t(fb, 6 + (q >> 2));
+            if (!(q & 1) && q >= 4 && kt + 1 < ktiles) flip_t(fa, (q >> 1) - 2);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -131,6 +168,30 @@ __global__ void __launch_bounds__(256, 2)
     // 8.5 KB of the idle stage buffers, then reads whole 256-byte rows back, 4 per instruction.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if constexpr (U8) {
+        // full sums: the four 16-lane groups hold the four 16-byte quarters of every k-step
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ra[i] += __shfl_xor(ra[i], 16, 64);
+            ra[i] += __shfl_xor(ra[i], 32, 64);
+            rb[i] += __shfl_xor(rb[i], 16, 64);
+            rb[i] += __shfl_xor(rb[i], 32, 64);
+        }
+        // acc[i][j] register r: row 16 i + lane % 16 (this lane's ra[i]), column 16 j + 4 (lane / 16) + r
+        // (rb[j] of lane 4 (lane / 16) + r)
+        const uint32_t kconst = 16384u * (uint32_t)ktiles * (uint32_t)TN_KB;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t cb[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cb[r] = (uint32_t)__shfl(rb[j], 4 * (lane >> 4) + r, 64);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[i][j][r] = (int32_t)((uint32_t)acc[i][j][r] + 128u * ((uint32_t)ra[i] + cb[r]) + kconst);
+        }
+    }
     constexpr int EP_PITCH = 64 * 4 + 16;
     typedef Acc Acc4 __attribute__((ext_vector_type(4)));
     typedef float F4 __attribute__((ext_vector_type(4)));
@@ -236,20 +297,20 @@ __global__ void __launch_bounds__(256, 2)
     half(std::integral_constant<int, 1>{});
 }
 
-template <typename T, typename OutT, bool EPI, bool AK, bool BK>
+template <typename T, typename OutT, bool EPI, bool AK, bool BK, bool U8>
 void launch_mid_layout(const T* A, const T* B, OutT* C, int tiles_m, int tiles_n, int ktiles, int64_t lda_b,
                        int64_t ldb_b, int64_t ldc, const Epilogue& epi, const TnBounds& bnd, hipStream_t s,
                        bool ragged) {
     const dim3 grid((unsigned)(tiles_m * tiles_n));
     if (ragged)
-        hipLaunchKernelGGL((gemm_mid_kernel<T, OutT, EPI, true, AK, BK>), grid, dim3(256), 0, s, A, B, C, tiles_m,
+        hipLaunchKernelGGL((gemm_mid_kernel<T, OutT, EPI, true, AK, BK, U8>), grid, dim3(256), 0, s, A, B, C, tiles_m,
                            tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
     else
-        hipLaunchKernelGGL((gemm_mid_kernel<T, OutT, EPI, false, AK, BK>), grid, dim3(256), 0, s, A, B, C, tiles_m,
+        hipLaunchKernelGGL((gemm_mid_kernel<T, OutT, EPI, false, AK, BK, U8>), grid, dim3(256), 0, s, A, B, C, tiles_m,
                            tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd);
 }
 
-template <typename T, typename OutT, bool EPI>
+template <typename T, typename OutT, bool EPI, bool U8>
 int launch_gemm_mid(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                     int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged, bool ak, bool bk) {
     const int tiles_m = (int)((M + TM_TILE - 1) / TM_TILE), tiles_n = (int)((N + TM_TILE - 1) / TM_TILE);
@@ -262,23 +323,23 @@ int launch_gemm_mid(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64
     bnd.cvec = ldc % 4 == 0 && aligned(C, 4 * sizeof(OutT));
     const int64_t lda_b = lda * (int64_t)sizeof(T), ldb_b = ldb * (int64_t)sizeof(T);
     if (!ak && !bk)
-        launch_mid_layout<T, OutT, EPI, false, false>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd,
+        launch_mid_layout<T, OutT, EPI, false, false, U8>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd,
                                                       s, ragged);
     else if (!ak)
-        launch_mid_layout<T, OutT, EPI, false, true>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd, s,
+        launch_mid_layout<T, OutT, EPI, false, true, U8>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd, s,
                                                      ragged);
     else if (!bk)
-        launch_mid_layout<T, OutT, EPI, true, false>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd, s,
+        launch_mid_layout<T, OutT, EPI, true, false, U8>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd, s,
                                                      ragged);
     else
-        launch_mid_layout<T, OutT, EPI, true, true>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd, s,
+        launch_mid_layout<T, OutT, EPI, true, true, U8>(A, B, C, tiles_m, tiles_n, ktiles, lda_b, ldb_b, ldc, epi, bnd, s,
                                                     ragged);
     LAVA_LAUNCH_CHECK("gemm_mid_kernel");
     return LAVA_HIP_OK;
 }
 
-#define LAVA_MID_LAUNCH_INST(T, O, E)                                                                             \
-    template int launch_gemm_mid<T, O, E>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t,     \
-                                          int64_t, hipStream_t, const Epilogue&, bool, bool, bool);
+#define LAVA_MID_LAUNCH_INST(T, O, E, U)                                                                          \
+    template int launch_gemm_mid<T, O, E, U>(const T*, const T*, O*, int64_t, int64_t, int64_t, int64_t, int64_t,  \
+                                             int64_t, hipStream_t, const Epilogue&, bool, bool, bool);
 
 }  // namespace lava

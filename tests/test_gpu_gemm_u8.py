@@ -1,7 +1,7 @@
 """uint8 x uint8 -> uint32 GEMM (the unsigned coopmat product of test/spirv/test_coopmat_int8.jl:71-98,
 whose operands carry no signed-component bits) at matrix scale, against the oracle, bit for bit.
 
-The tile kernel and the small-product kernel run it as a signed int8 product of the bytes flipped
+The tile, mid-size and small-product kernels run it as a signed int8 product of the bytes flipped
 by 128 plus a row-sum and column-sum correction; the tests pin the identity where it can go wrong:
 every operand layout, ragged M, N and K (the zero padding of a ragged K enters the identity), the
 extremes 0 and 255, a K long enough that the 32-bit sum wraps, split K (each split's partial
@@ -79,17 +79,17 @@ def test_gemm_u8_full_size(gpu, oracle):
     assert got == want
 
 
-@pytest.mark.parametrize("kernel", ["gemm_tn_kernel", "gemm_small_kernel<u8>", "splitk_sum_kernel"])
+@pytest.mark.parametrize("kernel", ["gemm_tn_kernel", "gemm_mid_kernel", "gemm_small_kernel<u8>", "splitk_sum_kernel"])
 @pytest.mark.parametrize("value", [0, 255])
 def test_gemm_u8_extremes_and_wrap(gpu, oracle, pin_gemm, value, kernel):
     """Every byte 0 or 255 (the extremes of the flipped encoding: -128 and 127) with K = 66064,
     where 255^2 K = 4295811600 passes 2^32: C must hold the product modulo 2^32 -- on the tile
-    kernel, on the small kernel unsplit, and on the small kernel with K split (the automatic choice
-    at this shape)."""
+    kernel, on the mid-size kernel, on the small kernel unsplit, and on the small kernel with K
+    split (the automatic choice at this shape)."""
     lh = gpu
     M, N, K = 256, 256, 66064
     announce(f"gemm u8 extremes value={value} K={K} kernel={kernel}")
-    pin_gemm({"gemm_tn_kernel": 1, "gemm_small_kernel<u8>": 2, "splitk_sum_kernel": 0}[kernel])
+    pin_gemm({"gemm_tn_kernel": 1, "gemm_mid_kernel": 4, "gemm_small_kernel<u8>": 2, "splitk_sum_kernel": 0}[kernel])
     A = lh.HIPDeviceArray("u8", (M, K), order="C")
     B = lh.HIPDeviceArray("u8", (K, N), order="F")
     A.fill_bytes(value)
@@ -100,6 +100,47 @@ def test_gemm_u8_extremes_and_wrap(gpu, oracle, pin_gemm, value, kernel):
     assert kernel in lh.kernel_log(), lh.kernel_log()
     want = (value * value * K) % (1 << 32)
     assert np.all(C.to_numpy() == np.uint32(want))
+
+
+@pytest.mark.parametrize("layout", range(8))
+@pytest.mark.parametrize("shape", [(512, 768, 1024), (1008, 784, 528), (144, 272, 16), (128, 128, 8208)])
+def test_gemm_u8_mid_kernel(gpu, oracle, pin_gemm, layout, shape):
+    """The mid-size kernel's unsigned form (128 x 128 tiles) in every layout: whole tiles, ragged M,
+    N and K (K = 528, 8208: a last k-tile of 16 bytes, whose zero padding enters the identity), a K
+    of one 16-byte chunk, against the oracle bit for bit."""
+    lh = gpu
+    M, N, K = shape
+    announce(f"gemm u8 mid kernel layout={layout} M={M} N={N} K={K}")
+    pin_gemm(4)
+    A, B = _inputs(lh, M, N, K, layout, 90 + layout)
+    C = lh.HIPDeviceArray("u32", (M, N), order="C" if layout & 4 else "F")
+    C.fill_bytes(0xFF)
+    lh.kernel_log_clear()
+    lh.gemm(C, A, B)
+    assert "gemm_mid_kernel" in lh.kernel_log(), lh.kernel_log()
+    rows = np.unique(np.concatenate([np.arange(0, M, 9), [r for r in (1, 15, 16, 127, 128, M - 1) if r < M]]))
+    _check(oracle, A, B, C, M, N, K, layout, rows)
+
+
+@pytest.mark.parametrize("layout,kernel", [(5, "gemm_mid_kernel"), (0, "gemm_mid_kernel"), (2, "gemm_mid_kernel")])
+def test_gemm_u8_mid_size_automatic(gpu, oracle, layout, kernel):
+    """2048 x 2048 x 4096 under the automatic choice (the mid-size kernel): sampled rows bit for bit,
+    and every element through the sum of C modulo 2^32 against the closed form (column sums of A) .
+    (row sums of B)."""
+    lh = gpu
+    M, N, K = 2048, 2048, 4096
+    announce(f"gemm u8 {M}x{N}x{K} layout={layout} automatic")
+    A, B = _inputs(lh, M, N, K, layout, 95 + layout)
+    C = lh.HIPDeviceArray("u32", (M, N), order="C" if layout & 4 else "F")
+    lh.kernel_log_clear()
+    lh.gemm(C, A, B)
+    assert kernel in lh.kernel_log(), lh.kernel_log()
+    _check(oracle, A, B, C, M, N, K, layout, np.array([0, 1, 127, 128, 1024, 2047]))
+    a = A.to_numpy().astype(np.uint64)
+    b = B.to_numpy().astype(np.uint64)
+    want = int((a.sum(axis=0) * b.sum(axis=1)).sum()) % (1 << 32)
+    got = int(C.to_numpy().astype(np.uint64).sum()) % (1 << 32)
+    assert got == want
 
 
 @pytest.mark.parametrize("layout", range(8))
