@@ -11,7 +11,7 @@ before timing starts.
   python bench.py [--gpus 1] [--steps K] [--warmup W]
                   [--workload headline|gemm_bf16|attn|gemm_i8|w8a16|gemm_f16_256|gemm_bf16_4096|gemm_ex_bf16|vendor_bf16|
                               gemm_bf16_ragged|gemm_cm2_f16|gemm_bf16_nn|gemm_shapes|attn_d64|attn_d96|attn_d256|w8a16_wrow|w8a16_julia|copy|
-                              hbm_read|gemm_u8|mfma_loop|gemm_bf16_pad64|w8a16_m64]
+                              hbm_read|gemm_u8|mfma_loop|gemm_bf16_pad64|w8a16_m64|gemm_mid]
 
 A step is one kernel launch over the whole problem (for the W8A16 and 256^3
 workloads, whose kernels take microseconds, 10 back-to-back launches:
@@ -359,7 +359,7 @@ def main():
                     choices=["headline", "gemm_bf16", "attn", "gemm_i8", "w8a16", "gemm_f16_256", "gemm_bf16_4096",
                              "gemm_ex_bf16", "gemm_bf16_ragged", "gemm_cm2_f16", "gemm_bf16_nn", "attn_d64", "attn_d96", "attn_d256",
                              "copy", "hbm_read", "vendor_bf16", "w8a16_wrow", "w8a16_julia", "gemm_shapes", "gemm_u8",
-                             "mfma_loop", "gemm_bf16_pad64", "w8a16_m64"])
+                             "mfma_loop", "gemm_bf16_pad64", "w8a16_m64", "gemm_mid"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--settle", type=float, default=1.0,
                     help="seconds of untimed load before the warmup, for the clock to leave its idle state")
@@ -423,6 +423,14 @@ def main():
         flop, kms, wms = bench_gemm(lh, "bf16", 4096, K, W, stream, 1)
         out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
                     "dtype": "bf16", "config": {"workload": "bf16 GEMM 4096^3 A row-major B column-major"},
+                    "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
+                    "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
+    elif args.workload == "gemm_mid":
+        # a mid-size product: 256 tiles of 128 x 128 (64 of 256 x 256), the 128 x 128 kernel's share
+        flop, kms, wms = bench_gemm(lh, "bf16", 0, K, W, stream, 1, shape=(2048, 4096, 4096))
+        out.update({"value": round(flop / (wms * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "ms_per_step": round(wms, 4),
+                    "dtype": "bf16", "config": {"workload": "bf16 GEMM M=2048 N=4096 K=4096, A row-major, B "
+                                                            "column-major (the mid-size kernel)"},
                     "kernel_ms": round(kms, 4), "kernel_ms_mean": round(TIMED_MEAN_MS[0], 4),
                     "roofline": roofline("mfma", flop / (kms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "TFLOP/s", None)})
     elif args.workload == "gemm_bf16_ragged":
