@@ -6,8 +6,8 @@
 // operand layout (K-contiguous operands read directly, M/N-contiguous ones through
 // transposing LDS reads, 16- or 8-bit) -- whole tiles, or ragged extents with
 // zero-clamped loads.  Mid-size products, plain or with the fused epilogue (at least 128 tiles of
-// 128 x 128 -- 64 for int8 with an M/N-contiguous operand -- and fewer than 144 of 256 x 256, or
-// 257 to 336 of them: mid_gemm_preferred), take the 128 x 128 kernel (gemm_mid_kernel.hpp).  Other products of at most 16
+// 128 x 128 and fewer than 144 of 256 x 256, or 257 to 336 of them: mid_gemm_preferred), take the
+// 128 x 128 kernel (gemm_mid_kernel.hpp).  Other products of at most 16
 // tiles of 256 x 256, and products that the tile kernel would run on few CUs or mostly empty
 // tiles (small_gemm_preferred's rate estimate), take the 64 x 64 small-product kernel (with K
 // split over the stream's workspace where its tiles alone would leave CUs idle:
@@ -78,8 +78,7 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     // the 128 x 128 mid-size kernel: plain output, the fused epilogue (f16 / bf16) or unsigned bytes
     if constexpr (EPI || std::is_same<OutT, typename Mfma16<T>::acc_elem>::value) {
         const int mfit = mid_gemm_eligible<T>(a, b, c, M, N, K, lda, ldb, ldc, sizeof(OutT), arow, !brow);
-        const bool i8_mn = sizeof(T) == 1 && (!arow || brow);
-        if (mfit != TN_NO && (pin == 4 || (pin == 0 && mid_gemm_preferred(M, N, i8_mn))))
+        if (mfit != TN_NO && (pin == 4 || (pin == 0 && mid_gemm_preferred(M, N))))
             return launch_gemm_mid<T, OutT, EPI, U8>(a, b, c, M, N, K, lda, ldb, ldc, s, epi, mfit == TN_RAGGED, arow,
                                                      !brow);
     }
@@ -89,7 +88,7 @@ int gemm_entry(const char* name, const void* A, const void* B, void* C, int64_t 
     else if (pin == 3 || (pin == 1 && fit != TN_NO))
         use_small = false;
     else
-        use_small = small_fits && small_gemm_preferred<T>(M, N, K, !arow || brow);
+        use_small = small_fits && small_gemm_preferred<T>(M, N, K);
     if (use_small) {
         if constexpr (!EPI) {
             const SmallSplit sp = pin == 2 ? SmallSplit{} : small_gemm_splits<T>(M, N, K);

@@ -110,7 +110,12 @@ __global__ void __launch_bounds__(256) gemm_staged_kernel(const T* __restrict__ 
 //  * an M/N-contiguous 16-bit operand is copied as loaded too, [k][row] (128-byte rows padded to
 //    144), and its fragments are read with two ds_read_b64_tr_b16 (4 k-values of one column per
 //    lane each);
-//  * an M/N-contiguous int8 operand is transposed by byte stores into the [row][k] layout.
+//  * an M/N-contiguous int8 operand is copied as loaded, [k][row] with 64-byte rows, chunk c of k
+//    row k at slot c ^ F(k), F(k) = (k / 4 % 2) | 2 ((k / 16 + k / 32) % 2), and its fragments are
+//    read with two ds_read_b64_tr_b8 (8 k-values of one column per lane each).  A 32-lane pass of
+//    such a read covers 16 k rows (8 consecutive ones from each of two 16-lane groups, 16 or 32
+//    apart) x one 16-byte column block; F gives the four rows of each k % 4 class distinct slots, so
+//    the pass reads every bank once.
 // Host conditions (small_gemm_fits): 16-byte aligned operands and leading dimensions, K a
 // multiple of EV when an operand is K-contiguous, M (N) a multiple of EV when A (B) is M (N)-
 // contiguous -- so every 16-byte chunk is wholly inside or wholly outside the matrix, and the
@@ -136,12 +141,15 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
     constexpr int PITCH = 528;                // [row][k] layout: LDS bytes per row
     constexpr int PTR = 144;                  // [k][row] layout (16-bit types): LDS bytes per k
     constexpr int JR = 64 / EV;               // 16-byte chunks across the 64 rows of an M/N-contiguous chunk
-    constexpr bool A_TR = !AROW && sizeof(T) == 2;   // A read through transposing LDS reads
-    constexpr bool B_TR = BROW && sizeof(T) == 2;
-    // each operand's staging sized for its own layout ([k][row] only for a transposed 16-bit operand):
-    // int8 needs 2 x 33 KB, so two workgroups share a CU
-    __shared__ __attribute__((aligned(16))) uint8_t As[A_TR ? KC * PTR : 64 * PITCH];
-    __shared__ __attribute__((aligned(16))) uint8_t Bs[B_TR ? KC * PTR : 64 * PITCH];
+    constexpr bool A_TR = !AROW;                      // A read through transposing LDS reads
+    constexpr bool B_TR = BROW;
+    constexpr int TR_BYTES = sizeof(T) == 2 ? KC * PTR : KC * 64;   // [k][row] staging of a transposed operand
+    // each operand's staging sized for its own layout: int8 needs 2 x 33 KB at most, so two
+    // workgroups share a CU
+    __shared__ __attribute__((aligned(16))) uint8_t As[A_TR ? TR_BYTES : 64 * PITCH];
+    __shared__ __attribute__((aligned(16))) uint8_t Bs[B_TR ? TR_BYTES : 64 * PITCH];
+    // the int8 [k][row] swizzle F(k)
+    auto f8 = [](int k) __attribute__((always_inline)) { return ((k >> 2) & 1) | ((((k >> 4) ^ (k >> 5)) & 1) << 1); };
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
@@ -180,22 +188,14 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
                 x.y ^= 0x80808080u;
                 x.z ^= 0x80808080u;
                 x.w ^= 0x80808080u;
-            } else if constexpr (sizeof(T) == 1 && !decltype(kcont)::value) {
-                // an opaque use of the loaded words before their byte stores: without it the
-                // compiler holds the bytes of all 8 loads apart (256-304 VGPRs, one workgroup per
-                // CU); with it 180-192, two workgroups (int8 A column-major 64 x 14336 x 4096:
-                // 146 -> 226 TOP/s; both operands M/N-contiguous at 2048^3: 116 -> 228)
-                asm volatile("; keep" : "+v"(x.x), "+v"(x.y), "+v"(x.z), "+v"(x.w));
             }
             if constexpr (decltype(kcont)::value) {
                 *reinterpret_cast<uint4*>(S + (e >> 5) * PITCH + 16 * (e & 31)) = x;
-            } else if constexpr (decltype(tr)::value) {
+            } else if constexpr (sizeof(T) == 2) {
                 *reinterpret_cast<uint4*>(S + (e / JR) * PTR + 16 * (e % JR)) = x;
             } else {
-                const int k = e / JR, j = e % JR;
-                const T* v = reinterpret_cast<const T*>(&x);
-#pragma unroll
-                for (int t = 0; t < EV; ++t) *reinterpret_cast<T*>(S + (EV * j + t) * PITCH + k * (int)sizeof(T)) = v[t];
+                const int k = e / JR, j = e % JR;   // k row, 16-byte column block
+                *reinterpret_cast<uint4*>(S + k * 64 + 16 * (j ^ f8(k))) = x;
             }
         }
     };
@@ -203,8 +203,20 @@ __global__ void __launch_bounds__(256) gemm_small_kernel(const T* __restrict__ A
     // row rb + r, k 8 g .. 8 g + 7 of the step
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    typedef int tr8_v2i __attribute__((ext_vector_type(2)));
     auto frag = [&](const uint8_t* S, auto tr, int rb, int ks) -> uint4 {
-        if constexpr (decltype(tr)::value) {
+        if constexpr (decltype(tr)::value && sizeof(T) == 1) {
+            // source lane s of group g points at k row 16 g + s / 2 (+ 8) of the step, byte 8 (s % 2)
+            // of column block rb / 16: output lane i gets 8 k-values of column rb + i per read
+            const int g = lane >> 4, s2 = lane & 15;
+            const int k = ks * KE + 16 * g + (s2 >> 1);   // bit 3 clear: k + 8 has the same F
+            const uint8_t* p0 = S + k * 64 + 16 * ((rb >> 4) ^ f8(k)) + 8 * (s2 & 1);
+            const tr8_v2i lo = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (__attribute__((address_space(3))) tr8_v2i*)(const __attribute__((address_space(3))) uint8_t*)(p0));
+            const tr8_v2i hi = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                (__attribute__((address_space(3))) tr8_v2i*)(const __attribute__((address_space(3))) uint8_t*)(p0 + 8 * 64));
+            return make_uint4((uint32_t)lo.x, (uint32_t)lo.y, (uint32_t)hi.x, (uint32_t)hi.y);
+        } else if constexpr (decltype(tr)::value) {
             // source lane (jj, q) = ((lane % 16) / 4, lane % 4) of group g points at k row
             // 8 g + jj (+ 4), rows rb + 4 q .. + 3: output lane r gets 4 k-values of row rb + r
             const int g = lane >> 4, jj = (lane & 15) >> 2, q = lane & 3;
@@ -392,7 +404,7 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
 }
 
 template <typename T>
-bool small_gemm_preferred(int64_t M, int64_t N, int64_t, bool mn_operand) {
+bool small_gemm_preferred(int64_t M, int64_t N, int64_t) {
     const int64_t tiles256 = ((M + 255) / 256) * ((N + 255) / 256);
     if (tiles256 <= SMALL_GEMM_MAX_TILES) return true;
     // Rate estimates (measured on shape lists): the tile kernel ~1500 TFLOP/s (bf16; int8 ~3000
@@ -402,12 +414,11 @@ bool small_gemm_preferred(int64_t M, int64_t N, int64_t, bool mn_operand) {
     // x 8192: 275 -> 342; 2048 x 4096 x 4096 stays on the tile kernel (898 against 494); int8
     // (tile kernel against small kernel, TOP/s): 64 x 14336 x 4096 166 / 383, 128 x 28672 x 8192
     // 727 / 755, 2048^3 653 / 681, 1536^2 x 8192 515 / 637 take the small kernel, 2048 x 4096 x
-    // 4096 (1558 / 916) the tile kernel.  An int8 operand that is M/N-contiguous (Julia's
-    // column-major default) is transposed by byte stores on the small kernel, about half its rate
-    // (2048^3 with A column-major: 343 TOP/s against 689), while the tile kernel reads it through
-    // transposing LDS reads at its full rate: ~400.
+    // 4096 (1558 / 916) the tile kernel.  An M/N-contiguous operand (Julia's column-major default) is
+    // read through transposing LDS reads on every kernel, at about the K-contiguous rate (int8 64 x
+    // 14336 x 4096 with A column-major 391 TOP/s against 390; 2048^3 621 against 694).
     const double tile_rate = sizeof(T) == 1 ? 3000.0 : 1500.0;
-    const double small_rate = sizeof(T) == 1 ? (mn_operand ? 400.0 : 800.0) : 450.0;
+    const double small_rate = sizeof(T) == 1 ? 800.0 : 450.0;
     const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
     const double occ256 = tiles256 >= 256 ? 1.0 : (double)tiles256 / 256.0;
     const double useful = (double)M * (double)N / ((double)tiles256 * 65536.0);
@@ -425,7 +436,7 @@ bool small_gemm_fits(const void* A, const void* B, int64_t M, int64_t N, int64_t
            ((arow || !brow) ? K % EV == 0 : true) && (arow || M % EV == 0) && (!brow || N % EV == 0);
 }
 #define LAVA_SMALL_RULE_INST(T)                                                                                      \
-    template bool small_gemm_preferred<T>(int64_t, int64_t, int64_t, bool);                                           \
+    template bool small_gemm_preferred<T>(int64_t, int64_t, int64_t);                                           \
     template bool small_gemm_fits<T>(const void*, const void*, int64_t, int64_t, int64_t, int64_t, int64_t, bool, bool);
 LAVA_SMALL_RULE_INST(f16)
 LAVA_SMALL_RULE_INST(bf16)

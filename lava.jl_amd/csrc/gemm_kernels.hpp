@@ -19,7 +19,7 @@ int launch_gemm_staged(const T* A, const T* B, OutT* C, int64_t M, int64_t N, in
 // arow / brow: A / B row-major).
 constexpr int64_t SMALL_GEMM_MAX_TILES = 16;
 template <typename T>
-bool small_gemm_preferred(int64_t M, int64_t N, int64_t K, bool mn_operand);   // mn_operand: A or B M/N-contiguous
+bool small_gemm_preferred(int64_t M, int64_t N, int64_t K);
 template <typename T>
 bool small_gemm_fits(const void* A, const void* B, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb, bool arow,
                      bool brow);
@@ -83,8 +83,8 @@ template <typename T, typename OutT, bool EPI, bool U8 = false>
 int launch_gemm_mid(const T* A, const T* B, OutT* C, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t ldb,
                     int64_t ldc, hipStream_t s, const Epilogue& epi, bool ragged, bool ak, bool bk);
 // Whether an M x N product takes the mid-size kernel when it fits (the measured choice against the
-// tile and small-product kernels); i8_mn: int8 with an M/N-contiguous operand.
-bool mid_gemm_preferred(int64_t M, int64_t N, bool i8_mn);
+// tile and small-product kernels).
+bool mid_gemm_preferred(int64_t M, int64_t N);
 // Any shape and layout: one thread per element of C, bytes widened and summed in uint32.
 int launch_gemm_u8_generic(const uint8_t* A, const uint8_t* B, uint32_t* C, int64_t M, int64_t N, int64_t K,
                            int64_t lda, int64_t ldb, int64_t ldc, uint32_t layout, hipStream_t s);

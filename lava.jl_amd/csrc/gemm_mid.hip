@@ -33,19 +33,18 @@ int mid_gemm_eligible(const void* A, const void* B, const void* C, int64_t M, in
 // least 128 tiles of 128 x 128, and fewer than 144 of 256 x 256.  With M/N-contiguous bf16 operands
 // the same boundaries hold (A and B column-major: 2048^3 620 / 401, 2048 x 4096 x 4096 1104 / 812,
 // 1536^2 x 8192 496 / 322, 3072^3 768 / 866, 1024^2 x 8192 221 / 374; A and B row-major or A
-// column-major and B row-major within 6 % of these).  int8 with an M/N-contiguous operand, which the
-// small-product kernel transposes by byte stores at about half its rate, keeps this kernel down to
-// 64 tiles (TOP/s, A and B column-major: 2048^3 1167 / 627, 1024^2 x 8192 403 / 306, 1024^3 226 /
-// 177; both M/N-contiguous 418 / 215 and 224 / 140).  Past one full round of 256 x 256 tiles, a
+// column-major and B row-major within 6 % of these; int8 with A and B column-major 2048^3 1167 / 627,
+// where the small kernel reads both operands through transposing LDS reads at 621 -- and at 1024^3, 64
+// tiles, it leads, 242 against 225).  Past one full round of 256 x 256 tiles, a
 // second round of at most 80 of them leaves this kernel ahead (bf16 TFLOP/s and int8 TOP/s, this
 // kernel / the tile kernel: 3072 x 6144 x 4096, 288 tiles, 1037 / 933 and 1789 / 1620; 4096 x 5120 x
 // 2048, 320 tiles, 986 / 906 and 1610 / 1453; 4608^2 x 4096, 324 tiles, 1073 / 1037 and 1855 / 1793;
 // 4608^2 x 1024 780 / 730 and 1201 / 1045), a fuller one does not (6144 x 4096 x 4096, 384 tiles, 1187 /
 // 1199 and 2002 / 2084; 5120^2 x 4096, 400, 1055 / 1237; 6144^2 x 4096, 576, 1151 / 1199).
-bool mid_gemm_preferred(int64_t M, int64_t N, bool i8_mn) {
+bool mid_gemm_preferred(int64_t M, int64_t N) {
     const int64_t t128 = ((M + TM_TILE - 1) / TM_TILE) * ((N + TM_TILE - 1) / TM_TILE);
     const int64_t t256 = ((M + TN_TILE - 1) / TN_TILE) * ((N + TN_TILE - 1) / TN_TILE);
-    return t128 >= (i8_mn ? 64 : 128) && (t256 < 144 || (t256 > 256 && t256 <= 336));
+    return t128 >= 128 && (t256 < 144 || (t256 > 256 && t256 <= 336));
 }
 
 LAVA_MID_LAUNCH_INST(f16, float, false, false)

@@ -83,7 +83,7 @@ def test_gemm_small_products(gpu, oracle, layout, dt, shape):
     """Products of at most 16 tiles of 256 x 256 run on 64 x 64 tiles, K in 512-byte chunks
     with the next chunk in flight (one chunk, several, a ragged last one, and extents that are
     not tile multiples); K-contiguous operands staged as loaded, M/N-contiguous ones through
-    transposing LDS reads (16-bit) or byte stores (int8).  int8 bit-exact."""
+    transposing LDS reads (ds_read_b64_tr_b16 / _tr_b8).  int8 bit-exact."""
     lh = gpu
     M, N, K = shape
     announce(f"gemm small {dt} layout={layout} M={M} N={N} K={K}")

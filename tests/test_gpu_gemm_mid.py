@@ -211,7 +211,7 @@ def test_mid_kernel_repeatable_and_linear(gpu, oracle, mid_kernel):
                           ("bf16", (1536, 1536, 8192), "gemm_mid_kernel", "F", "C"),
                           ("bf16", (3072, 3072, 3072), "gemm_tn_kernel", "F", "F"),
                           ("i8", (2048, 2048, 2048), "gemm_mid_kernel", "F", "F"),
-                          ("i8", (1024, 1024, 8192), "gemm_mid_kernel", "F", "F"),
+                          ("i8", (1024, 1024, 8192), "splitk_sum_kernel", "F", "F"),
                           ("i8", (1024, 1024, 8192), "splitk_sum_kernel", "C", "F"),
                           ("i8", (3072, 3072, 3072), "gemm_tn_kernel", "C", "C"),
                           ("bf16", (3072, 6144, 1024), "gemm_mid_kernel", "C", "F"),
@@ -219,9 +219,9 @@ def test_mid_kernel_repeatable_and_linear(gpu, oracle, mid_kernel):
                           ("bf16", (6144, 4096, 1024), "gemm_tn_kernel", "C", "F")])
 def test_mid_kernel_automatic_choice(gpu, oracle, dt, shape, kernel, aorder, border):
     """The automatic choice, in several operand layouts: the mid-size kernel from 128 tiles of 128 x
-    128 (64 for int8 with an M/N-contiguous operand) while there are fewer than 144 of 256 x 256 and
-    again from 257 to 336 of them, the tile kernel otherwise, the small-product kernel's K split
-    below; each result against the oracle on sampled rows."""
+    128 while there are fewer than 144 of 256 x 256 and again from 257 to 336 of them, the tile
+    kernel otherwise, the small-product kernel's K split below; each result against the oracle on
+    sampled rows."""
     lh = gpu
     M, N, K = shape
     announce(f"gemm automatic choice {dt} M={M} N={N} K={K} A {aorder} B {border}: {kernel}")

@@ -1,4 +1,6 @@
-"""CPU models of the mid-size GEMM kernel's LDS addressing (gemm_mid_kernel.hpp, gemm_tn_kernel.hpp).
+"""CPU models of LDS addressing in the GEMM kernels: the mid-size kernel's M/N-contiguous staging
+(gemm_mid_kernel.hpp, gemm_tn_kernel.hpp) and the small-product kernel's int8 [k][row] staging
+(gemm_generic.hip).
 
 Each model restates the kernel's integer address arithmetic -- the LDS-DMA placement of a k-tile's
 rows, the swizzle, and the addresses of the transposing fragment reads -- and checks what the
@@ -169,3 +171,54 @@ def u8_schedule(ktiles):
 def test_u8_flip_schedule(ktiles):
     flips = u8_schedule(ktiles)
     assert flips == {(kt, ks, t): 1 for kt in range(ktiles) for ks in range(2) for t in range(8)}
+
+
+def f8s(k):
+    """gemm_small_kernel's int8 [k][row] swizzle: (k / 4 % 2) | 2 ((k / 16 + k / 32) % 2)."""
+    return ((k >> 2) & 1) | ((((k >> 4) ^ (k >> 5)) & 1) << 1)
+
+
+def small_i8_reads(f):
+    """The small-product kernel's int8 [k][row] staging (512 k rows x 64 bytes, chunk j of k row k at
+    slot j ^ f(k)) and its two ds_read_b64_tr_b8 per fragment; returns (lds map, per-read addresses)."""
+    lds = {}
+    for e in range(2048):                       # 16-byte chunk e of the K chunk: k row e / 4, column block e % 4
+        k, j = e // 4, e % 4
+        dst = k * 64 + 16 * (j ^ f(k))
+        for b in range(16):
+            assert dst + b not in lds
+            lds[dst + b] = (k, 16 * j + b)
+    reads = {}
+    for ks in range(8):
+        for rb in (0, 16, 32, 48):
+            lo, hi = {}, {}
+            for lane in range(64):
+                g, s2 = lane >> 4, lane & 15
+                k = ks * 64 + 16 * g + (s2 >> 1)
+                p0 = k * 64 + 16 * ((rb >> 4) ^ f(k)) + 8 * (s2 & 1)
+                lo[lane], hi[lane] = p0, p0 + 8 * 64
+            reads[(ks, rb)] = (lo, hi)
+    return lds, reads
+
+
+def test_small_i8_placement_reads_and_banks():
+    lds, reads = small_i8_reads(f8s)
+    assert len(lds) == 512 * 64
+    for (ks, rb), (lo, hi) in reads.items():
+        for lane in range(64):
+            i, g = lane & 15, lane >> 4
+            for half, addrs in enumerate((lo, hi)):
+                for j in range(8):      # tr8: output lane i byte j from source lane 2 j + i / 8, byte i % 8
+                    k, col = lds[addrs[16 * g + 2 * j + i // 8] + i % 8]
+                    assert (k, col) == (ks * 64 + 16 * g + 8 * half + j, rb + i)
+        for addrs in (lo, hi):
+            for passes in PASSES:
+                for lanes in passes:
+                    assert banks_once(addrs, lanes), (ks, rb)
+
+
+def test_small_i8_swizzle_without_group_bit_conflicts():
+    """Without its (k / 16 + k / 32) term the two 16-lane groups of a pass collide."""
+    _, reads = small_i8_reads(lambda k: (k >> 2) & 1)
+    lo, _ = reads[(0, 0)]
+    assert not banks_once(lo, range(0, 32))
